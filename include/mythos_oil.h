@@ -1,0 +1,152 @@
+/*
+ * mythos_oil.h — C ABI of libmythos_oil.so: MI355X (gfx950) kernels for
+ * MYTHOS.cpp's quantized-weight matvec/matmul path.
+ *
+ * Every entry point takes DEVICE pointers (memory the caller allocated with
+ * hipMalloc or any HIP allocator), plain sizes and a HIP stream (hipStream_t
+ * passed as void*; NULL = the default stream).  Calls are stream-ordered and
+ * asynchronous: they validate, launch and return.  Outputs are overwritten,
+ * never accumulated, and no entry point allocates memory.
+ *
+ * Return value: MTH_OK (0) or a negative MTH_E* code; the thread-local message
+ * of the last failure is returned by mth_last_error().  Validation covers
+ * NULL pointers, non-positive or inconsistent sizes, and the layout
+ * constraints stated per function.  Unaligned or odd-sized inputs are not
+ * errors: they run on the generic kernels.
+ *
+ * Each function names the reference interface it replaces
+ * (path:line in the MYTHOS.cpp tree).  Host-pointer, synchronous drop-ins with
+ * the reference's exact C++ signatures (namespace oil::kernel) are declared in
+ * mythos.cpp_amd/host/include/oil/kernel.h and call these.
+ */
+#ifndef MYTHOS_OIL_H
+#define MYTHOS_OIL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mth_stream_t; /* hipStream_t */
+
+enum {
+    MTH_OK = 0,
+    MTH_EINVAL = -1,       /* bad pointer / size / layout argument          */
+    MTH_EDEVICE = -2,      /* HIP runtime or launch failure                 */
+    MTH_EUNSUPPORTED = -3, /* valid request this build does not implement    */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* mth_last_error(void);
+/* ABI version: (major << 16) | minor. */
+int mth_version(void);
+
+/* ---------------------------------------------------------------- OIL8 -- */
+
+/* Reference semantics of oil::kernel::oil8_gemm (include/oil/kernel.h:33-35,
+ * src/kernel_oil8.cpp:63-71): for every (m, n)
+ *   out[m*N + n] = sum_k codebook[indices[(m*N + n)*K + k]] * act[n*K + k]
+ * i.e. one weight row per (m, n) pair.  codebook: 256 floats. */
+int mth_oil8_gemm(const uint8_t* indices, const float* codebook, const float* act, float* out,
+                  int64_t M, int64_t N, int64_t K, mth_stream_t stream);
+
+/* Decode GEMV over one OIL8 weight matrix shared by `batch` tokens (the
+ * reference's oil8_gemm with N = 1, once per token, src/kernel_oil8.cpp:30-60):
+ *   y[t*M + m] = sum_k codebook[indices[m*K + k]] * x[t*K + k],  t < batch.
+ * Fast path: K % 16 == 0, K <= 4096, indices and x 16-byte aligned. */
+int mth_oil8_gemv(const uint8_t* indices, const float* codebook, const float* x, float* y,
+                  int64_t M, int64_t K, int64_t batch, mth_stream_t stream);
+
+/* ---------------------------------------------------------------- OIL4 -- */
+
+/* Reference semantics of oil::kernel::oil4_gemm (include/oil/kernel.h:39-41,
+ * scalar path src/kernel_oil4.cpp:31-54): one 16-entry FP16 codebook,
+ *   out[m*N + n] = sum_k f32(codebook[nib(r, k)]) * act[n*K + k],  r = m*N + n,
+ * where the weight row r starts at byte (r*K)/2 and element k is the low
+ * nibble of byte k/2 for even k, the high nibble for odd k.  The reference's
+ * AVX2 build adds codebook[0]*sum(act[k<16*floor(K/16)]) on top (a load-width
+ * bug); this entry point computes the scalar definition. */
+int mth_oil4_gemm(const uint8_t* packed, const uint16_t* codebook, const float* act, float* out,
+                  int64_t M, int64_t N, int64_t K, mth_stream_t stream);
+
+/* Decode GEMV with per-block FP16 codebooks (the layout the BASELINE configs
+ * use; the reference kernel takes one codebook per call):
+ *   y[t*M + m] = sum_k f32(codebooks[(m*(K/cb_block) + k/cb_block)*16 + nib(m,k)]) * x[t*K + k]
+ * packed: M rows of K/2 bytes, nibble order as above.  cb_block = 0 selects
+ * a single shared 16-entry codebook.  Requires K even and, for cb_block > 0,
+ * K % cb_block == 0.  Fast path: K % 32 == 0, K <= 4096, cb_block % 32 == 0,
+ * 16-byte aligned packed / codebooks / x. */
+int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_block,
+                  const float* x, float* y, int64_t M, int64_t K, int64_t batch,
+                  mth_stream_t stream);
+
+/* Prefill GEMM (no reference counterpart beyond oil4_gemm's per-token
+ * definition): C[m*N + n] = bf16( sum_k A[m*K + k] * W[n][k] ), A bf16
+ * [M][K] row-major, W OIL4 [N][K] with per-block codebooks as in
+ * mth_oil4_gemv, FP32 accumulation, C bf16 [M][N] (round to nearest even).
+ * Weights are dequantised to FP16 (exact) and activations converted
+ * bf16 -> FP16 (exact for |a| in [2^-14, 65504]; smaller magnitudes lose
+ * bits as FP16 subnormals, larger ones overflow). */
+int mth_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* packed, const uint16_t* codebooks,
+                          int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
+                          mth_stream_t stream);
+
+/* ---------------------------------------------------------- int8 / I2_S -- */
+
+/* quantize_per_token (include/oil/int8_quant.h:17-20, src/int8_quant.cpp:8-31):
+ * per row r: max_abs = max(max|src|, 1e-10), scale = 127/max_abs,
+ * dst = (int8)round_half_away(src*scale), inv_scale = max_abs/127.
+ * scale / inv_scale may be NULL. */
+int mth_quantize_per_token(const float* src, int8_t* dst, float* scale, float* inv_scale,
+                           int64_t rows, int64_t cols, mth_stream_t stream);
+
+/* dequantize_per_tensor (include/oil/int8_quant.h:22-24, src/int8_quant.cpp:33-37):
+ * dst[i] = (float)src[i] * inv_scale. */
+int mth_dequantize_per_tensor(const int8_t* src, float* dst, int64_t n, float inv_scale,
+                              mth_stream_t stream);
+
+/* oil::kernel::i2s_gemv (include/oil/kernel.h:15-17, src/kernel_i2s.cpp:32-40)
+ * applied to M rows and `batch` int8 tokens:
+ *   y[t*M + m] = ((float)sum_k tern(packed[m*K/4 ..], k) * act[t*K + k] * w_scale) * act_scale[t]
+ * with the LUT initialised (code 00 -> -1, 01 -> 0, 10/11 -> +1).
+ * act_scale: device array of `batch` floats (the reference's act_scale).
+ * Requires K % 4 == 0.  Bit-exact with the reference. */
+int mth_i2s_gemv(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
+                 float* y, int64_t M, int64_t K, int64_t batch, mth_stream_t stream);
+
+/* Fused decode op: quantize_per_token(x_t) then mth_i2s_gemv with
+ * act_scale = inv_scale, in one launch.  Requires K % 4 == 0.  Bit-exact. */
+int mth_i2s_gemv_f32(const uint8_t* packed, float w_scale, const float* x, float* y,
+                     int64_t M, int64_t K, int64_t batch, mth_stream_t stream);
+
+/* oil::kernel::i2s_gemm (include/oil/kernel.h:13-14, src/kernel_i2s.cpp:42-65):
+ * out[m*N + n] = sum_k tern(w + m*(K/4), k) * act[n*K + k]  (FP32, no scales). */
+int mth_i2s_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int64_t N, int64_t K,
+                 mth_stream_t stream);
+
+/* oil::kernel::i2s_gemm_vnni (include/oil/kernel.h:63-65, body at
+ * src/kernel_i2s.cpp:201-235): int8 activations, exact integer dot as FP32. */
+int mth_i2s_gemm_vnni(const uint8_t* w, const int8_t* act, float* out, int64_t M, int64_t N, int64_t K,
+                      mth_stream_t stream);
+
+/* oil::kernel::tl1_gemm (include/oil/kernel.h:20-21, src/kernel_tl.cpp:33-74),
+ * including its pair-LUT indexing by the first weight's code. */
+int mth_tl1_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int64_t N, int64_t K,
+                 mth_stream_t stream);
+
+/* oil::kernel::tl2_gemm (include/oil/kernel.h:26-27, src/kernel_tl.cpp:109-168).
+ * Requires K % 3 == 0 (the reference reads past the activation row otherwise). */
+int mth_tl2_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int64_t N, int64_t K,
+                 mth_stream_t stream);
+
+/* tl1_precompute_lut / tl2_precompute_lut (include/oil/kernel.h:22-23,28-29;
+ * src/kernel_tl.cpp:13-31, 88-107): group = 2 writes K/2 tables of 9 entries,
+ * group = 3 writes K/3 tables of 27 entries (requires K % 3 == 0); entry
+ * (w0, w1[, w2]) in {-1,0,1}^group, row-major, = clamp_int8(sum a_i*w_i). */
+int mth_tl_precompute_lut(const int8_t* act, int8_t* lut, int64_t K, int group, mth_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MYTHOS_OIL_H */

@@ -1,0 +1,69 @@
+// common.h — device helpers shared by the gfx950 kernels of libmythos_oil.
+//
+// Wave64 only (CDNA4).  Nothing here allocates; every helper is header-only
+// and inlined into the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MTH_WAVE 64
+
+namespace mth {
+
+// ---- cross-lane sums over groups of G consecutive lanes (G | 64) --------
+// Butterfly over xor-partners; every lane of a group ends with the group sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
+    return v;
+}
+template <int G>
+__device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MTH_WAVE));
+    return v;
+}
+
+// ---- fp16 bits -> f32 (hardware v_cvt_f32_f16: exact for normals and
+// subnormals, the same values as src/kernel_oil4.cpp:15-29; NaNs stay NaN) ----
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+__device__ __forceinline__ float h2f_lo(uint32_t w) { return h2f(w & 0xffffu); }
+__device__ __forceinline__ float h2f_hi(uint32_t w) { return h2f(w >> 16); }
+
+// ---- 128-bit loads ------------------------------------------------------
+// Streaming weight loads: each weight byte is read once per launch.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ld16(const void* p) { return *(const uint4*)p; }
+__device__ __forceinline__ float4 ldf4(const float* p) { return *(const float4*)p; }
+
+__device__ __forceinline__ uint32_t u4get(const uint4& v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// ---- int8 helpers ---------------------------------------------------------
+// sum_{i<4} (int8)a.byte[i] * (int8)b.byte[i] + c   (v_dot4_i32_i8)
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Reference int8 quantisation of one value (src/int8_quant.cpp:19):
+// (int8_t)std::round(v * scale) — round half away from zero, then truncate.
+__device__ __forceinline__ int quant_i8(float v, float scale) {
+    return (int)(int8_t)(int)__builtin_roundf(__fmul_rn(v, scale));
+}
+
+}  // namespace mth

@@ -1,0 +1,58 @@
+// launch.h — internal launcher interface between the C ABI (capi.hip) and the
+// kernel translation units.  Launchers assume validated arguments: the C ABI
+// checks sizes, pointers and alignment before calling them, and each launcher
+// only picks a kernel variant and a grid.  They return the hipError_t of the
+// launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mth {
+
+// ---- OIL8 (gemv.hip) ----------------------------------------------------
+// y[t*M + m] = sum_k cb[idx[m*K + k]] * x[t*K + k]          (t < batch)
+hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x, float* y,
+                            int64_t M, int64_t K, int64_t batch, hipStream_t s);
+// Reference per-(m,n) indexing (src/kernel_oil8.cpp:20-24):
+// out[r] = sum_k cb[idx[r*K + k]] * act[(r % N)*K + k],  r < M*N
+hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float* act, float* out,
+                               int64_t M, int64_t N, int64_t K, hipStream_t s);
+
+// ---- OIL4 (gemv.hip) ----------------------------------------------------
+// cb_block > 0: codebooks[(m*(K/cb_block) + k/cb_block)*16 + i] (fp16 bits);
+// cb_block == 0: one shared 16-entry codebook.
+hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block,
+                            const float* x, float* y, int64_t M, int64_t K, int64_t batch,
+                            hipStream_t s);
+// Reference per-(m,n) indexing with one codebook (src/kernel_oil4.cpp:41-52).
+hipError_t launch_oil4_gemm_mn(const uint8_t* nib, const uint16_t* cb, const float* act, float* out,
+                               int64_t M, int64_t N, int64_t K, hipStream_t s);
+
+// ---- int8 / ternary (ternary.hip) ----------------------------------------
+hipError_t launch_quantize_per_token(const float* src, int8_t* dst, float* scale, float* inv_scale,
+                                     int64_t rows, int64_t cols, hipStream_t s);
+hipError_t launch_dequantize(const int8_t* src, float* dst, int64_t n, float inv_scale, hipStream_t s);
+hipError_t launch_tl_precompute_lut(const int8_t* act, int8_t* lut, int64_t K, int group, hipStream_t s);
+// y[t*M + m] = ((float)dot(t(w_m), q_t) * w_scale) * inv_t
+//   fused:   q_t, inv_t from quantize_per_token(x_t) inside the kernel
+//   unfused: q_t = act[t*K..], inv_t = act_scale[t]
+hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x,
+                           const int8_t* act, const float* act_scale, float* y,
+                           int64_t M, int64_t K, int64_t batch, hipStream_t s);
+hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
+                           int64_t M, int64_t N, int64_t K, hipStream_t s);
+hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o,
+                                int64_t M, int64_t N, int64_t K, hipStream_t s);
+hipError_t launch_tl1_gemm(const uint8_t* w, const float* a, float* o,
+                           int64_t M, int64_t N, int64_t K, hipStream_t s);
+hipError_t launch_tl2_gemm(const uint8_t* w, const float* a, float* o,
+                           int64_t M, int64_t N, int64_t K, hipStream_t s);
+
+// ---- OIL4 prefill GEMM (gemm_oil4.hip) -----------------------------------
+hipError_t launch_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
+                                    int64_t cb_block, uint16_t* c_bf16,
+                                    int64_t M, int64_t N, int64_t K, hipStream_t s);
+bool oil4_gemm_prefill_supported(int64_t M, int64_t N, int64_t K, int64_t cb_block);
+
+}  // namespace mth

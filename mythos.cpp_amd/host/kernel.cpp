@@ -1,0 +1,302 @@
+// kernel.cpp — host-pointer, synchronous drop-ins for MYTHOS.cpp's
+// oil::kernel::* and oil::quantize_* (include/oil/kernel.h:13-65,
+// include/oil/int8_quant.h:7-28), running on the gfx950 kernels through the
+// C ABI of libmythos_oil.so.
+//
+// Each call stages its operands in a per-thread device arena (grown on
+// demand, never shrunk), copies inputs host->device, launches on the
+// thread's stream, copies outputs back and synchronises.  There is no CPU
+// code path: a missing or failing GPU raises oil::Error.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mythos_oil.h"
+#include "oil/int8_quant.h"
+#include "oil/kernel.h"
+
+namespace oil {
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
+}
+void mth_check(int rc, const char* what) {
+    if (rc != MTH_OK) throw Error(std::string(what) + ": " + mth_last_error());
+}
+
+// Per-thread device staging area.  carve() hands out 256-byte aligned slices
+// of one allocation; reset() starts a new call.
+class Arena {
+public:
+    ~Arena() {
+        if (base_) (void)hipFree(base_);
+        if (stream_) (void)hipStreamDestroy(stream_);
+    }
+    void begin(size_t bytes_needed) {
+        if (!stream_) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+        if (bytes_needed > cap_) {
+            if (base_) hip_check(hipFree(base_), "hipFree");
+            base_ = nullptr;
+            cap_ = 0;
+            hip_check(hipMalloc(&base_, bytes_needed), "hipMalloc");
+            cap_ = bytes_needed;
+        }
+        off_ = 0;
+    }
+    static size_t pad(size_t b) { return (b + 255) / 256 * 256; }
+    void* carve(size_t bytes) {
+        void* p = (char*)base_ + off_;
+        off_ += pad(bytes);
+        return p;
+    }
+    template <typename T> T* upload(const T* host, size_t n) {
+        T* d = (T*)carve(n * sizeof(T));
+        if (n) hip_check(hipMemcpyAsync(d, host, n * sizeof(T), hipMemcpyHostToDevice, stream_), "hipMemcpy H2D");
+        return d;
+    }
+    template <typename T> void download(T* host, const T* dev, size_t n) {
+        if (n) hip_check(hipMemcpyAsync(host, dev, n * sizeof(T), hipMemcpyDeviceToHost, stream_), "hipMemcpy D2H");
+    }
+    void sync() { hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize"); }
+    mth_stream_t stream() const { return (mth_stream_t)stream_; }
+
+private:
+    void* base_ = nullptr;
+    size_t cap_ = 0, off_ = 0;
+    hipStream_t stream_ = nullptr;
+};
+
+Arena& arena() {
+    thread_local Arena a;
+    return a;
+}
+
+inline size_t P(size_t b) { return Arena::pad(b); }
+
+void check_dims(int M, int N, int K, const char* what) {
+    if (M <= 0 || N <= 0 || K <= 0)
+        throw Error(std::string(what) + ": M, N, K must be positive");
+}
+
+}  // namespace
+
+namespace kernel {
+
+void oil8_gemm(const uint8_t* indices, const float* codebook, const float* activations, float* output,
+               int M, int N, int K) {
+    check_dims(M, N, K, "oil8_gemm");
+    const size_t R = (size_t)M * N, nw = R * K, na = (size_t)N * K;
+    Arena& a = arena();
+    a.begin(P(nw) + P(256 * 4) + P(na * 4) + P(R * 4));
+    const uint8_t* di = a.upload(indices, nw);
+    const float* dc = a.upload(codebook, 256);
+    const float* dx = a.upload(activations, na);
+    float* dy = (float*)a.carve(R * 4);
+    mth_check(mth_oil8_gemm(di, dc, dx, dy, M, N, K, a.stream()), "oil8_gemm");
+    a.download(output, dy, R);
+    a.sync();
+}
+
+void oil4_gemm(const uint8_t* packed_indices, const uint16_t* codebook, const float* activations,
+               float* output, int M, int N, int K) {
+    check_dims(M, N, K, "oil4_gemm");
+    const size_t R = (size_t)M * N, nb = (R * (size_t)K + 1) / 2, na = (size_t)N * K;
+    Arena& a = arena();
+    a.begin(P(nb) + P(32) + P(na * 4) + P(R * 4));
+    const uint8_t* dp = a.upload(packed_indices, nb);
+    const uint16_t* dc = a.upload(codebook, 16);
+    const float* dx = a.upload(activations, na);
+    float* dy = (float*)a.carve(R * 4);
+    mth_check(mth_oil4_gemm(dp, dc, dx, dy, M, N, K, a.stream()), "oil4_gemm");
+    a.download(output, dy, R);
+    a.sync();
+}
+
+void i2s_gemv(const uint8_t* packed_w, float w_scale, const int8_t* act, float act_scale, float* output, int K) {
+    if (K <= 0 || K % 4) throw Error("i2s_gemv: K must be a positive multiple of 4");
+    Arena& a = arena();
+    a.begin(P(K / 4) + P(K) + P(4) + P(4));
+    const uint8_t* dw = a.upload(packed_w, (size_t)K / 4);
+    const int8_t* dq = a.upload(act, (size_t)K);
+    const float* ds = a.upload(&act_scale, 1);
+    float* dy = (float*)a.carve(4);
+    mth_check(mth_i2s_gemv(dw, w_scale, dq, ds, dy, 1, K, 1, a.stream()), "i2s_gemv");
+    a.download(output, dy, 1);
+    a.sync();
+}
+
+void i2s_gemm(const Tensor& weights, const Tensor& activations, Tensor& output, int M, int N, int K) {
+    check_dims(M, N, K, "i2s_gemm");
+    const size_t nw = (size_t)M * (K / 4) + (K % 4 ? 1 : 0), na = (size_t)N * K, R = (size_t)M * N;
+    OIL_CHECK(weights.size_bytes() >= nw && activations.numel() >= (int64_t)na && output.numel() >= (int64_t)R,
+              "i2s_gemm: tensor too small");
+    Arena& a = arena();
+    a.begin(P(nw) + P(na * 4) + P(R * 4));
+    const uint8_t* dw = a.upload(weights.data<uint8_t>(), nw);
+    const float* dx = a.upload(activations.data<float>(), na);
+    float* dy = (float*)a.carve(R * 4);
+    mth_check(mth_i2s_gemm(dw, dx, dy, M, N, K, a.stream()), "i2s_gemm");
+    a.download(output.data<float>(), dy, R);
+    a.sync();
+}
+
+// Same contract as i2s_gemm (the reference's AVX2 variant differs only in
+// summation order, src/kernel_i2s.cpp:156-199).
+void i2s_gemm_avx2(const Tensor& weights, const Tensor& activations, Tensor& output, int M, int N, int K) {
+    i2s_gemm(weights, activations, output, M, N, K);
+}
+
+void i2s_gemm_vnni(const uint8_t* packed_w, const int8_t* activations, float* output, int M, int N, int K) {
+    check_dims(M, N, K, "i2s_gemm_vnni");
+    const size_t nw = (size_t)M * (K / 4) + (K % 4 ? 1 : 0), na = (size_t)N * K, R = (size_t)M * N;
+    Arena& a = arena();
+    a.begin(P(nw) + P(na) + P(R * 4));
+    const uint8_t* dw = a.upload(packed_w, nw);
+    const int8_t* dx = a.upload(activations, na);
+    float* dy = (float*)a.carve(R * 4);
+    mth_check(mth_i2s_gemm_vnni(dw, dx, dy, M, N, K, a.stream()), "i2s_gemm_vnni");
+    a.download(output, dy, R);
+    a.sync();
+}
+
+void tl1_gemm(const Tensor& weights, const Tensor& activations, Tensor& output, int M, int N, int K) {
+    check_dims(M, N, K, "tl1_gemm");
+    const size_t R = (size_t)M * N, nw = (R * (size_t)K) / 4 + 1, na = (size_t)N * K;
+    OIL_CHECK(weights.size_bytes() + 1 >= nw && activations.numel() >= (int64_t)na && output.numel() >= (int64_t)R,
+              "tl1_gemm: tensor too small");
+    Arena& a = arena();
+    a.begin(P(nw) + P(na * 4) + P(R * 4));
+    uint8_t* dw = (uint8_t*)a.carve(nw);
+    hip_check(hipMemsetAsync(dw, 0, nw, (hipStream_t)a.stream()), "hipMemset");
+    hip_check(hipMemcpyAsync(dw, weights.data(), std::min(nw, weights.size_bytes()), hipMemcpyHostToDevice,
+                             (hipStream_t)a.stream()),
+              "hipMemcpy H2D");
+    const float* dx = a.upload(activations.data<float>(), na);
+    float* dy = (float*)a.carve(R * 4);
+    mth_check(mth_tl1_gemm(dw, dx, dy, M, N, K, a.stream()), "tl1_gemm");
+    a.download(output.data<float>(), dy, R);
+    a.sync();
+}
+
+void tl2_gemm(const Tensor& weights, const Tensor& activations, Tensor& output, int M, int N, int K) {
+    check_dims(M, N, K, "tl2_gemm");
+    const size_t R = (size_t)M * N, bpr = ((size_t)K * 2 + 7) / 8, nw = R * bpr, na = (size_t)N * K;
+    OIL_CHECK(weights.size_bytes() >= nw && activations.numel() >= (int64_t)na && output.numel() >= (int64_t)R,
+              "tl2_gemm: tensor too small");
+    Arena& a = arena();
+    a.begin(P(nw) + P(na * 4) + P(R * 4));
+    const uint8_t* dw = a.upload(weights.data<uint8_t>(), nw);
+    const float* dx = a.upload(activations.data<float>(), na);
+    float* dy = (float*)a.carve(R * 4);
+    mth_check(mth_tl2_gemm(dw, dx, dy, M, N, K, a.stream()), "tl2_gemm");
+    a.download(output.data<float>(), dy, R);
+    a.sync();
+}
+
+void tl1_precompute_lut(const int8_t* activations, int8_t* lut, int K, float scales) {
+    (void)scales;  // unused by the reference as well (src/kernel_tl.cpp:15)
+    if (K < 2) return;
+    Arena& a = arena();
+    const size_t nl = (size_t)(K / 2) * 9;
+    a.begin(P(K) + P(nl));
+    const int8_t* dx = a.upload(activations, (size_t)K);
+    int8_t* dl = (int8_t*)a.carve(nl);
+    mth_check(mth_tl_precompute_lut(dx, dl, K, 2, a.stream()), "tl1_precompute_lut");
+    a.download(lut, dl, nl);
+    a.sync();
+}
+
+void tl2_precompute_lut(const int8_t* activations, int8_t* lut, int K, float scales) {
+    (void)scales;  // unused by the reference as well (src/kernel_tl.cpp:90)
+    if (K <= 0) return;
+    if (K % 3) throw Error("tl2_precompute_lut: K must be a multiple of 3");
+    Arena& a = arena();
+    const size_t nl = (size_t)(K / 3) * 27;
+    a.begin(P(K) + P(nl));
+    const int8_t* dx = a.upload(activations, (size_t)K);
+    int8_t* dl = (int8_t*)a.carve(nl);
+    mth_check(mth_tl_precompute_lut(dx, dl, K, 3, a.stream()), "tl2_precompute_lut");
+    a.download(lut, dl, nl);
+    a.sync();
+}
+
+void oil4_gemv_blocked(const uint8_t* packed, const uint16_t* codebooks, int cb_block, const float* x, float* y,
+                       int M, int K, int batch) {
+    check_dims(M, batch, K, "oil4_gemv_blocked");
+    const size_t nb = (size_t)M * K / 2, nc = cb_block ? (size_t)M * (K / cb_block) * 16 : 16;
+    Arena& a = arena();
+    a.begin(P(nb) + P(nc * 2) + P((size_t)batch * K * 4) + P((size_t)batch * M * 4));
+    const uint8_t* dp = a.upload(packed, nb);
+    const uint16_t* dc = a.upload(codebooks, nc);
+    const float* dx = a.upload(x, (size_t)batch * K);
+    float* dy = (float*)a.carve((size_t)batch * M * 4);
+    mth_check(mth_oil4_gemv(dp, dc, cb_block, dx, dy, M, K, batch, a.stream()), "oil4_gemv_blocked");
+    a.download(y, dy, (size_t)batch * M);
+    a.sync();
+}
+
+void i2s_gemv_f32(const uint8_t* packed, float w_scale, const float* x, float* y, int M, int K, int batch) {
+    check_dims(M, batch, K, "i2s_gemv_f32");
+    const size_t nw = (size_t)M * K / 4;
+    Arena& a = arena();
+    a.begin(P(nw) + P((size_t)batch * K * 4) + P((size_t)batch * M * 4));
+    const uint8_t* dw = a.upload(packed, nw);
+    const float* dx = a.upload(x, (size_t)batch * K);
+    float* dy = (float*)a.carve((size_t)batch * M * 4);
+    mth_check(mth_i2s_gemv_f32(dw, w_scale, dx, dy, M, K, batch, a.stream()), "i2s_gemv_f32");
+    a.download(y, dy, (size_t)batch * M);
+    a.sync();
+}
+
+}  // namespace kernel
+
+// ---- int8 quantisation (src/int8_quant.cpp:8-41) -------------------------
+
+std::vector<Int8QuantParams> quantize_per_token(const float* src, int8_t* dst, int64_t rows, int64_t cols) {
+    std::vector<Int8QuantParams> params((size_t)(rows > 0 ? rows : 0));
+    if (rows <= 0 || cols <= 0) return params;
+    const size_t n = (size_t)rows * (size_t)cols;
+    Arena& a = arena();
+    a.begin(P(n * 4) + P(n) + 2 * P((size_t)rows * 4));
+    const float* dx = a.upload(src, n);
+    int8_t* dq = (int8_t*)a.carve(n);
+    float* ds = (float*)a.carve((size_t)rows * 4);
+    float* di = (float*)a.carve((size_t)rows * 4);
+    mth_check(mth_quantize_per_token(dx, dq, ds, di, rows, cols, a.stream()), "quantize_per_token");
+    std::vector<float> s((size_t)rows), inv((size_t)rows);
+    a.download(dst, dq, n);
+    a.download(s.data(), ds, (size_t)rows);
+    a.download(inv.data(), di, (size_t)rows);
+    a.sync();
+    for (int64_t r = 0; r < rows; r++) params[(size_t)r] = Int8QuantParams{s[(size_t)r], inv[(size_t)r]};
+    return params;
+}
+
+Int8QuantParams quantize_per_tensor(const float* src, int8_t* dst, int64_t n) {
+    if (n <= 0) {
+        // the reference returns scale = 127/1e-10 for an empty tensor
+        const float mx = 1e-10f;
+        return Int8QuantParams{127.0f / mx, mx / 127.0f};
+    }
+    return quantize_per_token(src, dst, 1, n)[0];
+}
+
+void dequantize_per_tensor(const int8_t* src, float* dst, int64_t n, float inv_scale) {
+    if (n <= 0) return;
+    Arena& a = arena();
+    a.begin(P((size_t)n) + P((size_t)n * 4));
+    const int8_t* dq = a.upload(src, (size_t)n);
+    float* dy = (float*)a.carve((size_t)n * 4);
+    mth_check(mth_dequantize_per_tensor(dq, dy, n, inv_scale, a.stream()), "dequantize_per_tensor");
+    a.download(dst, dy, (size_t)n);
+    a.sync();
+}
+
+Int8QuantParams quantize_tensor(const Tensor& src, Tensor& dst) {
+    return quantize_per_tensor(src.data<float>(), dst.data<int8_t>(), src.numel());
+}
+
+}  // namespace oil

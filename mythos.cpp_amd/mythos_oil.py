@@ -1,0 +1,226 @@
+"""ctypes binding of libmythos_oil.so (include/mythos_oil.h) for Python callers.
+
+Device memory and the stream come from torch (plumbing only): every function
+takes torch CUDA tensors, checks dtype / size / contiguity on the host, and
+calls the C ABI with raw device pointers on torch's current stream.  There is
+no CPU fallback: importing this module raises if the library is missing, and
+every non-zero status from the library raises MythosError with the library's
+own message.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmythos_oil.so")
+HOST_LIB_PATH = os.path.join(_HERE, "libmythos_host.so")
+
+# Every extern "C" symbol declared in include/mythos_oil.h.
+EXPORTS = (
+    "mth_last_error", "mth_version",
+    "mth_oil8_gemm", "mth_oil8_gemv",
+    "mth_oil4_gemm", "mth_oil4_gemv", "mth_oil4_gemm_prefill",
+    "mth_quantize_per_token", "mth_dequantize_per_tensor",
+    "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
+    "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
+)
+
+MTH_OK, MTH_EINVAL, MTH_EDEVICE, MTH_EUNSUPPORTED = 0, -1, -2, -3
+
+
+class MythosError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def build() -> None:
+    """Compile libmythos_oil.so / libmythos_host.so in-tree (gfx950)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-j8"], check=True)
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built; run mythos_oil.build() (or __graft_entry__.build())")
+    return C.CDLL(path)
+
+
+# torch is loaded first so that libmythos_oil.so binds to the HIP runtime that
+# already owns torch's device memory and streams: loading the library first
+# would pull a second libamdhip64 into the process, whose context sees
+# neither torch's allocations nor (on the GPU boxes) the device.
+import torch as _torch_first  # noqa: E402,F401
+
+_lib = load_library()
+VP, I64, I32, F32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
+_SIG = {
+    "mth_oil8_gemm": [VP, VP, VP, VP, I64, I64, I64, VP],
+    "mth_oil8_gemv": [VP, VP, VP, VP, I64, I64, I64, VP],
+    "mth_oil4_gemm": [VP, VP, VP, VP, I64, I64, I64, VP],
+    "mth_oil4_gemv": [VP, VP, I64, VP, VP, I64, I64, I64, VP],
+    "mth_oil4_gemm_prefill": [VP, VP, VP, I64, VP, I64, I64, I64, VP],
+    "mth_quantize_per_token": [VP, VP, VP, VP, I64, I64, VP],
+    "mth_dequantize_per_tensor": [VP, VP, I64, F32, VP],
+    "mth_i2s_gemv": [VP, F32, VP, VP, VP, I64, I64, I64, VP],
+    "mth_i2s_gemv_f32": [VP, F32, VP, VP, I64, I64, I64, VP],
+    "mth_i2s_gemm": [VP, VP, VP, I64, I64, I64, VP],
+    "mth_i2s_gemm_vnni": [VP, VP, VP, I64, I64, I64, VP],
+    "mth_tl1_gemm": [VP, VP, VP, I64, I64, I64, VP],
+    "mth_tl2_gemm": [VP, VP, VP, I64, I64, I64, VP],
+    "mth_tl_precompute_lut": [VP, VP, I64, I32, VP],
+}
+for _n, _a in _SIG.items():
+    _f = getattr(_lib, _n)
+    _f.argtypes = _a
+    _f.restype = I32
+_lib.mth_last_error.argtypes = []
+_lib.mth_last_error.restype = C.c_char_p
+_lib.mth_version.argtypes = []
+_lib.mth_version.restype = I32
+
+lib = _lib
+
+
+def version() -> int:
+    return _lib.mth_version()
+
+
+def last_error() -> str:
+    return _lib.mth_last_error().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != MTH_OK:
+        raise MythosError(rc, last_error())
+
+
+def _torch():
+    import torch  # deferred: the library itself never needs torch
+    return torch
+
+
+def _stream(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _i2s_bytes(M: int, K: int) -> int:
+    # row m at m*(K/4), element k at byte k/4 of the row (src/kernel_i2s.cpp:54,207)
+    return (M - 1) * (K // 4) + (K - 1) // 4 + 1
+
+
+def _ptr(t, dtype, numel: int, name: str) -> int:
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: must be a device tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name}: {t.numel()} elements < {numel} required")
+    return t.data_ptr()
+
+
+# --------------------------------------------------------------------------
+# Thin wrappers: outputs are passed in (preallocated) and overwritten.
+# --------------------------------------------------------------------------
+def oil8_gemm(indices, codebook, act, out, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_oil8_gemm(_ptr(indices, t.uint8, M * N * K, "indices"), _ptr(codebook, t.float32, 256, "codebook"),
+                              _ptr(act, t.float32, N * K, "act"), _ptr(out, t.float32, M * N, "out"),
+                              M, N, K, _stream(stream)))
+
+
+def oil8_gemv(indices, codebook, x, y, M, K, batch=1, stream=None):
+    t = _torch()
+    _check(_lib.mth_oil8_gemv(_ptr(indices, t.uint8, M * K, "indices"), _ptr(codebook, t.float32, 256, "codebook"),
+                              _ptr(x, t.float32, batch * K, "x"), _ptr(y, t.float32, batch * M, "y"),
+                              M, K, batch, _stream(stream)))
+
+
+def oil4_gemm(packed, codebook, act, out, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_oil4_gemm(_ptr(packed, t.uint8, (M * N * K + 1) // 2, "packed"),
+                              _ptr(codebook, t.int16, 16, "codebook"),
+                              _ptr(act, t.float32, N * K, "act"), _ptr(out, t.float32, M * N, "out"),
+                              M, N, K, _stream(stream)))
+
+
+def oil4_gemv(packed, codebooks, cb_block, x, y, M, K, batch=1, stream=None):
+    t = _torch()
+    ncb = M * (K // cb_block) * 16 if cb_block else 16
+    _check(_lib.mth_oil4_gemv(_ptr(packed, t.uint8, M * K // 2, "packed"), _ptr(codebooks, t.int16, ncb, "codebooks"),
+                              cb_block, _ptr(x, t.float32, batch * K, "x"), _ptr(y, t.float32, batch * M, "y"),
+                              M, K, batch, _stream(stream)))
+
+
+def oil4_gemm_prefill(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_oil4_gemm_prefill(_ptr(a_bf16, t.bfloat16, M * K, "a"), _ptr(packed, t.uint8, N * K // 2, "packed"),
+                                      _ptr(codebooks, t.int16, N * (K // cb_block) * 16, "codebooks"), cb_block,
+                                      _ptr(c_bf16, t.bfloat16, M * N, "c"), M, N, K, _stream(stream)))
+
+
+def quantize_per_token(src, dst, scale, inv_scale, rows, cols, stream=None):
+    t = _torch()
+    _check(_lib.mth_quantize_per_token(_ptr(src, t.float32, rows * cols, "src"), _ptr(dst, t.int8, rows * cols, "dst"),
+                                       _ptr(scale, t.float32, rows, "scale") if scale is not None else None,
+                                       _ptr(inv_scale, t.float32, rows, "inv_scale") if inv_scale is not None else None,
+                                       rows, cols, _stream(stream)))
+
+
+def dequantize_per_tensor(src, dst, n, inv_scale, stream=None):
+    t = _torch()
+    _check(_lib.mth_dequantize_per_tensor(_ptr(src, t.int8, n, "src"), _ptr(dst, t.float32, n, "dst"), n,
+                                          float(inv_scale), _stream(stream)))
+
+
+def i2s_gemv(packed, w_scale, act, act_scale, y, M, K, batch=1, stream=None):
+    t = _torch()
+    _check(_lib.mth_i2s_gemv(_ptr(packed, t.uint8, M * K // 4, "packed"), float(w_scale),
+                             _ptr(act, t.int8, batch * K, "act"), _ptr(act_scale, t.float32, batch, "act_scale"),
+                             _ptr(y, t.float32, batch * M, "y"), M, K, batch, _stream(stream)))
+
+
+def i2s_gemv_f32(packed, w_scale, x, y, M, K, batch=1, stream=None):
+    t = _torch()
+    _check(_lib.mth_i2s_gemv_f32(_ptr(packed, t.uint8, M * K // 4, "packed"), float(w_scale),
+                                 _ptr(x, t.float32, batch * K, "x"), _ptr(y, t.float32, batch * M, "y"),
+                                 M, K, batch, _stream(stream)))
+
+
+def i2s_gemm(w, act, out, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_i2s_gemm(_ptr(w, t.uint8, _i2s_bytes(M, K), "w"), _ptr(act, t.float32, N * K, "act"),
+                             _ptr(out, t.float32, M * N, "out"), M, N, K, _stream(stream)))
+
+
+def i2s_gemm_vnni(w, act, out, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_i2s_gemm_vnni(_ptr(w, t.uint8, _i2s_bytes(M, K), "w"), _ptr(act, t.int8, N * K, "act"),
+                                  _ptr(out, t.float32, M * N, "out"), M, N, K, _stream(stream)))
+
+
+def tl1_gemm(w, act, out, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_tl1_gemm(_ptr(w, t.uint8, (M * N * K) // 4, "w"), _ptr(act, t.float32, N * K, "act"),
+                             _ptr(out, t.float32, M * N, "out"), M, N, K, _stream(stream)))
+
+
+def tl2_gemm(w, act, out, M, N, K, stream=None):
+    t = _torch()
+    _check(_lib.mth_tl2_gemm(_ptr(w, t.uint8, M * N * ((2 * K + 7) // 8), "w"), _ptr(act, t.float32, N * K, "act"),
+                             _ptr(out, t.float32, M * N, "out"), M, N, K, _stream(stream)))
+
+
+def tl_precompute_lut(act, lut, K, group, stream=None):
+    t = _torch()
+    n = (K // group) * (9 if group == 2 else 27)
+    _check(_lib.mth_tl_precompute_lut(_ptr(act, t.int8, K, "act"), _ptr(lut, t.int8, n, "lut"), K, group,
+                                      _stream(stream)))

@@ -1,0 +1,374 @@
+"""ctypes bindings for the CPU oracle (liboracle.so) and the compiled reference
+(oracle/_ref/libref_*.so).  TEST INFRASTRUCTURE ONLY — see oracle/__init__.py.
+
+All wrappers take and return numpy arrays; sizes are checked on the Python
+side so a wrong call raises instead of reading past a buffer.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def oracle_lib_path() -> str:
+    return os.path.join(_HERE, "liboracle.so")
+
+
+def ref_lib_path(variant: str = "avx2") -> str:
+    return os.path.join(_HERE, "_ref", f"libref_{variant}.so")
+
+
+def build(with_ref: bool | None = None) -> None:
+    """Compile liboracle.so and, when the reference tree exists, oracle/_ref."""
+    subprocess.run(["make", "-s", "-C", _HERE, "oracle"], check=True)
+    ref_root = os.environ.get("MYTHOS_REFERENCE", "/root/reference")
+    if with_ref is None:
+        with_ref = os.path.isdir(os.path.join(ref_root, "src"))
+    if with_ref:
+        subprocess.run(["make", "-s", "-C", _HERE, "ref", f"REF={ref_root}", "-j4"], check=True)
+
+
+def _p(a: np.ndarray, dtype) -> C.c_void_p:
+    assert a.dtype == dtype, (a.dtype, dtype)
+    assert a.flags["C_CONTIGUOUS"]
+    return C.c_void_p(a.ctypes.data)
+
+
+def i2s_bytes(M: int, K: int) -> int:
+    """Bytes the i2s_gemm family reads: row m at m*(K/4), element k at byte
+    k/4 of the row (src/kernel_i2s.cpp:54,207)."""
+    return (M - 1) * (K // 4) + (K - 1) // 4 + 1
+
+
+def _need(a: np.ndarray, n: int, name: str) -> None:
+    if a.size < n:
+        raise ValueError(f"{name}: {a.size} elements < {n} required")
+
+
+I64, I32, F32, U64 = C.c_int64, C.c_int, C.c_float, C.c_uint64
+VP = C.c_void_p
+
+
+class Oracle:
+    """The C restatement (oracle.c)."""
+
+    def __init__(self, path: str | None = None):
+        path = path or oracle_lib_path()
+        if not os.path.exists(path):
+            build(with_ref=False)
+        self.lib = L = C.CDLL(path)
+        sig = {
+            "orc_fp16_to_float_n": [VP, VP, I64],
+            "orc_oil8_gemm_scalar": [VP, VP, VP, VP, I64, I64, I64],
+            "orc_oil8_gemm_avx2": [VP, VP, VP, VP, I64, I64, I64],
+            "orc_oil8_gemv": [VP, VP, VP, VP, I64, I64, I64, I32],
+            "orc_oil4_gemm_scalar": [VP, VP, VP, VP, I64, I64, I64],
+            "orc_oil4_gemm_avx2": [VP, VP, VP, VP, I64, I64, I64],
+            "orc_oil4_gemv_blocked": [VP, VP, I64, VP, VP, I64, I64, I64, I32],
+            "orc_quantize_per_token": [VP, VP, I64, I64, VP, VP],
+            "orc_dequantize_per_tensor": [VP, VP, I64, F32],
+            "orc_i2s_gemv": [VP, F32, VP, F32, VP, I64],
+            "orc_i2s_gemm": [VP, VP, VP, I64, I64, I64],
+            "orc_i2s_gemm_vnni": [VP, VP, VP, I64, I64, I64],
+            "orc_i2s_gemv_f32": [VP, F32, VP, VP, I64, I64, I64, I32],
+            "orc_tl1_gemm": [VP, VP, VP, I64, I64, I64],
+            "orc_tl2_gemm": [VP, VP, VP, I64, I64, I64],
+            "orc_tl1_precompute_lut": [VP, VP, I64],
+            "orc_tl2_precompute_lut": [VP, VP, I64],
+            "orc_gemv": [F32, VP, VP, F32, VP, I64, I64],
+            "orc_rms_norm": [VP, VP, F32, VP, I64, I64],
+            "orc_silu": [VP, VP, I64],
+            "orc_oil4_gemm_prefill": [VP, VP, VP, I64, VP, VP, I64, I64, I64, I32],
+        }
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = None
+        L.orc_fp16_to_float.argtypes = [C.c_uint16]
+        L.orc_fp16_to_float.restype = F32
+        L.orc_half_to_float_codebook.argtypes = [C.c_uint16]
+        L.orc_half_to_float_codebook.restype = F32
+        L.orc_float_to_half_trunc.argtypes = [F32]
+        L.orc_float_to_half_trunc.restype = C.c_uint16
+        L.orc_rng_seed.argtypes = [VP, U64]
+        L.orc_rng_next_u64.argtypes = [VP]
+        L.orc_rng_next_u64.restype = U64
+        L.orc_rng_uniform.argtypes = [VP]
+        L.orc_rng_uniform.restype = F32
+        L.orc_rng_normal.argtypes = [VP]
+        L.orc_rng_normal.restype = F32
+        L.orc_rng_uniform_int.argtypes = [VP, I32, I32]
+        L.orc_rng_uniform_int.restype = I32
+
+    # -- rng ---------------------------------------------------------------
+    def _rng(self, seed):
+        st = (C.c_uint64 * 2)()
+        self.lib.orc_rng_seed(C.cast(st, VP), seed)
+        return st
+
+    def rng_u64(self, seed: int, n: int) -> np.ndarray:
+        st = self._rng(seed)
+        return np.array([self.lib.orc_rng_next_u64(C.cast(st, VP)) for _ in range(n)], np.uint64)
+
+    def rng_uniform(self, seed: int, n: int) -> np.ndarray:
+        st = self._rng(seed)
+        return np.array([self.lib.orc_rng_uniform(C.cast(st, VP)) for _ in range(n)], np.float32)
+
+    def rng_normal(self, seed: int, n: int) -> np.ndarray:
+        st = self._rng(seed)
+        return np.array([self.lib.orc_rng_normal(C.cast(st, VP)) for _ in range(n)], np.float32)
+
+    def rng_uniform_int(self, seed: int, lo: int, hi: int, n: int) -> np.ndarray:
+        st = self._rng(seed)
+        return np.array([self.lib.orc_rng_uniform_int(C.cast(st, VP), lo, hi) for _ in range(n)], np.int32)
+
+    # -- fp16 ----------------------------------------------------------------
+    def fp16_to_float(self, h: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(h, np.uint16)
+        f = np.empty(h.shape, np.float32)
+        self.lib.orc_fp16_to_float_n(_p(h, np.uint16), _p(f, np.float32), h.size)
+        return f
+
+    def half_to_float_codebook(self, h: int) -> float:
+        return self.lib.orc_half_to_float_codebook(h)
+
+    def float_to_half_trunc(self, f: float) -> int:
+        return self.lib.orc_float_to_half_trunc(f)
+
+    # -- oil8 ----------------------------------------------------------------
+    def oil8_gemm(self, idx, cb, act, M, N, K, variant="avx2"):
+        _need(idx, M * N * K, "idx"); _need(cb, 256, "cb"); _need(act, N * K, "act")
+        out = np.empty(M * N, np.float32)
+        f = self.lib.orc_oil8_gemm_avx2 if variant == "avx2" else self.lib.orc_oil8_gemm_scalar
+        f(_p(idx, np.uint8), _p(cb, np.float32), _p(act, np.float32), _p(out, np.float32), M, N, K)
+        return out
+
+    def oil8_gemv(self, idx, cb, x, M, K, batch, threads=1):
+        _need(idx, M * K, "idx"); _need(x, batch * K, "x")
+        y = np.empty((batch, M), np.float32)
+        self.lib.orc_oil8_gemv(_p(idx, np.uint8), _p(cb, np.float32), _p(x, np.float32),
+                               _p(y, np.float32), M, K, batch, threads)
+        return y
+
+    # -- oil4 ----------------------------------------------------------------
+    def oil4_gemm(self, nib, cb16, act, M, N, K, variant="scalar"):
+        _need(nib, M * N * K // 2, "nib"); _need(cb16, 16, "cb16"); _need(act, N * K, "act")
+        out = np.empty(M * N, np.float32)
+        f = self.lib.orc_oil4_gemm_avx2 if variant == "avx2" else self.lib.orc_oil4_gemm_scalar
+        f(_p(nib, np.uint8), _p(cb16, np.uint16), _p(act, np.float32), _p(out, np.float32), M, N, K)
+        return out
+
+    def oil4_gemv_blocked(self, nib, cb16, x, M, K, batch, block=128, threads=1):
+        _need(nib, M * K // 2, "nib"); _need(cb16, M * (K // block) * 16, "cb16"); _need(x, batch * K, "x")
+        y = np.empty((batch, M), np.float32)
+        self.lib.orc_oil4_gemv_blocked(_p(nib, np.uint8), _p(cb16, np.uint16), block,
+                                       _p(x, np.float32), _p(y, np.float32), M, K, batch, threads)
+        return y
+
+    def oil4_gemm_prefill(self, a_bf16, nib, cb16, M, N, K, block=128, threads=1):
+        _need(a_bf16, M * K, "a"); _need(nib, N * K // 2, "nib")
+        c16 = np.empty((M, N), np.uint16)
+        c32 = np.empty((M, N), np.float32)
+        self.lib.orc_oil4_gemm_prefill(_p(a_bf16, np.uint16), _p(nib, np.uint8), _p(cb16, np.uint16),
+                                       block, _p(c16, np.uint16), _p(c32, np.float32), M, N, K, threads)
+        return c16, c32
+
+    # -- int8 / ternary --------------------------------------------------------
+    def quantize_per_token(self, x, rows, cols):
+        _need(x, rows * cols, "x")
+        q = np.empty((rows, cols), np.int8)
+        s = np.empty(rows, np.float32)
+        inv = np.empty(rows, np.float32)
+        self.lib.orc_quantize_per_token(_p(x, np.float32), _p(q, np.int8), rows, cols,
+                                        _p(s, np.float32), _p(inv, np.float32))
+        return q, s, inv
+
+    def i2s_gemv(self, packed_row, w_scale, act, act_scale, K):
+        _need(packed_row, K // 4, "packed"); _need(act, K, "act")
+        out = np.empty(1, np.float32)
+        self.lib.orc_i2s_gemv(_p(packed_row, np.uint8), w_scale, _p(act, np.int8), act_scale,
+                              _p(out, np.float32), K)
+        return float(out[0])
+
+    def i2s_gemm(self, w, a, M, N, K):
+        _need(w, i2s_bytes(M, K), "w"); _need(a, N * K, "a")
+        o = np.empty(M * N, np.float32)
+        self.lib.orc_i2s_gemm(_p(w, np.uint8), _p(a, np.float32), _p(o, np.float32), M, N, K)
+        return o
+
+    def i2s_gemm_vnni(self, w, a, M, N, K):
+        _need(w, i2s_bytes(M, K), "w"); _need(a, N * K, "a")
+        o = np.empty(M * N, np.float32)
+        self.lib.orc_i2s_gemm_vnni(_p(w, np.uint8), _p(a, np.int8), _p(o, np.float32), M, N, K)
+        return o
+
+    def i2s_gemv_f32(self, packed, w_scale, x, M, K, batch, threads=1):
+        _need(packed, M * K // 4, "packed"); _need(x, batch * K, "x")
+        y = np.empty((batch, M), np.float32)
+        self.lib.orc_i2s_gemv_f32(_p(packed, np.uint8), w_scale, _p(x, np.float32),
+                                  _p(y, np.float32), M, K, batch, threads)
+        return y
+
+    def tl1_gemm(self, w, a, M, N, K):
+        _need(w, M * N * K // 4, "w"); _need(a, N * K, "a")
+        o = np.empty(M * N, np.float32)
+        self.lib.orc_tl1_gemm(_p(w, np.uint8), _p(a, np.float32), _p(o, np.float32), M, N, K)
+        return o
+
+    def tl2_gemm(self, w, a, M, N, K):
+        if K % 3:
+            raise ValueError("tl2_gemm is defined for K % 3 == 0")
+        _need(w, M * N * ((2 * K + 7) // 8), "w"); _need(a, N * K, "a")
+        o = np.empty(M * N, np.float32)
+        self.lib.orc_tl2_gemm(_p(w, np.uint8), _p(a, np.float32), _p(o, np.float32), M, N, K)
+        return o
+
+    # -- dense -----------------------------------------------------------------
+    def gemv(self, alpha, A, x, beta, y, M, N):
+        y = np.array(y, np.float32, copy=True)
+        self.lib.orc_gemv(alpha, _p(A, np.float32), _p(x, np.float32), beta, _p(y, np.float32), M, N)
+        return y
+
+    def rms_norm(self, x, g, eps, rows, dim):
+        y = np.empty((rows, dim), np.float32)
+        self.lib.orc_rms_norm(_p(x, np.float32), _p(g, np.float32), eps, _p(y, np.float32), rows, dim)
+        return y
+
+    def silu(self, x):
+        y = np.empty_like(x)
+        self.lib.orc_silu(_p(x, np.float32), _p(y, np.float32), x.size)
+        return y
+
+
+class Reference:
+    """The reference's own kernels (oracle/_ref/libref_<variant>.so)."""
+
+    def __init__(self, variant: str = "avx2"):
+        path = ref_lib_path(variant)
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.variant = variant
+        self.lib = L = C.CDLL(path)
+        sig = {
+            "ref_oil8_gemm": [VP, VP, VP, VP, I32, I32, I32],
+            "ref_oil4_gemm": [VP, VP, VP, VP, I32, I32, I32],
+            "ref_i2s_init": [],
+            "ref_i2s_gemv": [VP, F32, VP, F32, VP, I32],
+            "ref_i2s_gemm": [VP, VP, VP, I32, I32, I32],
+            "ref_i2s_gemm_vnni": [VP, VP, VP, I32, I32, I32],
+            "ref_tl1_gemm": [VP, VP, VP, I32, I32, I32],
+            "ref_tl2_gemm": [VP, VP, VP, I32, I32, I32],
+            "ref_quantize_per_token": [VP, VP, I64, I64, VP, VP],
+            "ref_rng_u64": [U64, VP, I64],
+            "ref_rng_uniform": [U64, VP, I64],
+            "ref_rng_normal": [U64, VP, I64],
+            "ref_rng_uniform_int": [U64, I32, I32, VP, I64],
+            "ref_gemv": [F32, VP, VP, F32, VP, I64, I64],
+            "ref_rms_norm": [VP, VP, F32, VP, I64, I64],
+            "ref_silu": [VP, VP, I64],
+        }
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = None
+        L.ref_float_to_half.argtypes = [F32]
+        L.ref_float_to_half.restype = C.c_uint16
+        L.ref_half_to_float.argtypes = [C.c_uint16]
+        L.ref_half_to_float.restype = F32
+
+    def oil8_gemm(self, idx, cb, act, M, N, K):
+        _need(idx, M * N * K, "idx"); _need(act, N * K, "act")
+        out = np.empty(M * N, np.float32)
+        self.lib.ref_oil8_gemm(_p(idx, np.uint8), _p(cb, np.float32), _p(act, np.float32),
+                               _p(out, np.float32), M, N, K)
+        return out
+
+    def oil4_gemm(self, nib, cb16, act, M, N, K):
+        _need(nib, M * N * K // 2, "nib"); _need(act, N * K, "act")
+        out = np.empty(M * N, np.float32)
+        self.lib.ref_oil4_gemm(_p(nib, np.uint8), _p(cb16, np.uint16), _p(act, np.float32),
+                               _p(out, np.float32), M, N, K)
+        return out
+
+    def i2s_init(self):
+        self.lib.ref_i2s_init()
+
+    def i2s_gemv(self, packed_row, w_scale, act, act_scale, K):
+        out = np.empty(1, np.float32)
+        self.lib.ref_i2s_gemv(_p(packed_row, np.uint8), w_scale, _p(act, np.int8), act_scale,
+                              _p(out, np.float32), K)
+        return float(out[0])
+
+    def i2s_gemm(self, w, a, M, N, K):
+        o = np.empty(M * N, np.float32)
+        self.lib.ref_i2s_gemm(_p(w, np.uint8), _p(a, np.float32), _p(o, np.float32), M, N, K)
+        return o
+
+    def i2s_gemm_vnni(self, w, a, M, N, K):
+        o = np.full(M * N, np.nan, np.float32)
+        self.lib.ref_i2s_gemm_vnni(_p(w, np.uint8), _p(a, np.int8), _p(o, np.float32), M, N, K)
+        return o
+
+    def tl1_gemm(self, w, a, M, N, K):
+        o = np.empty(M * N, np.float32)
+        self.lib.ref_tl1_gemm(_p(w, np.uint8), _p(a, np.float32), _p(o, np.float32), M, N, K)
+        return o
+
+    def tl2_gemm(self, w, a, M, N, K):
+        o = np.empty(M * N, np.float32)
+        self.lib.ref_tl2_gemm(_p(w, np.uint8), _p(a, np.float32), _p(o, np.float32), M, N, K)
+        return o
+
+    def quantize_per_token(self, x, rows, cols):
+        q = np.empty((rows, cols), np.int8)
+        s = np.empty(rows, np.float32)
+        inv = np.empty(rows, np.float32)
+        self.lib.ref_quantize_per_token(_p(x, np.float32), _p(q, np.int8), rows, cols,
+                                        _p(s, np.float32), _p(inv, np.float32))
+        return q, s, inv
+
+    def float_to_half(self, f: float) -> int:
+        return self.lib.ref_float_to_half(f)
+
+    def half_to_float(self, h: int) -> float:
+        return self.lib.ref_half_to_float(h)
+
+    def rng_u64(self, seed, n):
+        o = np.empty(n, np.uint64)
+        self.lib.ref_rng_u64(seed, _p(o, np.uint64), n)
+        return o
+
+    def rng_uniform(self, seed, n):
+        o = np.empty(n, np.float32)
+        self.lib.ref_rng_uniform(seed, _p(o, np.float32), n)
+        return o
+
+    def rng_normal(self, seed, n):
+        o = np.empty(n, np.float32)
+        self.lib.ref_rng_normal(seed, _p(o, np.float32), n)
+        return o
+
+    def rng_uniform_int(self, seed, lo, hi, n):
+        o = np.empty(n, np.int32)
+        self.lib.ref_rng_uniform_int(seed, lo, hi, _p(o, np.int32), n)
+        return o
+
+    def gemv(self, alpha, A, x, beta, y, M, N):
+        y = np.array(y, np.float32, copy=True)
+        self.lib.ref_gemv(alpha, _p(A, np.float32), _p(x, np.float32), beta, _p(y, np.float32), M, N)
+        return y
+
+    def rms_norm(self, x, g, eps, rows, dim):
+        y = np.empty((rows, dim), np.float32)
+        self.lib.ref_rms_norm(_p(x, np.float32), _p(g, np.float32), eps, _p(y, np.float32), rows, dim)
+        return y
+
+    def silu(self, x):
+        y = np.empty_like(x)
+        self.lib.ref_silu(_p(x, np.float32), _p(y, np.float32), x.size)
+        return y

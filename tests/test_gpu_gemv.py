@@ -1,0 +1,187 @@
+"""GPU parity: decode GEMV kernels (OIL8, OIL4, I2_S) through the C ABI
+against the CPU oracle on the same seeded inputs.
+
+Bars: OIL8 FP32 within 1e-5 relative (norm-wise and
+per element against sum|w*x|); OIL4 within 2e-3 (asserted here at 1e-5,
+since the kernel accumulates in FP32 with exact FP16 codebook values);
+ternary / int8 paths bit-exact.
+"""
+import numpy as np
+import pytest
+
+import synth
+from conftest import fp32_close
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dev):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a.copy()).to(dev)
+
+
+def empty(n, dtype, dev):
+    import torch
+    return torch.full((n,), float("nan") if dtype.is_floating_point else 0, dtype=dtype, device=dev)
+
+
+# ------------------------------------------------------------------ OIL8 --
+@pytest.mark.parametrize("M,K,batch", [
+    (4096, 4096, 1),     # config 1
+    (300, 4096, 1),      # ragged row count
+    (64, 1024, 1),       # one segment per lane
+    (129, 2048, 3),      # batch > 1
+    (4096, 4096, 16),    # decode batch 16
+    (33, 1000, 2),       # K % 16 != 0 -> generic kernel
+    (5, 4112, 1),        # K > 4096 -> generic kernel
+])
+def test_oil8_gemv(M, K, batch, oracle, mth, dev):
+    import torch
+    print(f"oil8_gemv M={M} K={K} batch={batch}", flush=True)
+    idx, cb, x = synth.oil8(M, K, batch)
+    y = empty(batch * M, torch.float32, dev)
+    mth.oil8_gemv(to_dev(idx, dev), to_dev(cb, dev), to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    ref = oracle.oil8_gemv(idx, cb, x, M, K, batch, threads=8)
+    absw = np.abs(cb[idx]).astype(np.float64) @ np.abs(x.astype(np.float64)).T
+    fp32_close(y.cpu().numpy().reshape(batch, M), ref, absw.T, 1e-5, "oil8_gemv")
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 3, 37), (16, 4, 256), (3, 1, 4096), (2, 5, 1)])
+def test_oil8_gemm_reference_indexing(M, N, K, oracle, mth, dev):
+    import torch
+    print(f"oil8_gemm M={M} N={N} K={K}", flush=True)
+    g = np.random.default_rng(11)
+    idx = g.integers(0, 256, M * N * K, dtype=np.uint8)
+    cb = g.normal(0, 0.02, 256).astype(np.float32)
+    act = g.normal(0, 1, N * K).astype(np.float32)
+    out = empty(M * N, torch.float32, dev)
+    mth.oil8_gemm(to_dev(idx, dev), to_dev(cb, dev), to_dev(act, dev), out, M, N, K)
+    torch.cuda.synchronize()
+    ref = oracle.oil8_gemm(idx, cb, act, M, N, K, "avx2")
+    W = np.abs(cb[idx.reshape(M * N, K)]).astype(np.float64)
+    A = np.abs(act.reshape(N, K)).astype(np.float64)
+    absw = np.einsum("rk,rk->r", W, A[np.arange(M * N) % N])
+    fp32_close(out.cpu().numpy(), ref, absw, 1e-5, "oil8_gemm")
+
+
+def test_oil8_integer_codebook_bit_exact(oracle, mth, dev):
+    """cb[i] = i - 128 and integer x: every partial sum is an exact integer,
+    so any summation order gives the reference's bits."""
+    import torch
+    M, K = 512, 4096
+    g = np.random.default_rng(5)
+    idx = g.integers(0, 256, (M, K), dtype=np.uint8)
+    cb = (np.arange(256) - 128).astype(np.float32)
+    x = g.integers(-3, 4, (1, K)).astype(np.float32)
+    y = empty(M, torch.float32, dev)
+    mth.oil8_gemv(to_dev(idx, dev), to_dev(cb, dev), to_dev(x, dev), y, M, K, 1)
+    ref = oracle.oil8_gemv(idx, cb, x, M, K, 1)
+    assert np.array_equal(y.cpu().numpy(), ref.ravel())
+
+
+# ------------------------------------------------------------------ OIL4 --
+@pytest.mark.parametrize("M,K,batch,block", [
+    (11008, 4096, 1, 128),   # config 2, b=1
+    (11008, 4096, 16, 128),  # config 2, b=16
+    (100, 256, 3, 32),
+    (257, 4096, 1, 0),       # one shared codebook
+    (31, 2048, 2, 2048),
+    (30, 100, 2, 50),        # K % 32 != 0 -> generic kernel
+    (9, 4352, 1, 128),       # K > 4096 -> generic kernel
+])
+def test_oil4_gemv(M, K, batch, block, oracle, mth, dev):
+    import torch
+    print(f"oil4_gemv M={M} K={K} batch={batch} block={block}", flush=True)
+    packed, cbs, x = synth.oil4(M, K, batch, block)
+    y = empty(batch * M, torch.float32, dev)
+    mth.oil4_gemv(to_dev(packed, dev), to_dev(cbs, dev), block, to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    if block:
+        ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, M, K, batch, block, threads=8)
+    else:
+        ref = oracle.oil4_gemm(packed.ravel(), cbs, np.ascontiguousarray(x[0]), M, 1, K, "scalar").reshape(1, M)
+    W = synth.dequant_oil4(packed, cbs, M, K, block)
+    absw = np.abs(W).astype(np.float64) @ np.abs(x.astype(np.float64)).T
+    fp32_close(y.cpu().numpy().reshape(batch, M), ref, absw.T, 1e-5, "oil4_gemv")
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 3, 48), (5, 2, 33), (4, 1, 4096), (3, 4, 1)])
+def test_oil4_gemm_reference_indexing(M, N, K, oracle, mth, dev):
+    import torch
+    print(f"oil4_gemm M={M} N={N} K={K}", flush=True)
+    g = np.random.default_rng(12)
+    nbytes = (M * N * K + 1) // 2
+    packed = g.integers(0, 256, nbytes, dtype=np.uint8)
+    cb = synth.float_to_half_trunc(g.normal(0, 0.02, 16).astype(np.float32))
+    act = g.normal(0, 1, N * K).astype(np.float32)
+    out = empty(M * N, torch.float32, dev)
+    mth.oil4_gemm(to_dev(packed, dev), to_dev(cb, dev), to_dev(act, dev), out, M, N, K)
+    torch.cuda.synchronize()
+    ref = oracle.oil4_gemm(np.concatenate([packed, np.zeros(8, np.uint8)]), cb, act, M, N, K, "scalar")
+    got = out.cpu().numpy()
+    scale = np.abs(synth.fp16_bits_to_f32(cb)).max() * np.abs(act).sum()
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * scale), np.abs(got - ref).max()
+
+
+# ------------------------------------------------------------- int8/I2_S --
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (16, 11008), (3, 5), (2, 1)])
+def test_quantize_per_token_bit_exact(rows, cols, oracle, mth, dev):
+    import torch
+    g = np.random.default_rng(rows * 1000 + cols)
+    x = g.normal(0, 1, (rows, cols)).astype(np.float32)
+    x[0, 0] = 0.0
+    if rows > 2:
+        x[2] = 0.0  # all-zero row: max_abs floor 1e-10
+    q = empty(rows * cols, torch.int8, dev)
+    s = empty(rows, torch.float32, dev)
+    inv = empty(rows, torch.float32, dev)
+    mth.quantize_per_token(to_dev(x, dev), q, s, inv, rows, cols)
+    torch.cuda.synchronize()
+    rq, rs, rinv = oracle.quantize_per_token(x, rows, cols)
+    assert np.array_equal(q.cpu().numpy().reshape(rows, cols), rq)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(inv.cpu().numpy(), rinv)
+
+
+@pytest.mark.parametrize("M,K,batch", [
+    (4096, 4096, 1),    # config 3
+    (4096, 11008, 1),   # decoder down projection shape
+    (100, 256, 3),
+    (77, 1024, 2),
+    (50, 100, 2),       # K % 64 != 0 -> generic kernel
+    (8, 20480, 1),      # K > 16384 -> generic kernel
+])
+def test_i2s_gemv_f32_bit_exact(M, K, batch, oracle, mth, dev):
+    import torch
+    print(f"i2s_gemv_f32 M={M} K={K} batch={batch}", flush=True)
+    packed, w_scale, x = synth.ternary(M, K, batch)
+    y = empty(batch * M, torch.float32, dev)
+    mth.i2s_gemv_f32(to_dev(packed, dev), w_scale, to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    ref = oracle.i2s_gemv_f32(packed.ravel(), float(w_scale), x, M, K, batch, threads=8)
+    assert np.array_equal(y.cpu().numpy().reshape(batch, M), ref)
+
+
+def test_i2s_code3_and_unfused_bit_exact(oracle, mth, dev):
+    """Code 11 decodes to +1 (src/kernel_i2s.cpp:16-21); the unfused entry
+    point takes int8 acts + act_scale like the reference i2s_gemv."""
+    import torch
+    M, K, batch = 640, 4096, 2
+    g = np.random.default_rng(3)
+    packed = g.integers(0, 256, (M, K // 4), dtype=np.uint8)  # all four codes
+    x = g.normal(0, 1, (batch, K)).astype(np.float32)
+    q, _, inv = oracle.quantize_per_token(x, batch, K)
+    y = empty(batch * M, torch.float32, dev)
+    mth.i2s_gemv(to_dev(packed, dev), 0.75, to_dev(q, dev), to_dev(inv, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    ref = np.array([[oracle.i2s_gemv(np.ascontiguousarray(packed[m]), 0.75, np.ascontiguousarray(q[t]),
+                                     float(inv[t]), K) for m in range(M)] for t in range(batch)], np.float32)
+    assert np.array_equal(y.cpu().numpy().reshape(batch, M), ref)
+    y2 = empty(batch * M, torch.float32, dev)
+    mth.i2s_gemv_f32(to_dev(packed, dev), 0.75, to_dev(x, dev), y2, M, K, batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(batch, M), ref)
