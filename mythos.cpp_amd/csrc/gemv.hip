@@ -1,25 +1,37 @@
-// gemv.hip — OIL8 / OIL4 codebook GEMV for decode (batch 1..16) on gfx950.
+// gemv.hip — OIL8 / OIL4 codebook GEMV for decode on gfx950.
 //
 // Replaces the CPU loops of src/kernel_oil8.cpp:14-71 and
-// src/kernel_oil4.cpp:31-125 (reference semantics: sum_k cb[idx]*x[k] in
-// FP32 with the codebook value exact in FP32).
+// src/kernel_oil4.cpp:31-125 (reference semantics: sum_k cb[idx]*x[k] in FP32
+// with the codebook value exact in FP32).  Weights stay in the reference's
+// row-major layout; every kernel issues its weight loads first, so HBM latency
+// overlaps the codebook staging.
 //
-// Fast path layout (row-major weights, as the reference stores them):
-//   * a wave owns a run of rows; lane l streams 16-byte segments
-//     seg = l + 64*s (s < NSEG) of every row with one 128-bit load each,
-//     so a wave reads 1 KiB of contiguous weight bytes per instruction;
-//   * the lane's activations x[seg*W .. +W) stay in VGPRs for the whole
-//     wave (W = weights per segment), loaded once;
-//   * OIL8: the 256-entry FP32 codebook is staged in LDS replicated over 32
-//     bank columns (tab[e*32 + c]); lane l reads column l%32, so the 32 lanes
-//     of a half-wave hit 32 different banks whatever the indices are;
-//   * OIL4: the 16 codebook entries a lane needs are written (as FP32) into a
-//     private LDS column of the lane's wave (tab[e*64 + lane]) and gathered
-//     from there: again one bank per lane, no conflicts;
-//   * per-row partial sums are reduced across the wave with xor-shuffles.
-// Anything else (K not a multiple of 16, unaligned pointers, K beyond the
-// register budget, the reference's per-(m,n) weight indexing) goes to the
-// generic kernels at the bottom: one wave per output, lanes striding k.
+// OIL8 (oil8_gemv_k):
+//   * workgroup = 4 waves x R rows; wave w owns columns [1024w, 1024w+1024),
+//     lane l the 16 consecutive indices at 1024w + 16l (one 128-bit load per
+//     row), its 16 activations live in VGPRs;
+//   * the 256-entry FP32 codebook is staged once per workgroup in LDS and
+//     gathered with one ds_read_b32 per weight;
+//   * R row sums are reduced across the wave by a transposed butterfly
+//     (log2(R) halving steps, then a plain butterfly) and across the 4 waves
+//     through LDS in a fixed order (deterministic).
+// OIL4 (oil4_gemv_mfma, batch 1):
+//   * workgroup = 16 rows; wave w owns K/4 columns in chunks of 128 (one
+//     codebook block);  the dequantised weights go straight into the A operand
+//     of v_mfma_f32_16x16x32_f16: lane (r = l%16, g = l/16) holds row r,
+//     k = 32g + 8i + v of MFMA i, i.e. exactly the 8 nibbles of dword i of its
+//     own 16-byte load;
+//   * the row's 16 FP16 codebook entries are written into two LDS columns
+//     (r and r+16) per wave; a nibble-spread dword gives each gather address
+//     with one v_perm_b32 and ds_read_u16_d16[_hi] packs the FP16 values into
+//     the MFMA operand registers directly (no conversions);
+//   * x is split per wave into FP16 hi + lo parts after a power-of-two scale
+//     (x*2^s = hi + lo + O(2^-22)), placed as B columns 0 and 1, so
+//     D[:,0] + D[:,1] is the FP32 dot product; products are exact, sums FP32.
+// Other shapes (K not a multiple of 16/512, K > 4096, unaligned pointers,
+// batched OIL4, codebook blocks that are not multiples of 128, the
+// reference's per-(m,n) indexing) run on oil4_gemv_valu or the generic
+// one-wave-per-output kernels.
 #include "common.h"
 #include "launch.h"
 
@@ -29,98 +41,108 @@ namespace {
 constexpr int kWG = 256;
 constexpr int kWaves = kWG / MTH_WAVE;
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// Compiler-level ordering point for wave-private LDS traffic.  LDS operations
+// of one wave execute in program order, so no wait is needed, only that the
+// compiler keeps the order.
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
+
+// v_perm selector building the LDS byte address (byte b of S0 << 8) | S1.byte0
+__device__ __forceinline__ uint32_t perm_addr(uint32_t packed, uint32_t lane4, int b) {
+    return __builtin_amdgcn_perm(packed, lane4, 0x0c0c0000u | ((uint32_t)(4 + b) << 8));
+}
+
+// Transposed reduction of R per-lane values over the 64 lanes.  After it,
+// every lane holds the wave total of row (lane / (64/R)).
+template <int R>
+__device__ __forceinline__ float transposed_sum(float (&v)[R], int lane) {
+#pragma unroll
+    for (int n = R, mask = 32; n > 1; n >>= 1, mask >>= 1) {
+        const bool hi = (lane & mask) != 0;
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const float send = hi ? v[j] : v[j + n / 2];
+            const float keep = hi ? v[j + n / 2] : v[j];
+            v[j] = keep + __shfl_xor(send, mask, MTH_WAVE);
+        }
+    }
+    float s = v[0];
+#pragma unroll
+    for (int mask = 32 / R; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask, MTH_WAVE);
+    return s;
+}
 
 // ===================================================================
 // OIL8
 // ===================================================================
-template <int NSEG, int RG>
-__global__ __launch_bounds__(kWG, 2) void oil8_gemv_fast(
-    const uint8_t* __restrict__ idx, const float* __restrict__ cb, const float* __restrict__ x,
-    float* __restrict__ y, int M, int K, int batch, int rows_per_wave) {
-    __shared__ float tab[256 * 32];
+// The codebook and x are fetched, and the table staged, before the weight
+// stream is released: a load issued after other waves' weight loads waits
+// behind them in the CU's in-order memory pipeline (~1.5-3 us at this size),
+// while the stream itself only starts ~0.5 us later this way.  The single
+// unreplicated 1 KiB table costs ~1.9x a conflict-free gather (measured on
+// gfx950: 3.6 vs 1.9 cycles per wave64 ds_read_b32) but needs one store per
+// thread to fill, where a replicated table's fill would sit on this critical
+// path.  idx and x are not __restrict__, so the compiler keeps their loads in
+// program order around the barrier.
+template <int R>
+__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void oil8_gemv_k(const uint8_t* idx, const float* __restrict__ cb, const float* x, float* __restrict__ y, int M,
+                 int K, int batch) {
+    __shared__ float tab[256];
+    __shared__ float part[kWaves][R];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nseg = K >> 4;
-    const int r0 = (blockIdx.x * kWaves + wave) * rows_per_wave;
-    const int r1 = min(M, r0 + rows_per_wave);
+    const int kq = wave * 1024 + lane * 16;  // first column of this lane
+    const bool act = kq < K;
+    const int kl = act ? kq : K - 16;        // clamped: every load below is unconditional
+    const int m0 = blockIdx.x * R;
 
-    auto load_rows = [&](uint4 (&w)[RG][NSEG], int r) {
+    float4 xq[4];
 #pragma unroll
-        for (int g = 0; g < RG; ++g)
-#pragma unroll
-            for (int s = 0; s < NSEG; ++s) {
-                const int seg = lane + 64 * s;
-                if (r + g < r1 && seg < nseg)
-                    w[g][s] = ld_stream(idx + (int64_t)(r + g) * K + (int64_t)seg * 16);
-                else
-                    w[g][s] = make_uint4(0, 0, 0, 0);
-            }
-    };
-
-    uint4 wc[RG][NSEG];
-    load_rows(wc, r0);  // first weights in flight before the table is staged
-
-#pragma unroll 4
-    for (int i = 0; i < 32; ++i) {
-        const int e = (tid >> 5) + 8 * i;
-        tab[e * 32 + (tid & 31)] = cb[e];
-    }
+    for (int q = 0; q < 4; ++q) xq[q] = ldf4(x + kl + 4 * q);
+    tab[tid] = cb[tid];
     __syncthreads();
-    if (r0 >= M) return;
-    const float* col = tab + (lane & 31);
+    uint4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = ld_stream(idx + (int64_t)min(m0 + r, M - 1) * K + kl);
 
     for (int t = 0; t < batch; ++t) {
-        const float* xt = x + (int64_t)t * K;
-        float xr[NSEG][16];
+        float xr[16];
+        if (t > 0) {
 #pragma unroll
-        for (int s = 0; s < NSEG; ++s) {
-            const int seg = lane + 64 * s;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float4 v = seg < nseg ? ldf4(xt + seg * 16 + 4 * q) : make_float4(0, 0, 0, 0);
-                xr[s][4 * q + 0] = v.x; xr[s][4 * q + 1] = v.y;
-                xr[s][4 * q + 2] = v.z; xr[s][4 * q + 3] = v.w;
-            }
+            for (int q = 0; q < 4; ++q) xq[q] = ldf4(x + (int64_t)t * K + kl + 4 * q);
         }
-        if (t > 0) load_rows(wc, r0);
-        for (int r = r0; r < r1; r += RG) {
-            uint4 wn[RG][NSEG];
-            const bool more = r + RG < r1;
-            if (more) load_rows(wn, r + RG);
-            float acc[RG];
 #pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                acc[g] = 0.0f;
-#pragma unroll
-                for (int s = 0; s < NSEG; ++s) {
-                    if (s == NSEG - 1 && lane + 64 * s >= nseg) continue;
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        const uint32_t wd = u4get(wc[g][s], d);
-#pragma unroll
-                        for (int b = 0; b < 4; ++b) {
-                            const uint32_t e = (wd >> (8 * b)) & 0xffu;
-                            acc[g] = fmaf(col[e * 32], xr[s][4 * d + b], acc[g]);
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                const float v = group_sum<64>(acc[g]);
-                if (lane == 0 && r + g < r1) y[(int64_t)t * M + r + g] = v;
-            }
-            if (more) {
-#pragma unroll
-                for (int g = 0; g < RG; ++g)
-#pragma unroll
-                    for (int s = 0; s < NSEG; ++s) wc[g][s] = wn[g][s];
-            }
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = act ? xq[q] : make_float4(0, 0, 0, 0);
+            xr[4 * q] = v.x; xr[4 * q + 1] = v.y; xr[4 * q + 2] = v.z; xr[4 * q + 3] = v.w;
         }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t wd = u4get(w[r], d);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) acc[r] = fmaf(tab[(wd >> (8 * b)) & 0xffu], xr[4 * d + b], acc[r]);
+            }
+            if (!act) acc[r] = 0.0f;
+        }
+        const float s = transposed_sum<R>(acc, lane);
+        constexpr int L = MTH_WAVE / R;
+        if ((lane % L) == 0) part[wave][lane / L] = s;
+        __syncthreads();
+        if (tid < R && m0 + tid < M)
+            y[(int64_t)t * M + m0 + tid] = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+        __syncthreads();
     }
 }
 
-// Generic: one wave per output element.  Row r uses weights base + r*K and
+// Generic: one wave per output element.  Row r uses weights idx + r*K and
 // activation row (r % xmod) + t; out[t*ldy + r].
 __global__ __launch_bounds__(kWG) void oil8_generic(
     const uint8_t* __restrict__ idx, const float* __restrict__ cb, const float* __restrict__ act,
@@ -139,12 +161,154 @@ __global__ __launch_bounds__(kWG) void oil8_generic(
 }
 
 // ===================================================================
-// OIL4
+// OIL4, batch 1, matrix cores
+// ===================================================================
+// LDS codebook table of the workgroup: entry e of wave w, column c (0..31)
+// sits in the low half of the dword at byte
+//     ((e*NW/2 + w/2) << 8) | ((w & 1) << 7) | (c << 2),
+// so one v_perm_b32 builds the address from a nibble-spread byte that already
+// carries e*NW/2 + w/2 and a per-lane byte (w & 1)*128 + 4c.  Lanes l and
+// l+32 share a column and always read the same row's table; the two 32-lane
+// halves of a wave64 access are serviced separately, so no gather conflicts.
+template <int NW, int NC, bool SHARED>
+__global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, const uint16_t* cbs,
+                                                          int cb_block, const float* __restrict__ x,
+                                                          float* __restrict__ y, int M, int K) {
+    constexpr int KW = NC * 128;  // columns per wave
+    constexpr int HS = (NW == 8) ? 2 : 1;  // nibble shift that leaves room for w/2 in the index byte
+    __shared__ uint32_t tab[16 * NW * 32];
+    // per wave: B fragments of x_hi (column 0), x_lo (column 1), then a zero
+    // block read by the lanes of columns 2..15
+    __shared__ __align__(16) _Float16 xf[NW][3 * KW];
+    __shared__ float part[NW][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int row = blockIdx.x * 16 + r;
+    const int rowc = min(row, M - 1);  // clamped: all loads are unconditional
+    const int k0 = wave * KW;
+    const int nb = SHARED ? 1 : K / cb_block;
+
+    // Issue order.  The CU's memory pipeline returns data in issue order, so
+    // a load issued behind another wave's HBM stream waits for that stream.
+    // Every wave therefore issues its x loads first, a plain s_barrier (no
+    // fence: it does not wait for the loads) makes sure the whole workgroup
+    // has issued them, and only then are the codebook and nibble streams
+    // issued.  nib / cbs are not __restrict__, so these loads stay below.
+    const bool xl = lane * 16 < KW;
+    float4 xq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xq[q] = ldf4(x + k0 + (xl ? lane * 16 : 0) + 4 * q);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    uint2 wc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int kc = k0 + c * 128;
+        const uint16_t* cp = SHARED ? cbs + 4 * g : cbs + ((int64_t)rowc * nb + kc / cb_block) * 16 + 4 * g;
+        wc[c] = *(const uint2*)cp;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wn[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        wn[c] = ld_stream(nib + (int64_t)rowc * (K >> 1) + ((k0 + c * 128 + 32 * g) >> 1));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // x slice of this wave -> power-of-two scale -> FP16 hi/lo B fragments
+    // (wave-private LDS: only the wave's own program order matters)
+    float xv[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        xv[4 * q] = xl ? xq[q].x : 0.0f; xv[4 * q + 1] = xl ? xq[q].y : 0.0f;
+        xv[4 * q + 2] = xl ? xq[q].z : 0.0f; xv[4 * q + 3] = xl ? xq[q].w : 0.0f;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(xv[j]));
+    mx = wave_max(mx);
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.0e38f) (void)frexpf(mx, &e);
+    const int sh = (mx > 0.0f && mx <= 3.0e38f) ? 15 - e : 0;  // max|x|*2^sh < 2^15
+    if (xl) {
+        const int c = lane >> 3, gg = (lane & 7) >> 1;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int i = 2 * (lane & 1) + q;
+            half8 hi, lo;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                const float xs = ldexpf(xv[8 * q + v], sh);
+                const _Float16 h = (_Float16)xs;
+                hi[v] = h;
+                lo[v] = (_Float16)(xs - (float)h);
+            }
+            *(half8*)&xf[wave][((c * 4 + i) * 4 + gg) * 8] = hi;
+            *(half8*)&xf[wave][(((NC + c) * 4 + i) * 4 + gg) * 8] = lo;
+        }
+    }
+    for (int z = lane * 8; z < KW; z += 64 * 8) *(half8*)&xf[wave][2 * KW + z] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    wave_lds_order();
+
+    const int n = lane & 15;
+    const uint32_t col4 = ((uint32_t)(wave & 1) << 7) | ((uint32_t)(lane & 31) << 2);
+    const uint32_t wmask = 0x01010101u * (uint32_t)(wave >> 1);
+    uint16_t* tw = (uint16_t*)tab;
+    const char* tr = (const char*)tab;
+    // B fragment of MFMA (c, i) for this lane: column n's block at byte
+    // offset (c*4 + i)*64 from its base; columns >= 2 read the zero block
+    const char* xb = (const char*)&xf[wave][(n < 2 ? n : 2) * KW] + g * 16;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        // row r's entries 4g..4g+3 into columns r and r+16 (fp16 in the low half)
+        const uint32_t e2[2] = {wc[c].x, wc[c].y};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint16_t h = (uint16_t)(e2[j >> 1] >> (16 * (j & 1)));
+            const int slot = (((4 * g + j) * (NW / 2) + (wave >> 1)) * 64) + (wave & 1) * 32;
+            tw[(slot + r) * 2] = h;
+            tw[(slot + r + 16) * 2] = h;
+        }
+        wave_lds_order();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = u4get(wn[c], i);
+            // index bytes e*NW/2 + wave/2 for the even (low) and odd (high) nibbles
+            const uint32_t lo4 = ((d << HS) & (0x0f0f0f0fu << HS)) | wmask;
+            const uint32_t hi4 = ((d >> (4 - HS)) & (0x0f0f0f0fu << HS)) | wmask;
+            half8 a;
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                a[v] = *(const _Float16*)(tr + perm_addr((v & 1) ? hi4 : lo4, col4, v >> 1));
+            const half8 b = *(const half8*)(xb + (c * 4 + i) * 64);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+        }
+        wave_lds_order();
+    }
+    // D[4g+i][n]: rows' hi (n = 0) + lo (n = 1) parts
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float s = acc[i] + __shfl_xor(acc[i], 1, MTH_WAVE);
+        if (n == 0) part[wave][4 * g + i] = ldexpf(s, -sh);
+    }
+    __syncthreads();
+    if (tid < 16 && blockIdx.x * 16 + tid < M) {
+        float sum = part[0][tid];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sum += part[w][tid];
+        y[blockIdx.x * 16 + tid] = sum;
+    }
+}
+
+// ===================================================================
+// OIL4, vector-ALU path (batched decode and other block sizes)
 // ===================================================================
 // 16 bytes of nibbles = 32 weights per segment; element k of a row is the low
-// nibble of byte k/2 for even k, the high nibble for odd k.
+// nibble of byte k/2 for even k, the high nibble for odd k.  Each lane writes
+// the 16 entries of its segment's codebook (FP32) into a private LDS column.
 template <int NSEG, int RG, bool SHARED>
-__global__ __launch_bounds__(kWG, 2) void oil4_gemv_fast(
+__global__ __launch_bounds__(kWG, 2) void oil4_gemv_valu(
     const uint8_t* __restrict__ nib, const uint16_t* __restrict__ cbs, int cb_block,
     const float* __restrict__ x, float* __restrict__ y, int M, int K, int batch, int rows_per_wave) {
     __shared__ float tab[kWaves][16 * 64];
@@ -156,22 +320,22 @@ __global__ __launch_bounds__(kWG, 2) void oil4_gemv_fast(
     const int r1 = min(M, r0 + rows_per_wave);
     float* col = &tab[wave][lane];
 
-    auto load_rows = [&](uint4 (&w)[RG][NSEG], uint4 (&c)[RG][NSEG][2], int r) {
+    auto load_rows = [&](uint4 (&w)[RG][NSEG], uint4 (&c)[RG][NSEG][2], int rr) {
 #pragma unroll
-        for (int g = 0; g < RG; ++g)
+        for (int gi = 0; gi < RG; ++gi)
 #pragma unroll
             for (int s = 0; s < NSEG; ++s) {
                 const int seg = lane + 64 * s;
-                if (r + g < r1 && seg < nseg) {
-                    w[g][s] = ld_stream(nib + (int64_t)(r + g) * (K >> 1) + (int64_t)seg * 16);
+                if (rr + gi < r1 && seg < nseg) {
+                    w[gi][s] = ld_stream(nib + (int64_t)(rr + gi) * (K >> 1) + (int64_t)seg * 16);
                     if (!SHARED) {
-                        const uint16_t* cp = cbs + ((int64_t)(r + g) * nb + seg / seg_per_blk) * 16;
-                        c[g][s][0] = ld16(cp);
-                        c[g][s][1] = ld16(cp + 8);
+                        const uint16_t* cp = cbs + ((int64_t)(rr + gi) * nb + seg / seg_per_blk) * 16;
+                        c[gi][s][0] = ld16(cp);
+                        c[gi][s][1] = ld16(cp + 8);
                     }
                 } else {
-                    w[g][s] = make_uint4(0, 0, 0, 0);
-                    if (!SHARED) c[g][s][0] = c[g][s][1] = make_uint4(0, 0, 0, 0);
+                    w[gi][s] = make_uint4(0, 0, 0, 0);
+                    if (!SHARED) c[gi][s][0] = c[gi][s][1] = make_uint4(0, 0, 0, 0);
                 }
             }
     };
@@ -179,7 +343,6 @@ __global__ __launch_bounds__(kWG, 2) void oil4_gemv_fast(
     uint4 wc[RG][NSEG], cc[RG][NSEG][2];
     load_rows(wc, cc, r0);
     if (SHARED) {
-        // one codebook for the tensor: every wave fills its own columns once
         const uint4 c0 = ld16(cbs), c1 = ld16(cbs + 8);
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -203,58 +366,57 @@ __global__ __launch_bounds__(kWG, 2) void oil4_gemv_fast(
             }
         }
         if (t > 0) load_rows(wc, cc, r0);
-        for (int r = r0; r < r1; r += RG) {
+        for (int rr = r0; rr < r1; rr += RG) {
             uint4 wn[RG][NSEG], cn[RG][NSEG][2];
-            const bool more = r + RG < r1;
-            if (more) load_rows(wn, cn, r + RG);
+            const bool more = rr + RG < r1;
+            if (more) load_rows(wn, cn, rr + RG);
             float acc[RG];
 #pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                acc[g] = 0.0f;
+            for (int gi = 0; gi < RG; ++gi) {
+                acc[gi] = 0.0f;
 #pragma unroll
                 for (int s = 0; s < NSEG; ++s) {
                     if (s == NSEG - 1 && lane + 64 * s >= nseg) continue;
                     if (!SHARED) {
 #pragma unroll
                         for (int e = 0; e < 16; ++e) {
-                            const uint32_t wd = u4get(cc[g][s][e >> 3], (e & 7) >> 1);
+                            const uint32_t wd = u4get(cc[gi][s][e >> 3], (e & 7) >> 1);
                             col[e * 64] = (e & 1) ? h2f_hi(wd) : h2f_lo(wd);
                         }
                     }
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
-                        const uint32_t wd = u4get(wc[g][s], d);
+                        const uint32_t wd = u4get(wc[gi][s], d);
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
                             const uint32_t e = (wd >> (4 * j)) & 0xfu;
-                            acc[g] = fmaf(col[e * 64], xr[s][8 * d + j], acc[g]);
+                            acc[gi] = fmaf(col[e * 64], xr[s][8 * d + j], acc[gi]);
                         }
                     }
                 }
             }
 #pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                const float v = group_sum<64>(acc[g]);
-                if (lane == 0 && r + g < r1) y[(int64_t)t * M + r + g] = v;
+            for (int gi = 0; gi < RG; ++gi) {
+                const float v = group_sum<64>(acc[gi]);
+                if (lane == 0 && rr + gi < r1) y[(int64_t)t * M + rr + gi] = v;
             }
             if (more) {
 #pragma unroll
-                for (int g = 0; g < RG; ++g)
+                for (int gi = 0; gi < RG; ++gi)
 #pragma unroll
                     for (int s = 0; s < NSEG; ++s) {
-                        wc[g][s] = wn[g][s];
-                        cc[g][s][0] = cn[g][s][0];
-                        cc[g][s][1] = cn[g][s][1];
+                        wc[gi][s] = wn[gi][s];
+                        cc[gi][s][0] = cn[gi][s][0];
+                        cc[gi][s][1] = cn[gi][s][1];
                     }
             }
         }
     }
 }
 
-// Generic OIL4: one wave per output.  Weight row r starts at byte
-// (r*K)/2 (the reference's `((m*N+n)*K)/2`), element k uses nibble k%2 of
-// byte k/2 of that row.  Codebook: shared (cb_block == 0) or per block of
-// row r (codebooks of row r at cbs + r*(K/cb_block)*16).
+// Generic OIL4: one wave per output.  Weight row r starts at byte (r*K)/2
+// (the reference's `((m*N+n)*K)/2`), element k uses nibble k%2 of byte k/2 of
+// that row.  Codebook: shared (cb_block == 0) or per block of row r.
 __global__ __launch_bounds__(kWG) void oil4_generic(
     const uint8_t* __restrict__ nib, const uint16_t* __restrict__ cbs, int64_t cb_block,
     const float* __restrict__ act, float* __restrict__ out, int64_t R, int64_t K, int64_t xmod,
@@ -280,13 +442,21 @@ __global__ __launch_bounds__(kWG) void oil4_generic(
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Rows per wave: enough waves for >= 2 workgroups per CU on 256 CUs, at
-// least RG rows each.
 inline int pick_rows_per_wave(int64_t M, int rg) {
     const int64_t target_waves = 256 * 2 * kWaves;
     int64_t rpw = (M + target_waves - 1) / target_waves;
     rpw = ((rpw + rg - 1) / rg) * rg;
     return (int)(rpw < rg ? rg : rpw);
+}
+
+template <int NW, int NC>
+void run_oil4_mfma(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y, int64_t M,
+                   int64_t K, hipStream_t s) {
+    const int grid = ceil_div(M, 16);
+    if (cb_block == 0)
+        oil4_gemv_mfma<NW, NC, true><<<grid, NW * 64, 0, s>>>(nib, cbs, 0, x, y, (int)M, (int)K);
+    else
+        oil4_gemv_mfma<NW, NC, false><<<grid, NW * 64, 0, s>>>(nib, cbs, (int)cb_block, x, y, (int)M, (int)K);
 }
 
 }  // namespace
@@ -295,18 +465,8 @@ hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x,
                             int64_t M, int64_t K, int64_t batch, hipStream_t s) {
     const bool fast = (K % 16 == 0) && K <= 4096 && M < (1ll << 31) && aligned16(idx) && aligned16(x);
     if (fast) {
-        constexpr int RG = 2;
-        const int rpw = pick_rows_per_wave(M, RG);
-        const int grid = ceil_div(ceil_div(M, rpw), kWaves);
-        const int nseg = (int)(K / 16);
-        if (nseg <= 64)
-            oil8_gemv_fast<1, RG><<<grid, kWG, 0, s>>>(idx, cb, x, y, (int)M, (int)K, (int)batch, rpw);
-        else if (nseg <= 128)
-            oil8_gemv_fast<2, RG><<<grid, kWG, 0, s>>>(idx, cb, x, y, (int)M, (int)K, (int)batch, rpw);
-        else if (nseg <= 192)
-            oil8_gemv_fast<3, RG><<<grid, kWG, 0, s>>>(idx, cb, x, y, (int)M, (int)K, (int)batch, rpw);
-        else
-            oil8_gemv_fast<4, RG><<<grid, kWG, 0, s>>>(idx, cb, x, y, (int)M, (int)K, (int)batch, rpw);
+        constexpr int R = 4;
+        oil8_gemv_k<R><<<ceil_div(M, R), kWG, 0, s>>>(idx, cb, x, y, (int)M, (int)K, (int)batch);
     } else {
         oil8_generic<<<ceil_div(M, kWaves), kWG, 0, s>>>(idx, cb, x, y, M, K, 1, batch, M);
     }
@@ -324,9 +484,22 @@ hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float*
 hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block,
                             const float* x, float* y, int64_t M, int64_t K, int64_t batch,
                             hipStream_t s) {
-    const bool fast = (K % 32 == 0) && K <= 4096 && M < (1ll << 31) && aligned16(nib) && aligned16(x) &&
-                      aligned16(cbs) && (cb_block == 0 || cb_block % 32 == 0);
-    if (fast) {
+    const bool aligned = aligned16(nib) && aligned16(x) && aligned16(cbs);
+    const bool mfma = batch == 1 && aligned && M < (1ll << 31) && (cb_block == 0 || cb_block % 128 == 0) &&
+                      (K == 512 || K == 1024 || K == 2048 || K == 4096);
+    if (mfma) {
+        // K split over the waves of a workgroup: 8 waves (K/8 columns each)
+        // for the long rows, so that ~5 waves per SIMD are in flight
+        switch (K) {
+            case 512: run_oil4_mfma<4, 1>(nib, cbs, cb_block, x, y, M, K, s); break;
+            case 1024: run_oil4_mfma<8, 1>(nib, cbs, cb_block, x, y, M, K, s); break;
+            case 2048: run_oil4_mfma<8, 2>(nib, cbs, cb_block, x, y, M, K, s); break;
+            default: run_oil4_mfma<8, 4>(nib, cbs, cb_block, x, y, M, K, s); break;
+        }
+        return hipGetLastError();
+    }
+    const bool valu = (K % 32 == 0) && K <= 4096 && M < (1ll << 31) && aligned && (cb_block == 0 || cb_block % 32 == 0);
+    if (valu) {
         constexpr int RG = 2;
         const int rpw = pick_rows_per_wave(M, RG);
         const int grid = ceil_div(ceil_div(M, rpw), kWaves);
@@ -334,14 +507,14 @@ hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_
         const int blk = (int)cb_block;
         if (cb_block == 0) {
             if (nseg <= 64)
-                oil4_gemv_fast<1, RG, true><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
+                oil4_gemv_valu<1, RG, true><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
             else
-                oil4_gemv_fast<2, RG, true><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
+                oil4_gemv_valu<2, RG, true><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
         } else {
             if (nseg <= 64)
-                oil4_gemv_fast<1, RG, false><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
+                oil4_gemv_valu<1, RG, false><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
             else
-                oil4_gemv_fast<2, RG, false><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
+                oil4_gemv_valu<2, RG, false><<<grid, kWG, 0, s>>>(nib, cbs, blk, x, y, (int)M, (int)K, (int)batch, rpw);
         }
     } else {
         oil4_generic<<<ceil_div(M, kWaves), kWG, 0, s>>>(nib, cbs, cb_block, x, y, M, K, 1, batch, M);

@@ -82,34 +82,79 @@ __device__ __forceinline__ int tdot16(uint32_t w, const uint32_t (&A)[4], int ac
 // Fast I2_S GEMV.  Requires K % 64 == 0, K <= 64*LPR*NSEG, 16-byte aligned
 // packed weights.  Dynamic LDS: K bytes of quantised activations.
 // ---------------------------------------------------------------------------
+// Workgroup = 4 waves x (64/LPR) rows; the weight loads are released once
+// the activations are in (see below) and stay in registers over the tokens
+// of a batch.
 template <int LPR, int NSEG, bool FUSED>
 __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
-    const uint8_t* __restrict__ packed, float w_scale, const float* __restrict__ x,
+    const uint8_t* packed, float w_scale, const float* __restrict__ x,
     const int8_t* __restrict__ act, const float* __restrict__ act_scale, float* __restrict__ y,
-    int M, int K, int batch, int rows_per_wave) {
+    int M, int K, int batch) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     int8_t* q = (int8_t*)lds_raw;
     __shared__ float red[kWaves];
-    constexpr int RPP = MTH_WAVE / LPR;  // rows per pass of the wave
+    constexpr int RPP = MTH_WAVE / LPR;          // rows per wave
+    constexpr int XQ = (64 * LPR * NSEG) / 1024;  // float4 of x per thread (K <= 64*LPR*NSEG)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane % LPR, ro = lane / LPR;
     const int bpr = K >> 2;        // bytes per row
     const int nseg = bpr >> 4;     // 16-byte segments per row
-    const int r0 = (blockIdx.x * kWaves + wave) * rows_per_wave;
-    const int r1 = min(M, r0 + rows_per_wave);
+    const int row = (blockIdx.x * kWaves + wave) * RPP + ro;
+    const bool rv = row < M;
+
+    // The token's activations are fetched (and reduced) before the weight
+    // stream is released: a load issued after other waves' weight loads waits
+    // behind them in the CU's in-order memory pipeline.  Weight loads are
+    // unconditional (clamped addresses); out-of-row segments get the padding
+    // code at use.  packed is not __restrict__, so the loads stay below the
+    // first barrier.
+    float4 xr[XQ];
+    if (FUSED) {
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int k = (tid + j * kWG) * 4;
+            xr[j] = ldf4(x + (k < K ? k : 0));
+        }
+    }
+    uint4 w[NSEG];
+    auto issue_w = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < NSEG; ++s) {
+            const int seg = li + LPR * s;
+            w[s] = ld_stream(packed + (int64_t)min(row, M - 1) * bpr + (int64_t)min(seg, nseg - 1) * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
     for (int t = 0; t < batch; ++t) {
         float inv;
         if (FUSED) {
             const float* xt = x + (int64_t)t * K;
-            const float mx = block_absmax(xt, K, red);
+            float m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < XQ; ++j) {
+                const int k = (tid + j * kWG) * 4;
+                if (t > 0) xr[j] = ldf4(xt + (k < K ? k : 0));
+                if (k >= K) xr[j] = make_float4(0, 0, 0, 0);
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(xr[j].x), fabsf(xr[j].y)), fmaxf(fabsf(xr[j].z), fabsf(xr[j].w))));
+            }
+            m = wave_max(m);
+            if (lane == 0) red[wave] = m;
+            __syncthreads();
+            if (t == 0) issue_w();
+            float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+            if (mx < 1e-10f) mx = 1e-10f;
             const float sc = __fdiv_rn(127.0f, mx);
             inv = __fdiv_rn(mx, 127.0f);
-            for (int k = tid * 4; k < K; k += kWG * 4) {
-                const float4 v = ldf4(xt + k);
-                const uint32_t b0 = (uint32_t)quant_i8(v.x, sc) & 0xffu, b1 = (uint32_t)quant_i8(v.y, sc) & 0xffu;
-                const uint32_t b2 = (uint32_t)quant_i8(v.z, sc) & 0xffu, b3 = (uint32_t)quant_i8(v.w, sc) & 0xffu;
-                *(uint32_t*)(q + k) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+#pragma unroll
+            for (int j = 0; j < XQ; ++j) {
+                const int k = (tid + j * kWG) * 4;
+                if (k < K) {
+                    const uint32_t b0 = (uint32_t)quant_i8(xr[j].x, sc) & 0xffu, b1 = (uint32_t)quant_i8(xr[j].y, sc) & 0xffu;
+                    const uint32_t b2 = (uint32_t)quant_i8(xr[j].z, sc) & 0xffu, b3 = (uint32_t)quant_i8(xr[j].w, sc) & 0xffu;
+                    *(uint32_t*)(q + k) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                }
             }
         } else {
             inv = act_scale[t];
@@ -117,6 +162,7 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
             for (int k = tid * 16; k < K; k += kWG * 16) *(uint4*)(q + k) = ld16(at + k);
         }
         __syncthreads();
+        if (!FUSED && t == 0) issue_w();
 
         // lane's activations, transposed: A[s][d][j] byte b = a[seg*64 + 16d + 4b + j]
         uint32_t A[NSEG][4][4];
@@ -145,38 +191,21 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
         }
         __syncthreads();  // q may be overwritten by the next token
 
-        if (r0 < M) {
-            for (int rb = r0; rb < r1; rb += 2 * RPP) {
-                uint4 w[2][NSEG];
+        {
+            int acc = 0;
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int row = rb + h * RPP + ro;
-#pragma unroll
-                    for (int s = 0; s < NSEG; ++s) {
-                        const int seg = li + LPR * s;
-                        w[h][s] = (row < r1 && seg < nseg)
-                                      ? ld_stream(packed + (int64_t)row * bpr + (int64_t)seg * 16)
-                                      : make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int row = rb + h * RPP + ro;
-                    int acc = 0;
-#pragma unroll
-                    for (int s = 0; s < NSEG; ++s) {
-                        // padding code 01 (t = 0, u = 1) contributes u*a = a = 0 for
-                        // missing segments (A = 0 there)
-                        acc = tdot16(w[h][s].x, A[s][0], acc);
-                        acc = tdot16(w[h][s].y, A[s][1], acc);
-                        acc = tdot16(w[h][s].z, A[s][2], acc);
-                        acc = tdot16(w[h][s].w, A[s][3], acc);
-                    }
-                    acc = group_sum_i<LPR>(acc - asum);
-                    if (li == 0 && row < r1)
-                        y[(int64_t)t * M + row] = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
-                }
+            for (int s = 0; s < NSEG; ++s) {
+                // segments past the row (and clamped rows) use the padding code
+                // 01 (t = 0, u = 1), which meets A = 0: they contribute nothing
+                const bool sv = li + LPR * s < nseg;
+                const uint32_t pad = 0x55555555u;
+                acc = tdot16(sv ? w[s].x : pad, A[s][0], acc);
+                acc = tdot16(sv ? w[s].y : pad, A[s][1], acc);
+                acc = tdot16(sv ? w[s].z : pad, A[s][2], acc);
+                acc = tdot16(sv ? w[s].w : pad, A[s][3], acc);
             }
+            acc = group_sum_i<LPR>(acc - asum);
+            if (li == 0 && rv) y[(int64_t)t * M + row] = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
         }
     }
 }
@@ -338,18 +367,14 @@ template <int LPR, int NSEG>
 hipError_t run_i2s_fast(const uint8_t* packed, float w_scale, const float* x, const int8_t* act,
                         const float* act_scale, float* y, int64_t M, int64_t K, int64_t batch, hipStream_t s) {
     constexpr int RPP = MTH_WAVE / LPR;
-    // rows per wave: a multiple of 2*RPP, sized for >= 2 workgroups per CU
-    const int64_t target_waves = 256 * 2 * kWaves;
-    int64_t rpw = (M + target_waves - 1) / target_waves;
-    rpw = ((rpw + 2 * RPP - 1) / (2 * RPP)) * (2 * RPP);
-    const int grid = ceil_div(ceil_div(M, rpw), kWaves);
+    const int grid = ceil_div(M, RPP * kWaves);
     const size_t lds = (size_t)((K + 15) / 16) * 16;
     if (x)
         i2s_gemv_fast<LPR, NSEG, true><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M,
-                                                               (int)K, (int)batch, (int)rpw);
+                                                               (int)K, (int)batch);
     else
         i2s_gemv_fast<LPR, NSEG, false><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M,
-                                                                (int)K, (int)batch, (int)rpw);
+                                                                (int)K, (int)batch);
     return hipGetLastError();
 }
 
@@ -383,8 +408,9 @@ hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x,
     if (fast) {
         if (nseg <= 16) return run_i2s_fast<16, 1>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
         if (nseg <= 32) return run_i2s_fast<16, 2>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
-        if (nseg <= 64) return run_i2s_fast<16, 4>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
+        if (nseg <= 64) return run_i2s_fast<32, 2>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
         if (nseg <= 128) return run_i2s_fast<32, 4>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
+        if (nseg <= 192) return run_i2s_fast<64, 3>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
         return run_i2s_fast<64, 4>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
     }
     if (x)
