@@ -163,24 +163,35 @@ __global__ __launch_bounds__(kWG) void oil8_generic(
 // ===================================================================
 // OIL4, batch 1, matrix cores
 // ===================================================================
-// LDS codebook table of the workgroup: entry e of wave w, column c (0..31)
-// sits in the low half of the dword at byte
-//     ((e*NW/2 + w/2) << 8) | ((w & 1) << 7) | (c << 2),
-// so one v_perm_b32 builds the address from a nibble-spread byte that already
-// carries e*NW/2 + w/2 and a per-lane byte (w & 1)*128 + 4c.  Lanes l and
-// l+32 share a column and always read the same row's table; the two 32-lane
-// halves of a wave64 access are serviced separately, so no gather conflicts.
-template <int NW, int NC, bool SHARED>
+// LDS of oil4_gemv_mfma (byte offsets, one static array).  The codebook table
+// sits at offset 0, so a gather address is the v_perm result itself: entry e of
+// wave w, column c (0..31) is the low half of the dword at
+//     ((e*NW/2 + w/2) << 8) | ((w & 1) << 7) | (c << 2).
+// Lanes l and l+32 share a column and always read the same row's table; the
+// two 32-lane halves of a wave64 access are serviced separately, so gathers
+// never conflict.
+template <int NW, int NC>
+struct Oil4Lds {
+    static constexpr int KW = NC * 128;
+    static constexpr int tab = 0;
+    static constexpr int tab_bytes = 16 * NW * 128;
+    static constexpr int xf = tab_bytes;              // per wave: hi, lo, zero blocks of KW halves
+    static constexpr int xf_wave = 3 * KW * 2;
+    static constexpr int part = xf + NW * xf_wave;
+    static constexpr int bytes = part + NW * 16 * 4;
+};
+
+template <int NW, int NC, int PD, bool SHARED, bool CB128>
 __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, const uint16_t* cbs,
                                                           int cb_block, const float* __restrict__ x,
                                                           float* __restrict__ y, int M, int K) {
-    constexpr int KW = NC * 128;  // columns per wave
-    constexpr int HS = (NW == 8) ? 2 : 1;  // nibble shift that leaves room for w/2 in the index byte
-    __shared__ uint32_t tab[16 * NW * 32];
-    // per wave: B fragments of x_hi (column 0), x_lo (column 1), then a zero
-    // block read by the lanes of columns 2..15
-    __shared__ __align__(16) _Float16 xf[NW][3 * KW];
-    __shared__ float part[NW][16];
+    using L = Oil4Lds<NW, NC>;
+    constexpr int KW = L::KW;                  // columns per wave
+    constexpr int HS = (NW == 8) ? 2 : 1;      // nibble shift leaving room for w/2 in the index byte
+    constexpr int NMF = NC * 4;                // MFMAs per wave
+    __shared__ __align__(16) uint8_t lds[L::bytes];  // the kernel's only LDS object
+    _Float16* xf = (_Float16*)(lds + L::xf);
+    float* part = (float*)(lds + L::part);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int row = blockIdx.x * 16 + r;
@@ -201,22 +212,27 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+
+    // The stream is software-pipelined: chunk c + PD is issued before chunk c
+    // is consumed.
     uint2 wc[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int kc = k0 + c * 128;
-        const uint16_t* cp = SHARED ? cbs + 4 * g : cbs + ((int64_t)rowc * nb + kc / cb_block) * 16 + 4 * g;
-        wc[c] = *(const uint2*)cp;
-    }
-    __builtin_amdgcn_sched_barrier(0);
     uint4 wn[NC];
+    const uint16_t* cbrow = cbs + (int64_t)rowc * nb * 16 + 4 * g;
+    const uint8_t* nrow = nib + (int64_t)rowc * (K >> 1) + 16 * g;
+    auto issue = [&](int c) {
+        const int kc = k0 + c * 128;
+        const int blk = CB128 ? (kc >> 7) : kc / cb_block;
+        const uint16_t* cp = SHARED ? cbs + 4 * g : cbrow + blk * 16;
+        wc[c] = *(const uint2*)cp;
+        wn[c] = ld_stream(nrow + (kc >> 1));
+        __builtin_amdgcn_sched_barrier(0);
+    };
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-        wn[c] = ld_stream(nib + (int64_t)rowc * (K >> 1) + ((k0 + c * 128 + 32 * g) >> 1));
-    __builtin_amdgcn_sched_barrier(0);
+    for (int c = 0; c < (PD < NC ? PD : NC); ++c) issue(c);
 
     // x slice of this wave -> power-of-two scale -> FP16 hi/lo B fragments
     // (wave-private LDS: only the wave's own program order matters)
+    _Float16* xw = xf + wave * 3 * KW;
     float xv[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -243,60 +259,76 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
                 hi[v] = h;
                 lo[v] = (_Float16)(xs - (float)h);
             }
-            *(half8*)&xf[wave][((c * 4 + i) * 4 + gg) * 8] = hi;
-            *(half8*)&xf[wave][(((NC + c) * 4 + i) * 4 + gg) * 8] = lo;
+            *(half8*)&xw[((c * 4 + i) * 4 + gg) * 8] = hi;
+            *(half8*)&xw[(((NC + c) * 4 + i) * 4 + gg) * 8] = lo;
         }
     }
-    for (int z = lane * 8; z < KW; z += 64 * 8) *(half8*)&xf[wave][2 * KW + z] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int z = lane * 8; z < KW; z += 64 * 8) *(half8*)&xw[2 * KW + z] = half8{0, 0, 0, 0, 0, 0, 0, 0};
     wave_lds_order();
 
     const int n = lane & 15;
     const uint32_t col4 = ((uint32_t)(wave & 1) << 7) | ((uint32_t)(lane & 31) << 2);
     const uint32_t wmask = 0x01010101u * (uint32_t)(wave >> 1);
-    uint16_t* tw = (uint16_t*)tab;
-    const char* tr = (const char*)tab;
-    // B fragment of MFMA (c, i) for this lane: column n's block at byte
-    // offset (c*4 + i)*64 from its base; columns >= 2 read the zero block
-    const char* xb = (const char*)&xf[wave][(n < 2 ? n : 2) * KW] + g * 16;
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
+    uint32_t* tab = (uint32_t*)lds;
+    // B fragment of MFMA m = c*4 + i: column n's block at byte offset m*64;
+    // columns >= 2 read the zero block
+    const int xb = L::xf + wave * L::xf_wave + (n < 2 ? n : 2) * KW * 2 + g * 16;
+
+    auto write_table = [&](int c) {
         // row r's entries 4g..4g+3 into columns r and r+16 (fp16 in the low half)
-        const uint32_t e2[2] = {wc[c].x, wc[c].y};
+        const uint32_t ev[4] = {wc[c].x, wc[c].x >> 16, wc[c].y, wc[c].y >> 16};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint16_t h = (uint16_t)(e2[j >> 1] >> (16 * (j & 1)));
-            const int slot = (((4 * g + j) * (NW / 2) + (wave >> 1)) * 64) + (wave & 1) * 32;
-            tw[(slot + r) * 2] = h;
-            tw[(slot + r + 16) * 2] = h;
+            const int slot = ((4 * g + j) * (NW / 2) + (wave >> 1)) * 64 + (wave & 1) * 32;
+            tab[slot + r] = ev[j];
+            tab[slot + r + 16] = ev[j];
         }
         wave_lds_order();
+    };
+    struct Frag { half8 a, b; };
+    auto gather = [&](int m) {
+        const int c = m >> 2, i = m & 3;
+        const uint32_t d = u4get(wn[c], i);
+        // index bytes e*NW/2 + wave/2 for the even (low) and odd (high) nibbles
+        const uint32_t lo4 = ((d << HS) & (0x0f0f0f0fu << HS)) | wmask;
+        const uint32_t hi4 = ((d >> (4 - HS)) & (0x0f0f0f0fu << HS)) | wmask;
+        Frag f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t d = u4get(wn[c], i);
-            // index bytes e*NW/2 + wave/2 for the even (low) and odd (high) nibbles
-            const uint32_t lo4 = ((d << HS) & (0x0f0f0f0fu << HS)) | wmask;
-            const uint32_t hi4 = ((d >> (4 - HS)) & (0x0f0f0f0fu << HS)) | wmask;
-            half8 a;
+        for (int v = 0; v < 8; ++v) f.a[v] = *(const _Float16*)(lds + perm_addr((v & 1) ? hi4 : lo4, col4, v >> 1));
+        f.b = *(const half8*)(lds + xb + m * 64);
+        return f;
+    };
+
+    // Software-pipelined in source order: the gathers of MFMA m+1 are issued
+    // before MFMA m consumes its operands (the compiler tracks the waits).
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    write_table(0);
+    Frag cur = gather(0);
 #pragma unroll
-            for (int v = 0; v < 8; ++v)
-                a[v] = *(const _Float16*)(tr + perm_addr((v & 1) ? hi4 : lo4, col4, v >> 1));
-            const half8 b = *(const half8*)(xb + (c * 4 + i) * 64);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    for (int m = 0; m < NMF; ++m) {
+        Frag nxt;
+        if (m + 1 < NMF) {
+            if (((m + 1) & 3) == 0) {  // next chunk: prefetch, then its table
+                const int c1 = (m + 1) >> 2;
+                if (c1 + PD - 1 < NC) issue(c1 + PD - 1);
+                write_table(c1);
+            }
+            nxt = gather(m + 1);
         }
-        wave_lds_order();
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.a, cur.b, acc, 0, 0, 0);
+        if (m + 1 < NMF) cur = nxt;
     }
     // D[4g+i][n]: rows' hi (n = 0) + lo (n = 1) parts
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float s = acc[i] + __shfl_xor(acc[i], 1, MTH_WAVE);
-        if (n == 0) part[wave][4 * g + i] = ldexpf(s, -sh);
+        if (n == 0) part[wave * 16 + 4 * g + i] = ldexpf(s, -sh);
     }
     __syncthreads();
     if (tid < 16 && blockIdx.x * 16 + tid < M) {
-        float sum = part[0][tid];
+        float sum = part[tid];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) sum += part[w][tid];
+        for (int w = 1; w < NW; ++w) sum += part[w * 16 + tid];
         y[blockIdx.x * 16 + tid] = sum;
     }
 }
@@ -449,14 +481,24 @@ inline int pick_rows_per_wave(int64_t M, int rg) {
     return (int)(rpw < rg ? rg : rpw);
 }
 
+#ifndef MTH_OIL4_NW
+#define MTH_OIL4_NW 4
+#endif
+#ifndef MTH_OIL4_PD
+#define MTH_OIL4_PD 2
+#endif
 template <int NW, int NC>
 void run_oil4_mfma(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y, int64_t M,
                    int64_t K, hipStream_t s) {
+    constexpr int PD = MTH_OIL4_PD;  // chunks in flight per wave
     const int grid = ceil_div(M, 16);
     if (cb_block == 0)
-        oil4_gemv_mfma<NW, NC, true><<<grid, NW * 64, 0, s>>>(nib, cbs, 0, x, y, (int)M, (int)K);
+        oil4_gemv_mfma<NW, NC, PD, true, false><<<grid, NW * 64, 0, s>>>(nib, cbs, 0, x, y, (int)M, (int)K);
+    else if (cb_block == 128)
+        oil4_gemv_mfma<NW, NC, PD, false, true><<<grid, NW * 64, 0, s>>>(nib, cbs, 128, x, y, (int)M, (int)K);
     else
-        oil4_gemv_mfma<NW, NC, false><<<grid, NW * 64, 0, s>>>(nib, cbs, (int)cb_block, x, y, (int)M, (int)K);
+        oil4_gemv_mfma<NW, NC, PD, false, false><<<grid, NW * 64, 0, s>>>(nib, cbs, (int)cb_block, x, y, (int)M,
+                                                                        (int)K);
 }
 
 }  // namespace
@@ -494,7 +536,7 @@ hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_
             case 512: run_oil4_mfma<4, 1>(nib, cbs, cb_block, x, y, M, K, s); break;
             case 1024: run_oil4_mfma<8, 1>(nib, cbs, cb_block, x, y, M, K, s); break;
             case 2048: run_oil4_mfma<8, 2>(nib, cbs, cb_block, x, y, M, K, s); break;
-            default: run_oil4_mfma<8, 4>(nib, cbs, cb_block, x, y, M, K, s); break;
+            default: run_oil4_mfma<MTH_OIL4_NW, 4096 / (128 * MTH_OIL4_NW)>(nib, cbs, cb_block, x, y, M, K, s); break;
         }
         return hipGetLastError();
     }
