@@ -3,8 +3,9 @@
 // Replaces the CPU loops of src/kernel_oil8.cpp:14-71 and
 // src/kernel_oil4.cpp:31-125 (reference semantics: sum_k cb[idx]*x[k] in FP32
 // with the codebook value exact in FP32).  Weights stay in the reference's
-// row-major layout; every kernel issues its weight loads first, so HBM latency
-// overlaps the codebook staging.
+// row-major layout.  The CU's memory pipeline returns loads in issue order, so
+// the small operands every wave needs first (x, the codebook) are issued
+// before the weight stream and the stream itself is software-pipelined.
 //
 // OIL8 (oil8_gemv_k):
 //   * workgroup = 4 waves x R rows; wave w owns columns [1024w, 1024w+1024),
@@ -28,6 +29,8 @@
 //   * x is split per wave into FP16 hi + lo parts after a power-of-two scale
 //     (x*2^s = hi + lo + O(2^-22)), placed as B columns 0 and 1, so
 //     D[:,0] + D[:,1] is the FP32 dot product; products are exact, sums FP32.
+//     Only the 8 lanes holding columns 0 and 1 read B from LDS; the other
+//     columns hold don't-care values and their outputs are discarded.
 // Other shapes (K not a multiple of 16/512, K > 4096, unaligned pointers,
 // batched OIL4, codebook blocks that are not multiples of 128, the
 // reference's per-(m,n) indexing) run on oil4_gemv_valu or the generic
@@ -175,8 +178,12 @@ struct Oil4Lds {
     static constexpr int KW = NC * 128;
     static constexpr int tab = 0;
     static constexpr int tab_bytes = 16 * NW * 128;
-    static constexpr int xf = tab_bytes;              // per wave: hi, lo, zero blocks of KW halves
-    static constexpr int xf_wave = 3 * KW * 2;
+    // per wave: the hi block (KW halves), 64 bytes of skew, the lo block.  The
+    // skew puts hi and lo of one k-group on different banks, so the 8 lanes
+    // that read B (columns 0 and 1 of 4 k-groups) hit 32 distinct banks.
+    static constexpr int xf = tab_bytes;
+    static constexpr int lo_off = KW * 2 + 64;
+    static constexpr int xf_wave = lo_off + KW * 2;
     static constexpr int part = xf + NW * xf_wave;
     static constexpr int bytes = part + NW * 16 * 4;
 };
@@ -232,7 +239,7 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
 
     // x slice of this wave -> power-of-two scale -> FP16 hi/lo B fragments
     // (wave-private LDS: only the wave's own program order matters)
-    _Float16* xw = xf + wave * 3 * KW;
+    _Float16* xw = xf + wave * (L::xf_wave / 2);
     float xv[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -260,10 +267,9 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
                 lo[v] = (_Float16)(xs - (float)h);
             }
             *(half8*)&xw[((c * 4 + i) * 4 + gg) * 8] = hi;
-            *(half8*)&xw[(((NC + c) * 4 + i) * 4 + gg) * 8] = lo;
+            *(half8*)&xw[L::lo_off / 2 + ((c * 4 + i) * 4 + gg) * 8] = lo;
         }
     }
-    for (int z = lane * 8; z < KW; z += 64 * 8) *(half8*)&xw[2 * KW + z] = half8{0, 0, 0, 0, 0, 0, 0, 0};
     wave_lds_order();
 
     const int n = lane & 15;
@@ -271,17 +277,20 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
     const uint32_t wmask = 0x01010101u * (uint32_t)(wave >> 1);
     uint32_t* tab = (uint32_t*)lds;
     // B fragment of MFMA m = c*4 + i: column n's block at byte offset m*64;
-    // columns >= 2 read the zero block
-    const int xb = L::xf + wave * L::xf_wave + (n < 2 ? n : 2) * KW * 2 + g * 16;
+    // columns >= 2 are zero and only lanes n < 2 read LDS
+    const int xb = L::xf + wave * L::xf_wave + (n == 1 ? L::lo_off : 0) + g * 16;
 
     auto write_table = [&](int c) {
-        // row r's entries 4g..4g+3 into columns r and r+16 (fp16 in the low half)
+        // row r's entries 4g..4g+3 into columns r and r+16 (fp16 in the low
+        // half).  Lanes of odd g write the two copies in the opposite order,
+        // so the two k-groups of a 32-lane half store to different banks.
         const uint32_t ev[4] = {wc[c].x, wc[c].x >> 16, wc[c].y, wc[c].y >> 16};
+        const int c0 = r + 16 * (g & 1), c1 = r + 16 * (~g & 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int slot = ((4 * g + j) * (NW / 2) + (wave >> 1)) * 64 + (wave & 1) * 32;
-            tab[slot + r] = ev[j];
-            tab[slot + r + 16] = ev[j];
+            tab[slot + c0] = ev[j];
+            tab[slot + c1] = ev[j];
         }
         wave_lds_order();
     };
@@ -295,7 +304,11 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
         Frag f;
 #pragma unroll
         for (int v = 0; v < 8; ++v) f.a[v] = *(const _Float16*)(lds + perm_addr((v & 1) ? hi4 : lo4, col4, v >> 1));
-        f.b = *(const half8*)(lds + xb + m * 64);
+        // D column n depends on B column n only, so the unused columns may
+        // hold any value: lanes n >= 2 skip the read and keep stale registers.
+        half8 b = __builtin_nondeterministic_value(b);
+        if (n < 2) b = *(const half8*)(lds + xb + m * 64);
+        f.b = b;
         return f;
     };
 

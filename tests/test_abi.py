@@ -1,0 +1,111 @@
+"""The drop-in boundary without a GPU: libmythos_oil.so loads and exports
+exactly the entry points include/mythos_oil.h declares, each rejects invalid
+arguments with MTH_EINVAL and a message before touching the device, and
+libmythos_host.so exports the reference's oil::kernel signatures
+(include/oil/kernel.h:13-65 of the reference).  The GPU half of the façade is
+in test_gpu_facade.py.
+"""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "mythos.cpp_amd")
+HDR = os.path.join(ROOT, "include", "mythos_oil.h")
+
+
+def declared():
+    src = open(HDR).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mth_[a-z0-9_]+)\s*\(", src)))
+
+
+def dynsyms(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True, text=True).stdout
+    return {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+
+
+def test_header_matches_exports(mth):
+    decl = declared()
+    assert decl == sorted(mth.EXPORTS)
+    syms = dynsyms(mth.LIB_PATH)
+    missing = [d for d in decl if d not in syms]
+    assert not missing, missing
+    extra = sorted(s for s in syms if s.startswith("mth_") and s not in decl)
+    assert not extra, f"exported but undeclared: {extra}"
+    for d in decl:                       # resolvable through the loader too
+        assert getattr(mth.lib, d) is not None
+
+
+def test_version(mth):
+    assert mth.version() >> 16 == 1
+
+
+NULL = None
+# (entry point, arguments with a null pointer, arguments with a bad size)
+P = C.c_void_p(16)   # never dereferenced: validation fails first
+CASES = [
+    ("mth_oil8_gemm", (NULL, P, P, P, 4, 1, 4, NULL), (P, P, P, P, 0, 1, 4, NULL)),
+    ("mth_oil8_gemv", (P, NULL, P, P, 4, 4, 1, NULL), (P, P, P, P, 4, -1, 1, NULL)),
+    ("mth_oil4_gemm", (P, P, NULL, P, 4, 1, 4, NULL), (P, P, P, P, 4, 1, 0, NULL)),
+    ("mth_oil4_gemv", (P, P, 128, NULL, P, 4, 128, 1, NULL), (P, P, 100, P, P, 4, 128, 1, NULL)),
+    ("mth_oil4_gemm_prefill", (P, P, P, 128, NULL, 4, 4, 128, NULL), (P, P, P, 128, P, 4, 4, 100, NULL)),
+    ("mth_quantize_per_token", (NULL, P, P, P, 1, 4, NULL), (P, P, P, P, 0, 4, NULL)),
+    ("mth_dequantize_per_tensor", (NULL, P, 4, C.c_float(1.0), NULL), (P, P, -4, C.c_float(1.0), NULL)),
+    ("mth_i2s_gemv", (P, C.c_float(1.0), P, NULL, P, 4, 8, 1, NULL), (P, C.c_float(1.0), P, P, P, 4, 6, 1, NULL)),
+    ("mth_i2s_gemv_f32", (NULL, C.c_float(1.0), P, P, 4, 8, 1, NULL), (P, C.c_float(1.0), P, P, 4, 10, 1, NULL)),
+    ("mth_i2s_gemm", (P, NULL, P, 4, 1, 8, NULL), (P, P, P, 4, 1, 0, NULL)),
+    ("mth_i2s_gemm_vnni", (P, P, NULL, 4, 1, 8, NULL), (P, P, P, -4, 1, 8, NULL)),
+    ("mth_tl1_gemm", (NULL, P, P, 4, 1, 8, NULL), (P, P, P, 4, 0, 8, NULL)),
+    ("mth_tl2_gemm", (P, NULL, P, 4, 1, 6, NULL), (P, P, P, 4, 1, 8, NULL)),
+    ("mth_tl_precompute_lut", (NULL, P, 6, 3, NULL), (P, P, 6, 4, NULL)),
+]
+
+
+@pytest.mark.parametrize("name,nullargs,badargs", CASES, ids=[c[0] for c in CASES])
+def test_invalid_arguments_rejected(mth, name, nullargs, badargs):
+    f = getattr(mth.lib, name)
+    for args in (nullargs, badargs):
+        rc = f(*args)
+        assert rc == mth.MTH_EINVAL, (name, args, rc)
+        msg = mth.last_error()
+        assert msg.startswith(name), msg
+    # the message stays readable until the calling thread's next call
+    assert mth.last_error().startswith(name)
+
+
+def test_errors_raise_in_wrapper(mth):
+    with pytest.raises(TypeError):
+        mth.oil8_gemv(None, None, None, None, 4, 4)
+
+
+# Reference signatures (include/oil/kernel.h:13-65) the façade must export,
+# demangled; Tensor-based ones take oil::Tensor exactly as the reference.
+FACADE = [
+    "oil::kernel::i2s_gemm(oil::Tensor const&, oil::Tensor const&, oil::Tensor&, int, int, int)",
+    "oil::kernel::i2s_gemv(unsigned char const*, float, signed char const*, float, float*, int)",
+    "oil::kernel::tl1_gemm(oil::Tensor const&, oil::Tensor const&, oil::Tensor&, int, int, int)",
+    "oil::kernel::tl1_precompute_lut(signed char const*, signed char*, int, float)",
+    "oil::kernel::tl2_gemm(oil::Tensor const&, oil::Tensor const&, oil::Tensor&, int, int, int)",
+    "oil::kernel::tl2_precompute_lut(signed char const*, signed char*, int, float)",
+    "oil::kernel::oil8_gemm(unsigned char const*, float const*, float const*, float*, int, int, int)",
+    "oil::kernel::oil4_gemm(unsigned char const*, unsigned short const*, float const*, float*, int, int, int)",
+    "oil::kernel::i2s_gemm_avx2(oil::Tensor const&, oil::Tensor const&, oil::Tensor&, int, int, int)",
+    "oil::kernel::i2s_gemm_vnni(unsigned char const*, signed char const*, float*, int, int, int)",
+    # src/int8_quant.cpp:8-41 / include/oil/int8_quant.h:7-28
+    "oil::quantize_per_token(float const*, signed char*, long, long)",
+    "oil::quantize_per_tensor(float const*, signed char*, long)",
+    "oil::dequantize_per_tensor(signed char const*, float*, long, float)",
+]
+
+
+def test_facade_exports_reference_signatures(mth):
+    path = mth.HOST_LIB_PATH
+    assert os.path.exists(path), "libmythos_host.so not built"
+    out = subprocess.run(["nm", "-DC", "--defined-only", path], check=True, capture_output=True, text=True).stdout
+    have = {ln.split(None, 2)[2] for ln in out.splitlines() if len(ln.split(None, 2)) == 3}
+    missing = [s for s in FACADE if s not in have]
+    assert not missing, missing
