@@ -13,10 +13,12 @@
 //     0 until some i2s_gemm* call has run);
 //   * i2s_gemm_vnni computes its documented body (the as-built reference
 //     compiles an empty stub);
-//   * tl2_gemm requires K % 3 == 0 (the reference reads out of bounds else).
-// Dense FP32 helpers of the reference header (scalar_gemm, tiled_gemm,
-// avx2_gemm, avx2_tiled_gemm) are not on the quantized path and are not
-// provided here.
+//   * tl2_gemm requires K % 3 == 0 (the reference reads out of bounds else);
+//   * the dense FP32 helpers (scalar_gemm, tiled_gemm, avx2_gemm,
+//     avx2_tiled_gemm) all run one rocBLAS SGEMM, for any N (the reference's
+//     avx2_gemm needs N % 8 == 0).
+// Weight operands registered with oil::mi355x::register_weights
+// (oil/mi355x.h) stay resident on the device.
 #pragma once
 
 #include <cstdint>
@@ -45,6 +47,12 @@ void oil4_gemm(const uint8_t* packed_indices, const uint16_t* codebook, const fl
 void i2s_gemm_avx2(const Tensor& weights, const Tensor& activations, Tensor& output, int M, int N, int K);
 
 void i2s_gemm_vnni(const uint8_t* packed_w, const int8_t* activations, float* output, int M, int N, int K);
+
+// Dense FP32: C[M][N] = A[M][K] * B[K][N], row-major, C overwritten.
+void scalar_gemm(const float* A, const float* B, float* C, int M, int N, int K);
+void tiled_gemm(const float* A, const float* B, float* C, int M, int N, int K);
+void avx2_gemm(const float* A, const float* B, float* C, int M, int N, int K);
+void avx2_tiled_gemm(const float* A, const float* B, float* C, int M, int N, int K);
 
 // ---- extensions (no reference counterpart): the decode formats of the
 // BASELINE configs, host-pointer + synchronous like the functions above ----

@@ -5,17 +5,25 @@
 //
 // Each call stages its operands in a per-thread device arena (grown on
 // demand, never shrunk), copies inputs host->device, launches on the
-// thread's stream, copies outputs back and synchronises.  There is no CPU
-// code path: a missing or failing GPU raises oil::Error.
+// thread's stream, copies outputs back and synchronises.  Weight operands
+// that lie inside a range registered with oil::mi355x::register_weights are
+// read from their resident device copy instead of being copied.  There is no
+// CPU code path: a missing or failing GPU raises oil::Error.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "mythos_oil.h"
 #include "oil/int8_quant.h"
 #include "oil/kernel.h"
+#include "oil/mi355x.h"
 
 namespace oil {
 namespace {
@@ -27,11 +35,72 @@ void mth_check(int rc, const char* what) {
     if (rc != MTH_OK) throw Error(std::string(what) + ": " + mth_last_error());
 }
 
+// Resident weights: host range -> device copy.  Entries are shared_ptr so a
+// call that is using a copy keeps it alive across a concurrent unregister.
+struct Resident {
+    void* dev = nullptr;
+    size_t bytes = 0;
+    ~Resident() {
+        if (dev) (void)hipFree(dev);
+    }
+};
+
+class Registry {
+public:
+    void add(const void* host, size_t bytes) {
+        if (!host || !bytes) throw Error("register_weights: empty range");
+        auto r = std::make_shared<Resident>();
+        hip_check(hipMalloc(&r->dev, bytes), "register_weights: hipMalloc");
+        r->bytes = bytes;
+        hip_check(hipMemcpy(r->dev, host, bytes, hipMemcpyHostToDevice), "register_weights: hipMemcpy");
+        std::lock_guard<std::mutex> g(mu_);
+        const uintptr_t b = (uintptr_t)host;
+        // a new range replaces every registered range it overlaps
+        for (auto it = map_.begin(); it != map_.end();) {
+            const uintptr_t ob = it->first, oe = ob + it->second->bytes;
+            if (ob < b + bytes && b < oe) it = map_.erase(it);
+            else ++it;
+        }
+        map_[b] = std::move(r);
+    }
+    bool remove(const void* host) {
+        std::lock_guard<std::mutex> g(mu_);
+        return map_.erase((uintptr_t)host) > 0;
+    }
+    // Device address of [host, host+n) if one registered range holds all of it.
+    std::shared_ptr<Resident> find(const void* host, size_t n, const void** dev) const {
+        std::lock_guard<std::mutex> g(mu_);
+        const uintptr_t p = (uintptr_t)host;
+        auto it = map_.upper_bound(p);
+        if (it == map_.begin()) return nullptr;
+        --it;
+        if (p + n > it->first + it->second->bytes) return nullptr;
+        *dev = (const char*)it->second->dev + (p - it->first);
+        return it->second;
+    }
+    size_t total() const {
+        std::lock_guard<std::mutex> g(mu_);
+        size_t t = 0;
+        for (auto& kv : map_) t += kv.second->bytes;
+        return t;
+    }
+
+private:
+    mutable std::mutex mu_;
+    std::map<uintptr_t, std::shared_ptr<Resident>> map_;
+};
+
+Registry& registry() {
+    static Registry r;
+    return r;
+}
+
 // Per-thread device staging area.  carve() hands out 256-byte aligned slices
-// of one allocation; reset() starts a new call.
+// of one allocation; begin() starts a new call.
 class Arena {
 public:
     ~Arena() {
+        if (blas_) (void)rocblas_destroy_handle(blas_);
         if (base_) (void)hipFree(base_);
         if (stream_) (void)hipStreamDestroy(stream_);
     }
@@ -45,6 +114,7 @@ public:
             cap_ = bytes_needed;
         }
         off_ = 0;
+        held_.clear();
     }
     static size_t pad(size_t b) { return (b + 255) / 256 * 256; }
     void* carve(size_t bytes) {
@@ -57,16 +127,38 @@ public:
         if (n) hip_check(hipMemcpyAsync(d, host, n * sizeof(T), hipMemcpyHostToDevice, stream_), "hipMemcpy H2D");
         return d;
     }
+    // A weight operand: its resident copy when registered (held until the
+    // next begin()), else staged like any input.  Size the arena with
+    // P(bytes) for it either way.
+    template <typename T> const T* weights(const T* host, size_t n) {
+        const void* dev = nullptr;
+        auto r = registry().find(host, n * sizeof(T), &dev);
+        if (r) {
+            held_.push_back(std::move(r));
+            carve(n * sizeof(T));
+            return (const T*)dev;
+        }
+        return upload(host, n);
+    }
     template <typename T> void download(T* host, const T* dev, size_t n) {
         if (n) hip_check(hipMemcpyAsync(host, dev, n * sizeof(T), hipMemcpyDeviceToHost, stream_), "hipMemcpy D2H");
     }
     void sync() { hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize"); }
     mth_stream_t stream() const { return (mth_stream_t)stream_; }
+    rocblas_handle blas() {
+        if (!blas_) {
+            if (rocblas_create_handle(&blas_) != rocblas_status_success) throw Error("rocblas_create_handle failed");
+        }
+        if (rocblas_set_stream(blas_, stream_) != rocblas_status_success) throw Error("rocblas_set_stream failed");
+        return blas_;
+    }
 
 private:
     void* base_ = nullptr;
     size_t cap_ = 0, off_ = 0;
     hipStream_t stream_ = nullptr;
+    rocblas_handle blas_ = nullptr;
+    std::vector<std::shared_ptr<Resident>> held_;
 };
 
 Arena& arena() {
@@ -91,8 +183,8 @@ void oil8_gemm(const uint8_t* indices, const float* codebook, const float* activ
     const size_t R = (size_t)M * N, nw = R * K, na = (size_t)N * K;
     Arena& a = arena();
     a.begin(P(nw) + P(256 * 4) + P(na * 4) + P(R * 4));
-    const uint8_t* di = a.upload(indices, nw);
-    const float* dc = a.upload(codebook, 256);
+    const uint8_t* di = a.weights(indices, nw);
+    const float* dc = a.weights(codebook, 256);
     const float* dx = a.upload(activations, na);
     float* dy = (float*)a.carve(R * 4);
     mth_check(mth_oil8_gemm(di, dc, dx, dy, M, N, K, a.stream()), "oil8_gemm");
@@ -106,8 +198,8 @@ void oil4_gemm(const uint8_t* packed_indices, const uint16_t* codebook, const fl
     const size_t R = (size_t)M * N, nb = (R * (size_t)K + 1) / 2, na = (size_t)N * K;
     Arena& a = arena();
     a.begin(P(nb) + P(32) + P(na * 4) + P(R * 4));
-    const uint8_t* dp = a.upload(packed_indices, nb);
-    const uint16_t* dc = a.upload(codebook, 16);
+    const uint8_t* dp = a.weights(packed_indices, nb);
+    const uint16_t* dc = a.weights(codebook, 16);
     const float* dx = a.upload(activations, na);
     float* dy = (float*)a.carve(R * 4);
     mth_check(mth_oil4_gemm(dp, dc, dx, dy, M, N, K, a.stream()), "oil4_gemm");
@@ -119,7 +211,7 @@ void i2s_gemv(const uint8_t* packed_w, float w_scale, const int8_t* act, float a
     if (K <= 0 || K % 4) throw Error("i2s_gemv: K must be a positive multiple of 4");
     Arena& a = arena();
     a.begin(P(K / 4) + P(K) + P(4) + P(4));
-    const uint8_t* dw = a.upload(packed_w, (size_t)K / 4);
+    const uint8_t* dw = a.weights(packed_w, (size_t)K / 4);
     const int8_t* dq = a.upload(act, (size_t)K);
     const float* ds = a.upload(&act_scale, 1);
     float* dy = (float*)a.carve(4);
@@ -135,7 +227,7 @@ void i2s_gemm(const Tensor& weights, const Tensor& activations, Tensor& output, 
               "i2s_gemm: tensor too small");
     Arena& a = arena();
     a.begin(P(nw) + P(na * 4) + P(R * 4));
-    const uint8_t* dw = a.upload(weights.data<uint8_t>(), nw);
+    const uint8_t* dw = a.weights(weights.data<uint8_t>(), nw);
     const float* dx = a.upload(activations.data<float>(), na);
     float* dy = (float*)a.carve(R * 4);
     mth_check(mth_i2s_gemm(dw, dx, dy, M, N, K, a.stream()), "i2s_gemm");
@@ -154,7 +246,7 @@ void i2s_gemm_vnni(const uint8_t* packed_w, const int8_t* activations, float* ou
     const size_t nw = (size_t)M * (K / 4) + (K % 4 ? 1 : 0), na = (size_t)N * K, R = (size_t)M * N;
     Arena& a = arena();
     a.begin(P(nw) + P(na) + P(R * 4));
-    const uint8_t* dw = a.upload(packed_w, nw);
+    const uint8_t* dw = a.weights(packed_w, nw);
     const int8_t* dx = a.upload(activations, na);
     float* dy = (float*)a.carve(R * 4);
     mth_check(mth_i2s_gemm_vnni(dw, dx, dy, M, N, K, a.stream()), "i2s_gemm_vnni");
@@ -188,7 +280,7 @@ void tl2_gemm(const Tensor& weights, const Tensor& activations, Tensor& output, 
               "tl2_gemm: tensor too small");
     Arena& a = arena();
     a.begin(P(nw) + P(na * 4) + P(R * 4));
-    const uint8_t* dw = a.upload(weights.data<uint8_t>(), nw);
+    const uint8_t* dw = a.weights(weights.data<uint8_t>(), nw);
     const float* dx = a.upload(activations.data<float>(), na);
     float* dy = (float*)a.carve(R * 4);
     mth_check(mth_tl2_gemm(dw, dx, dy, M, N, K, a.stream()), "tl2_gemm");
@@ -229,8 +321,8 @@ void oil4_gemv_blocked(const uint8_t* packed, const uint16_t* codebooks, int cb_
     const size_t nb = (size_t)M * K / 2, nc = cb_block ? (size_t)M * (K / cb_block) * 16 : 16;
     Arena& a = arena();
     a.begin(P(nb) + P(nc * 2) + P((size_t)batch * K * 4) + P((size_t)batch * M * 4));
-    const uint8_t* dp = a.upload(packed, nb);
-    const uint16_t* dc = a.upload(codebooks, nc);
+    const uint8_t* dp = a.weights(packed, nb);
+    const uint16_t* dc = a.weights(codebooks, nc);
     const float* dx = a.upload(x, (size_t)batch * K);
     float* dy = (float*)a.carve((size_t)batch * M * 4);
     mth_check(mth_oil4_gemv(dp, dc, cb_block, dx, dy, M, K, batch, a.stream()), "oil4_gemv_blocked");
@@ -243,7 +335,7 @@ void i2s_gemv_f32(const uint8_t* packed, float w_scale, const float* x, float* y
     const size_t nw = (size_t)M * K / 4;
     Arena& a = arena();
     a.begin(P(nw) + P((size_t)batch * K * 4) + P((size_t)batch * M * 4));
-    const uint8_t* dw = a.upload(packed, nw);
+    const uint8_t* dw = a.weights(packed, nw);
     const float* dx = a.upload(x, (size_t)batch * K);
     float* dy = (float*)a.carve((size_t)batch * M * 4);
     mth_check(mth_i2s_gemv_f32(dw, w_scale, dx, dy, M, K, batch, a.stream()), "i2s_gemv_f32");
@@ -251,7 +343,49 @@ void i2s_gemv_f32(const uint8_t* packed, float w_scale, const float* x, float* y
     a.sync();
 }
 
+// ---- dense FP32 GEMMs of the same header (src/kernel_i2s.cpp:67-154,236-246)
+// C[M][N] = A[M][K] * B[K][N], row-major, C overwritten.  The reference keeps
+// four loop orders of one product; all four run as one rocBLAS SGEMM here
+// (row-major C = A*B is column-major C^T = B^T * A^T).
+namespace {
+void dense_gemm(const float* A, const float* B, float* C, int M, int N, int K, const char* what) {
+    check_dims(M, N, K, what);
+    const size_t na = (size_t)M * K, nb = (size_t)K * N, nc = (size_t)M * N;
+    Arena& a = arena();
+    a.begin(P(na * 4) + P(nb * 4) + P(nc * 4));
+    const float* dA = a.weights(A, na);
+    const float* dB = a.weights(B, nb);
+    float* dC = (float*)a.carve(nc * 4);
+    const float one = 1.0f, zero = 0.0f;
+    if (rocblas_sgemm(a.blas(), rocblas_operation_none, rocblas_operation_none, N, M, K, &one, dB, N, dA, K, &zero,
+                      dC, N) != rocblas_status_success)
+        throw Error(std::string(what) + ": rocblas_sgemm failed");
+    a.download(C, dC, nc);
+    a.sync();
+}
+}  // namespace
+
+void scalar_gemm(const float* A, const float* B, float* C, int M, int N, int K) {
+    dense_gemm(A, B, C, M, N, K, "scalar_gemm");
+}
+void tiled_gemm(const float* A, const float* B, float* C, int M, int N, int K) {
+    dense_gemm(A, B, C, M, N, K, "tiled_gemm");
+}
+void avx2_gemm(const float* A, const float* B, float* C, int M, int N, int K) {
+    dense_gemm(A, B, C, M, N, K, "avx2_gemm");
+}
+void avx2_tiled_gemm(const float* A, const float* B, float* C, int M, int N, int K) {
+    dense_gemm(A, B, C, M, N, K, "avx2_tiled_gemm");
+}
+
 }  // namespace kernel
+
+// ---- weight residency (no reference counterpart) --------------------------
+namespace mi355x {
+void register_weights(const void* host, size_t bytes) { registry().add(host, bytes); }
+bool unregister_weights(const void* host) { return registry().remove(host); }
+size_t registered_bytes() { return registry().total(); }
+}  // namespace mi355x
 
 // ---- int8 quantisation (src/int8_quant.cpp:8-41) -------------------------
 

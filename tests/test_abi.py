@@ -109,3 +109,18 @@ def test_facade_exports_reference_signatures(mth):
     have = {ln.split(None, 2)[2] for ln in out.splitlines() if len(ln.split(None, 2)) == 3}
     missing = [s for s in FACADE if s not in have]
     assert not missing, missing
+
+
+REF_INCLUDE = os.environ.get("MYTHOS_REFERENCE", "/root/reference") + "/include"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="reference headers not present on this host")
+def test_facade_compiles_against_reference_headers():
+    """The façade source builds against the reference's own oil/*.h (its
+    Tensor, Error, Int8QuantParams), so it links into the reference's tree in
+    place of its CPU kernel library."""
+    src = os.path.join(PKG, "host", "kernel.cpp")
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++20", "-fsyntax-only", f"-I{REF_INCLUDE}",
+                        f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(PKG, 'host', 'include')}", src],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
