@@ -9,6 +9,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "launch.h"
 #include "../../include/mythos_oil.h"
@@ -40,6 +43,40 @@ inline hipStream_t S(mth_stream_t s) { return (hipStream_t)s; }
 // int32 row/column indices are used inside kernels for the fast paths; the
 // generic kernels index with int64.  Reject sizes whose byte counts overflow.
 constexpr int64_t kMaxDim = (int64_t)1 << 40;
+
+// Device scratch of the batched OIL4 GEMV (partial sums of its K slices),
+// one per (device, stream): calls on one stream are ordered and may share it;
+// another stream gets its own.  Grown on demand, never shrunk.
+struct Workspace {
+    void* base = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+hipError_t bt_workspace(hipStream_t s, int64_t M, int64_t K, float** partial) {
+    const size_t need = mth::oil4_bt_partial_bytes(M, K);
+    *partial = nullptr;
+    if (need == 0) return hipSuccess;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    Workspace& w = g_ws[{dev, s}];
+    if (w.bytes < need) {
+        void* p = nullptr;
+        e = hipMalloc(&p, need);
+        if (e != hipSuccess) return e;
+        if (w.base) {
+            (void)hipStreamSynchronize(s);  // earlier launches on s may still use it
+            (void)hipFree(w.base);
+        }
+        w.base = p;
+        w.bytes = need;
+    }
+    *partial = (float*)w.base;
+    return hipSuccess;
+}
 
 #define REQUIRE(cond, ...) \
     do {                   \
@@ -86,6 +123,15 @@ int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_b
     REQUIRE(cb_block >= 0, "mth_oil4_gemv: cb_block=%lld < 0", (long long)cb_block);
     REQUIRE(cb_block == 0 || K % cb_block == 0, "mth_oil4_gemv: K=%lld not a multiple of cb_block=%lld",
             (long long)K, (long long)cb_block);
+    const bool aligned = (((uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)x) & 15u) == 0;
+    if (aligned && mth::oil4_bt_supported(M, K, cb_block, batch)) {
+        float* partial = nullptr;
+        const hipError_t e = bt_workspace(S(stream), M, K, &partial);
+        if (e != hipSuccess)
+            return fail(MTH_EDEVICE, "mth_oil4_gemv: workspace allocation failed: %s", hipGetErrorString(e));
+        return check_launch(mth::launch_oil4_gemv_bt(packed, codebooks, cb_block, x, y, M, K, batch, partial, S(stream)),
+                            "mth_oil4_gemv");
+    }
     return check_launch(mth::launch_oil4_gemv(packed, codebooks, cb_block, x, y, M, K, batch, S(stream)),
                         "mth_oil4_gemv");
 }

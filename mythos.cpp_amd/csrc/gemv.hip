@@ -37,6 +37,7 @@
 // one-wave-per-output kernels.
 #include "common.h"
 #include "launch.h"
+#include "oil4_common.h"
 
 namespace mth {
 namespace {
@@ -44,15 +45,9 @@ namespace {
 constexpr int kWG = 256;
 constexpr int kWaves = kWG / MTH_WAVE;
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Compiler-level ordering point for wave-private LDS traffic.  LDS operations
-// of one wave execute in program order, so no wait is needed, only that the
-// compiler keeps the order.
-__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
 
 // v_perm selector building the LDS byte address (byte b of S0 << 8) | S1.byte0
 __device__ __forceinline__ uint32_t perm_addr(uint32_t packed, uint32_t lane4, int b) {
@@ -347,106 +342,36 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
 }
 
 // ===================================================================
-// OIL4, batch 1: codebook lookup in registers (oil4_gemv_v2)
+// OIL4, batch 1 (oil4_gemv_v2): 128-byte row runs, v_perm codebook lookups
 // ===================================================================
-// The row block's 16 FP16 entries sit in 8 VGPRs as byte planes (lo bytes of
-// entries 0-3, 4-7, 8-11, 12-15, then the hi bytes) and v_perm_b32 serves as
-// a four-wide 8-entry byte lookup: the low 3 bits of each nibble select
-// within entries 0-7 and 8-15, a second v_perm picks by bit 3, a third
-// interleaves lo and hi bytes into FP16 pairs.
-
-struct CbPlanes {
-    uint32_t l[4], h[4];
-};
-
-// entries 2i (low half) and 2i+1 (high half) in dword i of a (i < 4) / b
-__device__ __forceinline__ CbPlanes cb_planes(const uint4& a, const uint4& b) {
-    CbPlanes p;
-    p.l[0] = __builtin_amdgcn_perm(a.y, a.x, 0x06040200u);
-    p.h[0] = __builtin_amdgcn_perm(a.y, a.x, 0x07050301u);
-    p.l[1] = __builtin_amdgcn_perm(a.w, a.z, 0x06040200u);
-    p.h[1] = __builtin_amdgcn_perm(a.w, a.z, 0x07050301u);
-    p.l[2] = __builtin_amdgcn_perm(b.y, b.x, 0x06040200u);
-    p.h[2] = __builtin_amdgcn_perm(b.y, b.x, 0x07050301u);
-    p.l[3] = __builtin_amdgcn_perm(b.w, b.z, 0x06040200u);
-    p.h[3] = __builtin_amdgcn_perm(b.w, b.z, 0x07050301u);
-    return p;
-}
-
-// Weights 0..7 of d (weight v = low nibble of byte v/2 for even v, high for
-// odd v) -> FP16 pairs {0,2}, {4,6}, {1,3}, {5,7}: the A operand element
-// order is w[0,2,4,6,1,3,5,7], and B is stored in the same order.
-__device__ __forceinline__ half8 lookup8(uint32_t d, const CbPlanes& p) {
-    const uint32_t sE = d & 0x07070707u;
-    const uint32_t dO = d >> 4;
-    const uint32_t sO = dO & 0x07070707u;
-    // byte j of the pick selector: j (entries 0-7) or 4 + j (entries 8-15)
-    const uint32_t pE = ((d >> 1) & 0x04040404u) | 0x03020100u;
-    const uint32_t pO = ((dO >> 1) & 0x04040404u) | 0x03020100u;
-    const uint32_t loE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sE),
-                                               __builtin_amdgcn_perm(p.l[1], p.l[0], sE), pE);
-    const uint32_t hiE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sE),
-                                               __builtin_amdgcn_perm(p.h[1], p.h[0], sE), pE);
-    const uint32_t loO = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sO),
-                                               __builtin_amdgcn_perm(p.l[1], p.l[0], sO), pO);
-    const uint32_t hiO = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sO),
-                                               __builtin_amdgcn_perm(p.h[1], p.h[0], sO), pO);
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-    const u32x4v r = {__builtin_amdgcn_perm(hiE, loE, 0x05010400u), __builtin_amdgcn_perm(hiE, loE, 0x07030602u),
-                      __builtin_amdgcn_perm(hiO, loO, 0x05010400u), __builtin_amdgcn_perm(hiO, loO, 0x07030602u)};
-    return __builtin_bit_cast(half8, r);
-}
-
-// Value of lane (l & ~15) | ((l + 8) & 15): DPP row_ror:8 inside each
-// 16-lane row.  The empty asm pins the read in the convergent code: a DPP
-// read sunk under a partial exec mask would see the source lane disabled.
-__device__ __forceinline__ uint32_t dpp_ror8(uint32_t v) {
-    uint32_t r = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
-    asm volatile("" : "+v"(r));
-    return r;
-}
-
-// K = NW * NPH * 256; each wave owns NPH phases of 256 columns of 16 rows.
+// Workgroup = 16 rows x K; wave w owns columns [w*KW, (w+1)*KW) as NPH phases
+// of 256 (weight path: oil4_common.h).  x is split per wave into FP16 hi + lo
+// parts after a power-of-two scale (x*2^s = hi + lo + O(2^-22)), placed as B
+// columns 0 and 1, so D[:,0] + D[:,1] is the FP32 dot product: products are
+// exact, sums FP32.
 template <int NW, int NPH, bool SHARED>
 struct Oil4V2Lds {
     static constexpr int KW = NPH * 256;             // columns per wave
     static constexpr int lo_off = KW * 2 + 64;       // B: hi block, 64 B skew, lo block
     static constexpr int bwave = lo_off + KW * 2;
-    static constexpr int stage = SHARED ? 0 : 2048;  // codebook staging: 16 rows x 128 B
+    static constexpr int stage = SHARED ? 0 : 2048;  // codebook stage
     static constexpr int per_wave = bwave + stage;
     static constexpr int part = NW * per_wave;
     static constexpr int bytes = part + NW * 16 * 4;
 };
 
-// OIL4 GEMV, batch 1, codebooks per 128-weight row block (or one shared).
-//
-// Loads.  A wave instruction that reads 64-byte runs of 16 rows reaches only
-// ~4.2 TB/s on MI355X; runs of 128 bytes or more reach the streaming rate.  So
-// every nibble load reads 8 rows x 128 contiguous bytes (lane 16q + jj: row
-// jj % 8 (+8 for the second load), 16-byte piece 2q + (jj >= 8)), and one
-// DPP row rotation by 8 plus a select hands each lane (j, q) the 32 bytes of
-// row j it feeds to the MFMA: pieces 2q, 2q+1 of the phase, i.e. columns
-// [64q, 64q + 64).  Codebooks (4 blocks = 128 bytes per row per phase pair)
-// load the same way into a small wave-private LDS stage (XOR-swizzled, no
-// bank conflicts) and each lane reads back the 32-byte block of its columns.
-//
-// Dequantisation.  The block's 16 FP16 entries become 8 byte-plane VGPRs and
-// v_perm_b32 does the lookups (lookup8), so the weight path needs no LDS.
-// MFMA m of phase p covers columns 256p + 64q + 8m + v for lane group q.
 template <int NW, int NPH, bool SHARED>
 __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, const uint16_t* cbs,
                                                         const float* __restrict__ x, float* __restrict__ y,
                                                         int M, int K) {
     using L = Oil4V2Lds<NW, NPH, SHARED>;
     constexpr int KW = L::KW;
-    static_assert(SHARED || NPH % 2 == 0, "codebooks load per phase pair");
     __shared__ __align__(16) uint8_t lds[L::bytes];
     float* part = (float*)(lds + L::part);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
     const int row0 = blockIdx.x * 16;
     const int k0 = wave * KW;
-    const int nbr = K >> 7;  // codebook blocks per row
 
     // x first, then (once every wave of the workgroup has issued it) the
     // weight streams: the CU returns loads in issue order.
@@ -458,32 +383,14 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- issue every weight load of the wave, in consumption order ----
-    const int jj8 = j & 7, hi8 = j >> 3;
-    // nibble loads: X (rows 0-7) and Y (rows 8-15) per phase
-    const uint8_t* nx = nib + (int64_t)min(row0 + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
-    const uint8_t* ny = nib + (int64_t)min(row0 + 8 + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
-    // codebook loads: lane l -> row 8u + l/8, 16-byte piece l % 8 of the
-    // 4 blocks of a phase pair
-    const uint16_t* cl0 = cbs + ((int64_t)min(row0 + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
-    const uint16_t* cl1 = cbs + ((int64_t)min(row0 + 8 + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
-    uint4 wx[NPH], wy[NPH], c0[NPH / 2 + 1], c1[NPH / 2 + 1];
-#pragma unroll
-    for (int p = 0; p < NPH; ++p) {
-        if (!SHARED && p % 2 == 0) {
-            c0[p / 2] = ld16(cl0 + (p / 2) * 64);
-            c1[p / 2] = ld16(cl1 + (p / 2) * 64);
-        }
-        wx[p] = ld_stream(nx + 128 * p);
-        wy[p] = ld_stream(ny + 128 * p);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    Oil4TileLoads<NPH, SHARED> w;
+    w.issue(nib, cbs, row0, M, K, k0, lane);
     CbPlanes shared_planes;
     if (SHARED) shared_planes = cb_planes(ld16(cbs), ld16(cbs + 8));
 
     // ---- x slice -> power-of-two scale -> FP16 hi/lo B fragments --------
     // lane l holds columns 16l .. 16l+15 = phase l/16, group (l%16)/4,
-    // MFMAs 2(l%4) and 2(l%4)+1; elements in the order w[0,2,4,6,1,3,5,7]
+    // MFMAs 2(l%4) and 2(l%4)+1
     uint8_t* wl = lds + wave * L::per_wave;
     _Float16* xw = (_Float16*)wl;
     float xv[16];
@@ -495,10 +402,7 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(xv[i]));
-    mx = wave_max(mx);
-    int e = 0;
-    if (mx > 0.0f && mx <= 3.0e38f) (void)frexpf(mx, &e);
-    const int sh = (mx > 0.0f && mx <= 3.0e38f) ? 15 - e : 0;  // max|x|*2^sh < 2^15
+    const int sh = fp16_scale_shift(wave_max(mx));  // max|x|*2^sh < 2^15
     if (xl) {
         const int p = lane >> 4, qq = (lane & 15) >> 2;
 #pragma unroll
@@ -507,8 +411,7 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
             half8 vh, vl;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const int v = (t < 4) ? 2 * t : 2 * (t - 4) + 1;
-                const float xs = ldexpf(xv[8 * h + v], sh);
+                const float xs = ldexpf(xv[8 * h + oil4_elem_col(t)], sh);
                 const _Float16 hh = (_Float16)xs;
                 vh[t] = hh;
                 vl[t] = (_Float16)(xs - (float)hh);
@@ -526,38 +429,13 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
     const int xb = ((j & 1) ? L::lo_off : 0) + q * 16;
     auto bfrag = [&](int pm) { return *(const half8*)(wl + xb + pm * 64); };
 
-    // codebook stage: (row r, piece c) at r*128 + 16*(c ^ s(r))
-    uint8_t* st = wl + L::bwave;
-    auto swz = [](int r, int c) { return r * 128 + 16 * (c ^ ((r & 7) ^ ((r >> 3) & 1))); };
-
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     half8 bnext = bfrag(0);
 #pragma unroll
     for (int p = 0; p < NPH; ++p) {
-        CbPlanes pl;
-        if (SHARED) {
-            pl = shared_planes;
-        } else {
-            if (p % 2 == 0) {
-                *(uint4*)(st + swz(lane >> 3, lane & 7)) = c0[p / 2];
-                *(uint4*)(st + swz(8 + (lane >> 3), lane & 7)) = c1[p / 2];
-                wave_lds_order();
-            }
-            const int bi = 2 * (p & 1) + (q >> 1);  // block of this lane's columns
-            pl = cb_planes(*(const uint4*)(st + swz(j, 2 * bi)), *(const uint4*)(st + swz(j, 2 * bi + 1)));
-            wave_lds_order();
-        }
-        // rows 0-7 / 8-15 -> lane (j, q): a = pieces 2q (X'), b = 2q+1 (Y')
-        const bool keep = j < 8;
+        const CbPlanes pl = SHARED ? shared_planes : w.planes(p, wl + L::bwave, lane);
         uint4 xa, yb;
-        {
-            const uint32_t ry0 = dpp_ror8(wy[p].x), ry1 = dpp_ror8(wy[p].y), ry2 = dpp_ror8(wy[p].z),
-                           ry3 = dpp_ror8(wy[p].w);
-            const uint32_t rx0 = dpp_ror8(wx[p].x), rx1 = dpp_ror8(wx[p].y), rx2 = dpp_ror8(wx[p].z),
-                           rx3 = dpp_ror8(wx[p].w);
-            xa = make_uint4(keep ? wx[p].x : ry0, keep ? wx[p].y : ry1, keep ? wx[p].z : ry2, keep ? wx[p].w : ry3);
-            yb = make_uint4(keep ? rx0 : wy[p].x, keep ? rx1 : wy[p].y, keep ? rx2 : wy[p].z, keep ? rx3 : wy[p].w);
-        }
+        w.exchange(p, lane, xa, yb);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const int pm = p * 8 + m;
@@ -577,7 +455,7 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
     if (tid < 16 && row0 + tid < M) {
         float sum = part[tid];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) sum += part[w * 16 + tid];
+        for (int w2 = 1; w2 < NW; ++w2) sum += part[w2 * 16 + tid];
         y[row0 + tid] = sum;
     }
 }

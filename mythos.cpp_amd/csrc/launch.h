@@ -25,6 +25,13 @@ hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float*
 hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block,
                             const float* x, float* y, int64_t M, int64_t K, int64_t batch,
                             hipStream_t s);
+// Batches of 2 and more (gemv_batched.hip), groups of 16 tokens per launch.
+// partial: oil4_bt_partial_bytes(M, K) bytes of device scratch (null when
+// that is 0); calls that share it must be stream-ordered.
+bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch);
+size_t oil4_bt_partial_bytes(int64_t M, int64_t K);
+hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y,
+                               int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
 // Reference per-(m,n) indexing with one codebook (src/kernel_oil4.cpp:41-52).
 hipError_t launch_oil4_gemm_mn(const uint8_t* nib, const uint16_t* cb, const float* act, float* out,
                                int64_t M, int64_t N, int64_t K, hipStream_t s);

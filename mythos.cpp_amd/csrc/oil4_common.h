@@ -1,0 +1,180 @@
+// oil4_common.h — the OIL4 weight path shared by the decode kernels
+// (oil4_gemv_v2 for batch 1, oil4_gemv_bt for batches up to 16).
+//
+// Weight layout (the reference's, src/kernel_oil4.cpp:45-48): row m is K/2
+// bytes, element k is the low nibble of byte k/2 for even k and the high
+// nibble for odd k; codebooks cb[m][K/128][16] FP16.
+//
+// Loads.  A wave instruction that reads 64-byte runs of 16 rows reaches only
+// ~4.2 TB/s on MI355X; runs of 128 bytes or more reach the streaming rate.  So
+// for a 16-row tile every nibble load reads 8 rows x 128 contiguous bytes
+// (lane 16q + jj: row jj % 8 (+8 for the second load), 16-byte piece
+// 2q + (jj >= 8) of a 256-column phase), and one DPP row rotation by 8 plus a
+// select hands each lane (j = l % 16, q = l / 16) the 32 bytes of row j it
+// feeds to the MFMA: pieces 2q, 2q+1, i.e. columns [64q, 64q + 64) of the
+// phase.  Codebooks (4 blocks = 128 bytes per row per phase pair) load the
+// same way into a 2 KB wave-private LDS stage (XOR-swizzled: conflict-free for
+// the writes and for the reads) and each lane reads back the 32-byte block of
+// its columns.
+//
+// Dequantisation.  The block's 16 FP16 entries become 8 byte-plane VGPRs and
+// v_perm_b32 is a four-wide 8-entry byte lookup (lookup8): no LDS on the
+// weight path.  MFMA m of phase p then covers columns 256p + 64q + 8m + v of
+// the tile for lane group q, with the 8 elements of a lane in the order
+// v = 0, 2, 4, 6, 1, 3, 5, 7.
+#pragma once
+
+#include "common.h"
+
+namespace mth {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Compiler-level ordering point for wave-private LDS traffic.  LDS operations
+// of one wave execute in program order, so no wait is needed, only that the
+// compiler keeps the order.
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
+
+// Element e of an A/B fragment holds column offset kOrder[e] of its 8.
+__device__ __forceinline__ int oil4_elem_col(int e) { return (e < 4) ? 2 * e : 2 * (e - 4) + 1; }
+
+struct CbPlanes {
+    uint32_t l[4], h[4];
+};
+
+// entries 2i (low half) and 2i+1 (high half) in dword i of a (i < 4) / b
+__device__ __forceinline__ CbPlanes cb_planes(const uint4& a, const uint4& b) {
+    CbPlanes p;
+    p.l[0] = __builtin_amdgcn_perm(a.y, a.x, 0x06040200u);
+    p.h[0] = __builtin_amdgcn_perm(a.y, a.x, 0x07050301u);
+    p.l[1] = __builtin_amdgcn_perm(a.w, a.z, 0x06040200u);
+    p.h[1] = __builtin_amdgcn_perm(a.w, a.z, 0x07050301u);
+    p.l[2] = __builtin_amdgcn_perm(b.y, b.x, 0x06040200u);
+    p.h[2] = __builtin_amdgcn_perm(b.y, b.x, 0x07050301u);
+    p.l[3] = __builtin_amdgcn_perm(b.w, b.z, 0x06040200u);
+    p.h[3] = __builtin_amdgcn_perm(b.w, b.z, 0x07050301u);
+    return p;
+}
+
+// Weights 0..7 of d (weight v = low nibble of byte v/2 for even v, high for
+// odd v) -> FP16 pairs {0,2}, {4,6}, {1,3}, {5,7}.  The low 3 bits of each
+// nibble select within entries 0-7 and 8-15, a second v_perm picks by bit 3,
+// a third interleaves lo and hi bytes into FP16 pairs.
+__device__ __forceinline__ half8 lookup8(uint32_t d, const CbPlanes& p) {
+    const uint32_t sE = d & 0x07070707u;
+    const uint32_t dO = d >> 4;
+    const uint32_t sO = dO & 0x07070707u;
+    // byte j of the pick selector: j (entries 0-7) or 4 + j (entries 8-15)
+    const uint32_t pE = ((d >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t pO = ((dO >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t loE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sE),
+                                               __builtin_amdgcn_perm(p.l[1], p.l[0], sE), pE);
+    const uint32_t hiE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sE),
+                                               __builtin_amdgcn_perm(p.h[1], p.h[0], sE), pE);
+    const uint32_t loO = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sO),
+                                               __builtin_amdgcn_perm(p.l[1], p.l[0], sO), pO);
+    const uint32_t hiO = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sO),
+                                               __builtin_amdgcn_perm(p.h[1], p.h[0], sO), pO);
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v r = {__builtin_amdgcn_perm(hiE, loE, 0x05010400u), __builtin_amdgcn_perm(hiE, loE, 0x07030602u),
+                      __builtin_amdgcn_perm(hiO, loO, 0x05010400u), __builtin_amdgcn_perm(hiO, loO, 0x07030602u)};
+    return __builtin_bit_cast(half8, r);
+}
+
+// DPP row rotation inside each 16-lane row (CTRL 0x121..0x12F = row_ror:1..15).
+// The empty asm pins the read in the convergent code: a DPP read sunk under a
+// partial exec mask would see its source lane disabled.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_row(uint32_t v) {
+    uint32_t r = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+    asm volatile("" : "+v"(r));
+    return r;
+}
+__device__ __forceinline__ uint32_t dpp_ror8(uint32_t v) { return dpp_row<0x128>(v); }
+
+// Max over the 16 lanes of each DPP row (every lane gets the row's max).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __uint_as_float(dpp_row<0x128>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_row<0x124>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_row<0x122>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_row<0x121>(__float_as_uint(v))));
+    return v;
+}
+
+// Power-of-two exponent s with max|x| * 2^s < 2^15 (0 for zero / non-finite).
+__device__ __forceinline__ int fp16_scale_shift(float mx) {
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.0e38f) {
+        (void)frexpf(mx, &e);
+        return 15 - e;
+    }
+    return 0;
+}
+
+// Codebook stage (2 KB, wave-private): (row r, 16-byte piece c) at
+// r*128 + 16*(c ^ s(r)).  Lanes 0-7 / 0-15 of a wave access distinct banks
+// both when 8 lanes write one row and when 16 lanes read 16 rows.
+__device__ __forceinline__ int oil4_stage_off(int r, int c) {
+    return r * 128 + 16 * (c ^ ((r & 7) ^ ((r >> 3) & 1)));
+}
+
+// All weight loads of one wave for a 16-row tile and NPH phases of 256
+// columns starting at column k0, issued in consumption order.
+template <int NPH, bool SHARED>
+struct Oil4TileLoads {
+    static_assert(SHARED || NPH % 2 == 0, "codebooks load per phase pair");
+    uint4 wx[NPH], wy[NPH], c0[NPH / 2 + 1], c1[NPH / 2 + 1];
+
+    __device__ __forceinline__ void issue(const uint8_t* nib, const uint16_t* cbs, int row0, int M, int K, int k0,
+                                          int lane) {
+        const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
+        const int nbr = K >> 7;  // codebook blocks per row
+        const uint8_t* nx = nib + (int64_t)min(row0 + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
+        const uint8_t* ny = nib + (int64_t)min(row0 + 8 + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
+        // codebook loads: lane l -> row 8u + l/8, 16-byte piece l % 8 of the
+        // 4 blocks of a phase pair
+        const uint16_t* cl0 = cbs + ((int64_t)min(row0 + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
+        const uint16_t* cl1 =
+            cbs + ((int64_t)min(row0 + 8 + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
+#pragma unroll
+        for (int p = 0; p < NPH; ++p) {
+            if (!SHARED && p % 2 == 0) {
+                c0[p / 2] = ld16(cl0 + (p / 2) * 64);
+                c1[p / 2] = ld16(cl1 + (p / 2) * 64);
+            }
+            wx[p] = ld_stream(nx + 128 * p);
+            wy[p] = ld_stream(ny + 128 * p);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Byte planes of the codebook block behind this lane's columns of phase p
+    // (stage: the wave's 2 KB codebook stage).
+    __device__ __forceinline__ CbPlanes planes(int p, uint8_t* stage, int lane) {
+        const int j = lane & 15, q = lane >> 4;
+        if (p % 2 == 0) {
+            *(uint4*)(stage + oil4_stage_off(lane >> 3, lane & 7)) = c0[p / 2];
+            *(uint4*)(stage + oil4_stage_off(8 + (lane >> 3), lane & 7)) = c1[p / 2];
+            wave_lds_order();
+        }
+        const int bi = 2 * (p & 1) + (q >> 1);  // block of this lane's columns
+        const CbPlanes pl = cb_planes(*(const uint4*)(stage + oil4_stage_off(j, 2 * bi)),
+                                      *(const uint4*)(stage + oil4_stage_off(j, 2 * bi + 1)));
+        wave_lds_order();
+        return pl;
+    }
+
+    // Rows 0-7 / 8-15 -> lane (j, q): a = piece 2q, b = piece 2q+1 of row j.
+    __device__ __forceinline__ void exchange(int p, int lane, uint4& a, uint4& b) const {
+        const bool keep = (lane & 15) < 8;
+        const uint32_t ry0 = dpp_ror8(wy[p].x), ry1 = dpp_ror8(wy[p].y), ry2 = dpp_ror8(wy[p].z),
+                       ry3 = dpp_ror8(wy[p].w);
+        const uint32_t rx0 = dpp_ror8(wx[p].x), rx1 = dpp_ror8(wx[p].y), rx2 = dpp_ror8(wx[p].z),
+                       rx3 = dpp_ror8(wx[p].w);
+        a = make_uint4(keep ? wx[p].x : ry0, keep ? wx[p].y : ry1, keep ? wx[p].z : ry2, keep ? wx[p].w : ry3);
+        b = make_uint4(keep ? rx0 : wy[p].x, keep ? rx1 : wy[p].y, keep ? rx2 : wy[p].z, keep ? rx3 : wy[p].w);
+    }
+};
+
+}  // namespace mth

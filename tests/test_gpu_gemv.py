@@ -109,6 +109,57 @@ def test_oil4_gemv(M, K, batch, block, oracle, mth, dev):
     fp32_close(y.cpu().numpy().reshape(batch, M), ref, absw.T, 1e-5, "oil4_gemv")
 
 
+@pytest.mark.parametrize("M,K,batch,block", [
+    (11008, 4096, 2, 128),   # 4 K slices, cross-workgroup sums
+    (1000, 4096, 17, 128),   # two groups of tokens
+    (130, 1024, 16, 128),    # 2 slices, rows not a multiple of 64
+    (64, 512, 3, 128),       # one slice: no workspace
+    (200, 1536, 8, 128),     # 3 slices of 512 columns
+    (77, 3072, 4, 128),      # 3 slices of 1024 columns
+    (300, 2048, 16, 0),      # one shared codebook
+])
+def test_oil4_gemv_batched(M, K, batch, block, oracle, mth, dev):
+    """Batches >= 2 run the split-K MFMA kernel; FP32 accuracy as batch 1."""
+    import torch
+    print(f"oil4_gemv batched M={M} K={K} batch={batch} block={block}", flush=True)
+    packed, cbs, x = synth.oil4(M, K, batch, block)
+    y = empty(batch * M, torch.float32, dev)
+    p_d, c_d, x_d = to_dev(packed, dev), to_dev(cbs, dev), to_dev(x, dev)
+    mth.oil4_gemv(p_d, c_d, block, x_d, y, M, K, batch)
+    torch.cuda.synchronize()
+    if block:
+        ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, M, K, batch, block, threads=8)
+    else:  # the shared codebook as one block per row
+        ref = oracle.oil4_gemv_blocked(packed.ravel(), np.tile(cbs, M), x, M, K, batch, K, threads=8)
+    W = synth.dequant_oil4(packed, cbs, M, K, block)
+    absw = np.abs(W).astype(np.float64) @ np.abs(x.astype(np.float64)).T
+    got = y.cpu().numpy().reshape(batch, M)
+    fp32_close(got, ref, absw.T, 1e-5, "oil4_gemv batched")
+    # deterministic: a second call gives the same bits
+    y2 = empty(batch * M, torch.float32, dev)
+    mth.oil4_gemv(p_d, c_d, block, x_d, y2, M, K, batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(batch, M), got)
+
+
+def test_oil4_gemv_batched_two_streams(mth, dev):
+    """Each stream has its own workspace; interleaved calls stay exact."""
+    import torch
+    M, K, batch = 2048, 4096, 8
+    packed, cbs, x = synth.oil4(M, K, batch, 128)
+    p_d, c_d, x_d = to_dev(packed, dev), to_dev(cbs, dev), to_dev(x, dev)
+    y0 = empty(batch * M, torch.float32, dev)
+    mth.oil4_gemv(p_d, c_d, 128, x_d, y0, M, K, batch)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    ys = [empty(batch * M, torch.float32, dev) for _ in range(4)]
+    for i, yy in enumerate(ys):
+        mth.oil4_gemv(p_d, c_d, 128, x_d, yy, M, K, batch, stream=s1 if i % 2 == 0 else s2)
+    torch.cuda.synchronize()
+    for yy in ys:
+        assert torch.equal(yy, y0)
+
+
 @pytest.mark.parametrize("M,N,K", [(7, 3, 48), (5, 2, 33), (4, 1, 4096), (3, 4, 1)])
 def test_oil4_gemm_reference_indexing(M, N, K, oracle, mth, dev):
     import torch
