@@ -12,11 +12,11 @@
 // 64x64, register double-buffered global loads.
 #include "common.h"
 #include "launch.h"
+#include "oil4_common.h"
 
 namespace mth {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 32;
@@ -135,6 +135,179 @@ __global__ __launch_bounds__(256, 2) void oil4_gemm_prefill_k(
         }
 }
 
+// ===================================================================
+// Production kernel (oil4_prefill_mfma)
+// ===================================================================
+// C[m][n] = bf16(sum_k A[m][k] * W[n][k]) with FP32 accumulation on
+// v_mfma_f32_16x16x32_f16: W is exact in FP16 (the codebook entries) and A
+// is converted bf16 -> FP16 when its fragments are read (exact for
+// 2^-14 <= |a| <= 65504; smaller values keep FP16's subnormal precision).
+// Rounding W to bf16 instead would add a second 2^-8 rounding per weight and
+// put the result over the 2e-3 budget of this path.
+//
+//   * workgroup tile 256 (m) x BN (n), K steps of 64; 4 waves stacked along m,
+//     each 64 x BN = 4 x BN/16 MFMA tiles held in accumulators;
+//   * A: each wave instruction reads 8 rows x 128 contiguous bytes; the
+//     choice of source chunk per lane XOR-swizzles the 16-byte chunks of a row
+//     in LDS so that the MFMA fragment reads hit distinct banks;
+//   * W: two threads per row each stream 32 nibbles per step and dequantise
+//     them with v_perm byte-plane lookups (oil4_common.h) into the FP16 tile;
+//   * one barrier per K step; A loaded 2 steps ahead and W nibbles and
+//     codebooks 4 steps ahead into VGPR rings (covering L2 / HBM latency),
+//     A and dequantised W tiles double-buffered in LDS.
+constexpr int PBM = 256, PBK = 64;
+
+// byte offset of 16-byte chunk c (0..7) of row r in a 128-byte-row tile
+__device__ __forceinline__ int pf_off(int r, int c) { return r * 128 + 16 * (c ^ ((r & 7) ^ ((r >> 3) & 1))); }
+
+// 8 bf16 -> 8 FP16 (through FP32: v_cvt_pk_f16_f32 rounds to nearest even)
+__device__ __forceinline__ half8 bf16x8_to_f16(uint4 v) {
+    half8 r;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[2 * i] = (_Float16)__uint_as_float(w[i] << 16);
+        r[2 * i + 1] = (_Float16)__uint_as_float(w[i] & 0xffff0000u);
+    }
+    return r;
+}
+
+template <int BN>
+struct PfLds {
+    static constexpr int a = PBM * 128;  // one A tile (double-buffered)
+    static constexpr int w = BN * 128;   // one dequantised W tile (double-buffered)
+    static constexpr int bytes = 2 * a + 2 * w;
+};
+
+template <int BN>
+__global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __restrict__ A, const uint8_t* nib,
+                                                            const uint16_t* cbs, int cb_block,
+                                                            uint16_t* __restrict__ C, int M, int N, int K) {
+    using L = PfLds<BN>;
+    constexpr int NT = BN / 16;
+    __shared__ __align__(16) uint8_t lds[L::bytes];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m0 = blockIdx.y * PBM, n0 = blockIdx.x * BN;
+    const int nb = K / cb_block;
+    const int steps = K / PBK;
+
+    // ---- A: thread T loads 8 16-byte chunks per step (chunk id 256 i + T:
+    // row id/8, 16-byte slot id%8 of that row in LDS, holding source chunk
+    // slot ^ f(row)); each wave instruction reads 8 rows x 128 contiguous bytes.
+    uint4 av[2][8];
+    auto load_a = [&](int step, int slot) {
+        const int k0 = step * PBK;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int id = i * 256 + tid;
+            const int r = id >> 3;
+            const int c = (id & 7) ^ ((r & 7) ^ ((r >> 3) & 1));
+            av[slot][i] = ld16(A + (int64_t)min(m0 + r, M - 1) * K + k0 + 8 * c);
+        }
+    };
+    auto store_a = [&](int slot, uint8_t* base) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *(uint4*)(base + (i * 256 + tid) * 16) = av[slot][i];
+    };
+
+    // ---- W: thread T < 2 BN dequantises row T/2, columns 32 (T%2) .. +31 of
+    // each step.  Every thread loads (the others a clamped row), so that all
+    // waves issue the same number of loads per step.  Ring of 4 steps in
+    // VGPRs: the nibbles and codebook of step s are loaded at step s - 4.
+    const bool wt = tid < 2 * BN;
+    const int wn = tid >> 1, wh = tid & 1;
+    const int wrow = min(n0 + (wt ? wn : 0), N - 1);
+    const uint8_t* wnib = nib + (int64_t)wrow * (K >> 1) + 16 * wh;
+    const uint16_t* wcb = cbs + (int64_t)wrow * nb * 16;
+    uint4 nv[4], ca[4], cc[4];
+    auto load_w = [&](int step, int slot) {
+        const int k0 = step * PBK;
+        nv[slot] = ld_stream(wnib + (k0 >> 1));
+        const uint16_t* cp = wcb + (k0 / cb_block) * 16;
+        ca[slot] = ld16(cp);
+        cc[slot] = ld16(cp + 8);
+    };
+
+    floatx4 acc[4][NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Pipeline (all loads into VGPR rings, so the compiler tracks every wait):
+    // step s stores A(s) (loaded at s - 2) and the dequantised W(s) (nibbles
+    // and codebook loaded at s - 4) into LDS buffers s % 2, passes the one
+    // barrier of the step, issues A(s + 2) and W(s + 4) (clamped to the last
+    // step near the end) and runs its MFMAs.
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_w(u < steps ? u : steps - 1, u);
+    load_a(0, 0);
+    load_a(steps > 1 ? 1 : 0, 1);
+    for (int s0 = 0; s0 < steps; s0 += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int step = s0 + u;
+            uint8_t* ab = lds + (u & 1) * L::a;
+            uint8_t* wb = lds + 2 * L::a + (u & 1) * L::w;
+            store_a(u & 1, ab);
+            if (wt) {
+                const CbPlanes pl = cb_planes(ca[u], cc[u]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    *(half8*)(wb + pf_off(wn, 4 * wh + i)) = lookup8_natural(u4get(nv[u], i), pl);
+            }
+            __syncthreads();
+            load_a(min(step + 2, steps - 1), u & 1);
+            load_w(min(step + 4, steps - 1), u);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int c = 4 * kk + (lane >> 4);
+                half8 af[4], bfr[NT];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    af[i] = bf16x8_to_f16(*(const uint4*)(ab + pf_off(64 * wave + 16 * i + (lane & 15), c)));
+#pragma unroll
+                for (int j = 0; j < NT; ++j) bfr[j] = *(const half8*)(wb + pf_off(16 * j + (lane & 15), c));
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // D layout: lane l holds column (l%16), rows 4*(l/16) + r
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int n = n0 + 16 * j + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+                if (m < M && n < N) C[(int64_t)m * N + n] = f32_to_bf16_rne(acc[i][j][r]);
+            }
+        }
+}
+
+// BN with the best fill of 256 CUs (ties: the larger tile)
+inline int pick_bn(int64_t M, int64_t N) {
+    const int cand[3] = {128, 112, 96};
+    int best = 128;
+    double beff = -1.0;
+    for (int bn : cand) {
+        const int64_t tiles = ((N + bn - 1) / bn) * ((M + PBM - 1) / PBM);
+        const int64_t rounds = (tiles + 255) / 256;
+        const double eff = (double)tiles / (double)(rounds * 256) * ((double)N / (double)(((N + bn - 1) / bn) * bn));
+        if (eff > beff + 1e-9) {
+            beff = eff;
+            best = bn;
+        }
+    }
+    return best;
+}
+
 }  // namespace
 
 bool oil4_gemm_prefill_supported(int64_t M, int64_t N, int64_t K, int64_t cb_block) {
@@ -145,6 +318,17 @@ bool oil4_gemm_prefill_supported(int64_t M, int64_t N, int64_t K, int64_t cb_blo
 hipError_t launch_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                     int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
                                     hipStream_t s) {
+    if (K % (4 * PBK) == 0 && cb_block % PBK == 0 && (M + PBM - 1) / PBM < 65536) {
+        const int bn = pick_bn(M, N);
+        const dim3 g2((unsigned)((N + bn - 1) / bn), (unsigned)((M + PBM - 1) / PBM));
+        if (bn == 112)
+            oil4_prefill_mfma<112><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+        else if (bn == 96)
+            oil4_prefill_mfma<96><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+        else
+            oil4_prefill_mfma<128><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
     oil4_gemm_prefill_k<<<grid, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
     return hipGetLastError();

@@ -151,14 +151,22 @@ __global__ __launch_bounds__(256) void oil4_gemv_bt(const uint8_t* nib, const ui
                 partial[((int64_t)blockIdx.y * kBtTok + j) * M + row0w + 4 * q + i] = ysum[i];
 }
 
-// y[t][m] = sum over slices z = 0, 1, ... of partial[z][t][m]
+// y[t][m] = sum over slices z = 0, 1, ... of partial[z][t][m]; all loads
+// are issued before the first add (at most 16 slices).
 __global__ __launch_bounds__(256) void oil4_bt_reduce(const float* __restrict__ partial, float* __restrict__ y,
                                                       int M, int batch, int nslice) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t)batch * M) return;
     const int64_t t = i / M, m = i - t * M;
-    float s = 0.0f;
-    for (int z = 0; z < nslice; ++z) s += partial[((int64_t)z * kBtTok + t) * M + m];
+    const float* p = partial + t * M + m;
+    const int64_t zs = (int64_t)kBtTok * M;
+    float v[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) v[z] = z < nslice ? p[z * zs] : 0.0f;
+    float s = v[0];
+#pragma unroll
+    for (int z = 1; z < 16; ++z)
+        if (z < nslice) s += v[z];
     y[i] = s;
 }
 
@@ -181,6 +189,7 @@ void run_bt(const uint8_t* nib, const uint16_t* cbs, const float* x, float* y, f
 }  // namespace
 
 bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch) {
+    // K <= 8192 keeps the slice count <= 16 (the reduction kernel's limit)
     return batch >= 2 && (cb_block == 0 || cb_block == 128) && K >= 512 && K <= 8192 && K % 512 == 0 &&
            M < (1ll << 31) && M * K < (1ll << 40);
 }

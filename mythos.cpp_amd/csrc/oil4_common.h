@@ -82,6 +82,31 @@ __device__ __forceinline__ half8 lookup8(uint32_t d, const CbPlanes& p) {
     return __builtin_bit_cast(half8, r);
 }
 
+// As lookup8, but in natural order: FP16/BF16 pairs {0,1}, {2,3}, {4,5},
+// {6,7} (for operands whose other side is stored in column order).
+__device__ __forceinline__ half8 lookup8_natural(uint32_t d, const CbPlanes& p) {
+    const uint32_t sE = d & 0x07070707u;
+    const uint32_t dO = d >> 4;
+    const uint32_t sO = dO & 0x07070707u;
+    const uint32_t pE = ((d >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t pO = ((dO >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t loE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sE),
+                                               __builtin_amdgcn_perm(p.l[1], p.l[0], sE), pE);
+    const uint32_t hiE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sE),
+                                               __builtin_amdgcn_perm(p.h[1], p.h[0], sE), pE);
+    const uint32_t loO = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sO),
+                                               __builtin_amdgcn_perm(p.l[1], p.l[0], sO), pO);
+    const uint32_t hiO = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sO),
+                                               __builtin_amdgcn_perm(p.h[1], p.h[0], sO), pO);
+    // lo / hi bytes of weights 0-3 and 4-7 in order, then byte pairs
+    const uint32_t l03 = __builtin_amdgcn_perm(loO, loE, 0x05010400u), h03 = __builtin_amdgcn_perm(hiO, hiE, 0x05010400u);
+    const uint32_t l47 = __builtin_amdgcn_perm(loO, loE, 0x07030602u), h47 = __builtin_amdgcn_perm(hiO, hiE, 0x07030602u);
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v r = {__builtin_amdgcn_perm(h03, l03, 0x05010400u), __builtin_amdgcn_perm(h03, l03, 0x07030602u),
+                      __builtin_amdgcn_perm(h47, l47, 0x05010400u), __builtin_amdgcn_perm(h47, l47, 0x07030602u)};
+    return __builtin_bit_cast(half8, r);
+}
+
 // DPP row rotation inside each 16-lane row (CTRL 0x121..0x12F = row_ror:1..15).
 // The empty asm pins the read in the convergent code: a DPP read sunk under a
 // partial exec mask would see its source lane disabled.
