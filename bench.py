@@ -282,7 +282,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded numpy PCG64; weights resident in HBM, rotated over >=1 GiB of copies)",
+        "data": "synthetic (MYTHOS.cpp RNG xoroshiro128+, seed 0x5EED0000+config; weights resident in HBM, "
+                "rotated over >=1 GiB of copies)",
         "config": {"workload": "OIL4 GEMV W 11008x4096, per-128-weight FP16 codebooks, batch 1 (BASELINE config 2)",
                    "M": head["M"], "K": head["K"], "batch": 1, "cb_block": 128,
                    "weight_copies": r["copies"]},
