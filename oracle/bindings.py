@@ -278,6 +278,14 @@ class Reference:
             f.restype = None
         L.ref_float_to_half.argtypes = [F32]
         L.ref_float_to_half.restype = C.c_uint16
+        for name in ("ref_serialize_oil8", "ref_serialize_oil4"):
+            getattr(L, name).argtypes = [VP, VP]
+            getattr(L, name).restype = I64
+        L.ref_oil_write.argtypes = [C.c_char_p, VP, C.c_uint32, C.c_int, VP, VP, VP, VP, VP, VP,
+                                    C.c_int, C.POINTER(C.c_char_p), VP, VP]
+        L.ref_oil_write.restype = None
+        L.ref_oil_read_tensor.argtypes = [C.c_char_p, C.c_char_p, VP, I64]
+        L.ref_oil_read_tensor.restype = I64
         L.ref_half_to_float.argtypes = [C.c_uint16]
         L.ref_half_to_float.restype = F32
 
@@ -372,3 +380,40 @@ class Reference:
         y = np.empty_like(x)
         self.lib.ref_silu(_p(x, np.float32), _p(y, np.float32), x.size)
         return y
+
+    # ---- .oil container (src/oil_format.cpp, src/codebook.cpp) ----------
+    def serialize_oil8(self, centroids) -> np.ndarray:
+        out = np.zeros(4 + 1024, np.uint8)
+        n = self.lib.ref_serialize_oil8(_p(np.asarray(centroids, np.float32), np.float32), _p(out, np.uint8))
+        return out[:n]
+
+    def serialize_oil4(self, centroids16) -> np.ndarray:
+        out = np.zeros(4 + 32, np.uint8)
+        n = self.lib.ref_serialize_oil4(_p(np.asarray(centroids16, np.uint16), np.uint16), _p(out, np.uint8))
+        return out[:n]
+
+    def oil_write(self, path, config: bytes, blocks, tensors) -> None:
+        """blocks: [(format, num_weights, codebook bytes, index bytes)] in file
+        order; tensors: [(name, block_start, num_blocks)]."""
+        fm = np.array([b[0] for b in blocks], np.uint8)
+        nw = np.array([b[1] for b in blocks], np.uint32)
+        cbs = np.array([len(b[2]) for b in blocks], np.uint32)
+        ids = np.array([len(b[3]) for b in blocks], np.uint32)
+        cbd = np.concatenate([np.frombuffer(bytes(b[2]), np.uint8) for b in blocks] + [np.zeros(1, np.uint8)])
+        idd = np.concatenate([np.frombuffer(bytes(b[3]), np.uint8) for b in blocks] + [np.zeros(1, np.uint8)])
+        cfg = np.frombuffer(config + b"\0", np.uint8)
+        names = (C.c_char_p * len(tensors))(*[t[0].encode() for t in tensors])
+        bs = np.array([t[1] for t in tensors], np.uint32)
+        nb = np.array([t[2] for t in tensors], np.uint32)
+        self.lib.ref_oil_write(str(path).encode(), _p(cfg, np.uint8), len(config), len(blocks),
+                               _p(fm, np.uint8), _p(nw, np.uint32), _p(cbs, np.uint32), _p(cbd, np.uint8),
+                               _p(ids, np.uint32), _p(idd, np.uint8), len(tensors), names,
+                               _p(bs, np.uint32), _p(nb, np.uint32))
+
+    def oil_read_tensor(self, path, name: str, cap: int) -> np.ndarray:
+        """OILReader::read_tensor(name) (the reference's FP32 dequantisation)."""
+        out = np.zeros(max(cap, 1), np.float32)
+        n = self.lib.ref_oil_read_tensor(str(path).encode(), name.encode(), _p(out, np.float32), cap)
+        if n < 0:
+            raise ValueError(f"reference OILReader rejected {path}")
+        return out[:min(n, cap)]

@@ -13,9 +13,12 @@
 #include "oil/random.h"
 #include "oil/math.h"
 #include "oil/tensor.h"
+#include "oil/oil_format.h"
 
 #include <cstdint>
 #include <cstring>
+#include <string>
+#include <vector>
 
 using namespace oil;
 
@@ -133,6 +136,75 @@ void ref_silu(const float* x, float* y, int64_t n) {
     Tensor ty(Shape{n}, DType::F32);
     math::silu(tx, ty);
     std::memcpy(y, ty.data(), (size_t)n * 4);
+}
+
+// ---- .oil container (src/oil_format.cpp, src/codebook.cpp) ---------------
+// Serialised codebooks exactly as CodebookOIL8/OIL4::serialize write them.
+int64_t ref_serialize_oil8(const float* centroids, uint8_t* dst) {
+    CodebookOIL8 cb;
+    std::memcpy(cb.centroids, centroids, sizeof(cb.centroids));
+    return (int64_t)cb.serialize(dst);
+}
+int64_t ref_serialize_oil4(const uint16_t* centroids, uint8_t* dst) {
+    CodebookOIL4 cb;
+    std::memcpy(cb.centroids, centroids, sizeof(cb.centroids));
+    return (int64_t)cb.serialize(dst);
+}
+
+// Writes a .oil file with OILWriter: header (+ config), format table, tensor
+// table, then every block.  Blocks are given in file order: formats[b],
+// nweights[b], cb_sizes[b] bytes of codebook_data, idx_sizes[b] bytes of
+// index_data (both concatenated).  Tensor t owns blocks
+// [block_start[t], block_start[t] + num_blocks[t]).
+void ref_oil_write(const char* path, const uint8_t* config, uint32_t config_size, int nblocks,
+                   const uint8_t* formats, const uint32_t* nweights, const uint32_t* cb_sizes,
+                   const uint8_t* codebook_data, const uint32_t* idx_sizes, const uint8_t* index_data,
+                   int ntensors, const char* const* names, const uint32_t* block_start, const uint32_t* num_blocks) {
+    OILWriter w(path);
+    OILHeader h;
+    std::memcpy(h.magic, "OIL1", 4);
+    h.version = (1u << 22);
+    h.flags = 0;
+    h.config_size = config_size;
+    w.write_header(h, config);
+    std::vector<FormatBlockEntry> ft((size_t)nblocks);
+    for (int b = 0; b < nblocks; b++) {
+        ft[(size_t)b].block_id = (uint32_t)b;
+        ft[(size_t)b].format = formats[b];
+        ft[(size_t)b].cb_bytes = cb_sizes[b];
+    }
+    w.write_format_table(ft);
+    std::vector<TensorEntry> te((size_t)ntensors);
+    std::vector<std::string> nm((size_t)ntensors);
+    for (int t = 0; t < ntensors; t++) {
+        nm[(size_t)t] = names[t];
+        te[(size_t)t].name_len = (uint16_t)nm[(size_t)t].size();
+        te[(size_t)t].block_start = block_start[t];
+        te[(size_t)t].num_blocks = num_blocks[t];
+    }
+    w.write_tensor_table(te, nm);
+    size_t co = 0, io = 0;
+    for (int b = 0; b < nblocks; b++) {
+        BlockData bd;
+        bd.num_weights = nweights[b];
+        bd.codebook.assign(codebook_data + co, codebook_data + co + cb_sizes[b]);
+        bd.indices.assign(index_data + io, index_data + io + idx_sizes[b]);
+        co += cb_sizes[b];
+        io += idx_sizes[b];
+        w.write_block(bd);
+    }
+    w.close();
+}
+
+// OILReader::read_tensor: the reference's dequantised FP32 copy of a tensor.
+// Returns the number of weights (0 if absent), writes at most cap floats.
+int64_t ref_oil_read_tensor(const char* path, const char* name, float* out, int64_t cap) {
+    OILReader r(path);
+    if (!r.valid()) return -1;
+    Tensor t = r.read_tensor(name);
+    const int64_t n = t.numel();
+    if (n > 0 && out) std::memcpy(out, t.data(), (size_t)(n < cap ? n : cap) * 4);
+    return n;
 }
 
 }  // extern "C"

@@ -179,6 +179,64 @@ def main() -> None:
          rms_x=xr, rms_g=g, rms=scalar.rms_norm(xr, g, 1e-5, 3, 64), rms_fma=avx2.rms_norm(xr, g, 1e-5, 3, 64),
          silu_x=xs, silu=scalar.silu(xs), silu_fma=avx2.silu(xs))
 
+    # ---- .oil container (src/oil_format.cpp OILWriter / OILReader) --------
+    # A small model file written by the reference's own OILWriter, holding
+    # every block format the quantised path reads, and the reference's
+    # OILReader::read_tensor dequantisation of each tensor.
+    def normal_cb16(n):
+        v = rng.standard_normal(n).astype(np.float32) * 0.02
+        v = np.where(np.abs(v) < 1e-3, np.float32(1e-3), v)      # keep FP16 normals
+        return np.array([avx2.float_to_half(float(x)) for x in v], np.uint16)
+
+    blocks, tensors, inputs = [], [], {}
+    # OIL8, one block (the converter's layout: tools/convert.cpp:521-533)
+    r, c = 6, 40
+    cb8 = np.sort(rng.standard_normal(256).astype(np.float32) * 0.05)
+    i8 = rng.integers(0, 256, r * c, dtype=np.uint8)
+    tensors.append(("blk.0.attn_q.weight", len(blocks), 1))
+    blocks.append((3, r * c, avx2.serialize_oil8(cb8).tobytes(), i8.tobytes()))
+    inputs.update(oil8_idx=i8, oil8_cb=cb8, oil8_shape=np.array([r, c]))
+    # OIL8, three blocks sharing one codebook (rows 4 x 96, blocks of 128)
+    i8m = rng.integers(0, 256, 4 * 96, dtype=np.uint8)
+    tensors.append(("blk.0.ffn_up.weight", len(blocks), 3))
+    for b in range(3):
+        blocks.append((3, 128, avx2.serialize_oil8(cb8).tobytes(), i8m[b * 128:(b + 1) * 128].tobytes()))
+    inputs.update(oil8m_idx=i8m, oil8m_shape=np.array([4, 96]))
+    # OIL4, per-128-weight blocks, each with its own codebook (rows 3 x 256)
+    r, c, B = 3, 256, 128
+    v4 = rng.integers(0, 16, r * c)
+    cbs4 = np.stack([normal_cb16(16) for _ in range(r * c // B)])
+    tensors.append(("blk.0.ffn_down.weight", len(blocks), r * c // B))
+    for b in range(r * c // B):
+        blocks.append((2, B, avx2.serialize_oil4(cbs4[b]).tobytes(), pack_nibbles(v4[b * B:(b + 1) * B]).tobytes()))
+    inputs.update(oil4_vals=v4.astype(np.uint8), oil4_cbs=cbs4, oil4_shape=np.array([r, c, B]))
+    # OIL4, one block for the whole tensor (rows 2 x 48)
+    v4s = rng.integers(0, 16, 2 * 48)
+    cb4s = normal_cb16(16)
+    tensors.append(("output.weight", len(blocks), 1))
+    blocks.append((2, 96, avx2.serialize_oil4(cb4s).tobytes(), pack_nibbles(v4s).tobytes()))
+    inputs.update(oil4s_vals=v4s.astype(np.uint8), oil4s_cb=cb4s, oil4s_shape=np.array([2, 48]))
+    # TERNARY, one block: codes q+1, 4 per byte, codebook {-1, 0, +1} as FP32
+    # (tools/convert.cpp:329-341)
+    tq = rng.integers(0, 3, 5 * 64)
+    tensors.append(("blk.1.attn_k.weight", len(blocks), 1))
+    blocks.append((1, 5 * 64, np.array([-1, 0, 1], np.float32).tobytes(), pack_codes(tq).tobytes()))
+    inputs.update(tern_codes=tq.astype(np.uint8), tern_shape=np.array([5, 64]))
+    # FP32 block (format byte 5)
+    fw = rng.standard_normal(64).astype(np.float32)
+    tensors.append(("token_norm.weight", len(blocks), 1))
+    blocks.append((5, 64, b"", fw.tobytes()))
+    inputs.update(fp32_vals=fw)
+    import tempfile
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "tiny.oil")
+        avx2.oil_write(path, b'{"arch":"mythos","n_layers":2}', blocks, tensors)
+        raw = np.fromfile(path, np.uint8)
+        reads = {f"read_{i}": avx2.oil_read_tensor(path, t[0], 1 << 16) for i, t in enumerate(tensors)}
+    save("oil_file", oil=raw, names=np.array([t[0] for t in tensors]),
+         block_start=np.array([t[1] for t in tensors]), num_blocks=np.array([t[2] for t in tensors]),
+         **inputs, **reads)
+
 
 if __name__ == "__main__":
     main()

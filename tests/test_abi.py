@@ -40,6 +40,19 @@ def test_header_matches_exports(mth):
         assert getattr(mth.lib, d) is not None
 
 
+def test_file_reader_header_matches_exports():
+    """include/mythos_oil_file.h (the .oil reader) is served by libmythos_host.so."""
+    import oil_file
+    hdr = os.path.join(ROOT, "include", "mythos_oil_file.h")
+    src = re.sub(r"/\*.*?\*/", "", open(hdr).read(), flags=re.S)
+    decl = sorted(set(re.findall(r"\b(mth_[a-z0-9_]+)\s*\(", src)))
+    assert decl == sorted(oil_file.EXPORTS)
+    syms = dynsyms(oil_file.HOST_LIB_PATH)
+    assert not [d for d in decl if d not in syms]
+    for d in decl:
+        assert getattr(oil_file.lib, d) is not None
+
+
 def test_version(mth):
     assert mth.version() >> 16 == 1
 
