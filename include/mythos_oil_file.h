@@ -51,7 +51,7 @@ extern "C" {
 #define MTH_FILE_EUNSUPPORTED (-3) /* a valid tensor this layout cannot express */
 #define MTH_FILE_EDEVICE (-4)      /* HIP error while uploading */
 
-/* .oil format byte of a block (include/oil/oil_format.h:23) */
+/* .oil format byte of a block (include/oil/types.h:17-24) */
 #define MTH_OIL_BINARY 0
 #define MTH_OIL_TERNARY 1
 #define MTH_OIL_OIL4 2
@@ -74,16 +74,25 @@ const char* mth_oil_tensor_name(const mth_oil_file* f, int64_t i);
 int mth_oil_tensor_info(const mth_oil_file* f, const char* name, int* format, int64_t* num_weights,
                         int64_t* num_blocks, int64_t* block_weights);
 
-/* Repack into host buffers (sizes in bytes; see the layouts above).
+/* Repack into host buffers (sizes in bytes; see the layouts above) as a
+ * rows x cols matrix, row = output feature (the kernels' [M][K]).
+ * in_major = 0: the file holds the weights row-major as [rows][cols] (the
+ *   converter's order, tools/convert.cpp:502-509).
+ * in_major = 1: the file holds them as the reference's Linear layer keeps its
+ *   weight in memory, input-major: element (m, k) at k*rows + m (Linear::forward
+ *   multiplies with scalar_gemm, which reads B[k*N + n], src/transformer.cpp:62-70,
+ *   src/kernel_i2s.cpp:91-102); the repack transposes.  An input-major OIL4
+ *   tensor needs one codebook for all its blocks.
  * *cb_block receives the OIL4 block length (0 = one codebook). */
-int mth_oil_repack(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, void* indices,
-                   int64_t indices_bytes, void* codebooks, int64_t codebooks_bytes, int64_t* cb_block);
+int mth_oil_repack(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, int in_major,
+                   void* indices, int64_t indices_bytes, void* codebooks, int64_t codebooks_bytes,
+                   int64_t* cb_block);
 
 /* Repack and copy into device buffers on `stream` (hipStream_t); returns when
  * the copies are complete. */
-int mth_oil_upload(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, void* d_indices,
-                   int64_t indices_bytes, void* d_codebooks, int64_t codebooks_bytes, int64_t* cb_block,
-                   void* stream);
+int mth_oil_upload(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, int in_major,
+                   void* d_indices, int64_t indices_bytes, void* d_codebooks, int64_t codebooks_bytes,
+                   int64_t* cb_block, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -128,6 +129,43 @@ size_t idx_need(int fmt, uint64_t n) {
     }
 }
 
+// Per-element codes of a tensor in file order: OIL8 index bytes, OIL4 nibbles
+// (each block's own even/odd nibble order, as OILReader::read_tensor walks
+// them, src/oil_format.cpp:444-449), ternary 2-bit codes (element j of a
+// block in bits 2(j%4) of its byte j/4, tools/convert.cpp:338-341).
+int gather_codes(const mth_oil_file* f, const Tensor* t, int fm, uint8_t* out) {
+    for (uint32_t b = t->start; b < t->start + t->count; b++) {
+        const Block& k = f->blocks[b];
+        if (k.idx_bytes < idx_need(fm, k.nw))
+            return fail(MTH_FILE_EFORMAT, "block %u of '%s': short indices", b, t->name.c_str());
+        const uint8_t* src = f->data + k.idx_off;
+        for (uint32_t j = 0; j < k.nw; j++) {
+            if (fm == MTH_OIL_OIL8) out[j] = src[j];
+            else if (fm == MTH_OIL_OIL4) out[j] = (src[j >> 1] >> ((j & 1) * 4)) & 15;
+            else out[j] = (src[j >> 2] >> ((j & 3) * 2)) & 3;
+        }
+        out += k.nw;
+    }
+    return MTH_FILE_OK;
+}
+
+// dst[r][c] = src[c][r] for a [cols][rows] source, in 64x64 tiles.
+template <typename T>
+void transpose(const T* src, T* dst, int64_t rows, int64_t cols) {
+    for (int64_t c0 = 0; c0 < cols; c0 += 64)
+        for (int64_t r0 = 0; r0 < rows; r0 += 64)
+            for (int64_t r = r0; r < std::min(rows, r0 + 64); r++)
+                for (int64_t c = c0; c < std::min(cols, c0 + 64); c++) dst[r * cols + c] = src[c * rows + r];
+}
+
+// Checks that every block of `t` carries the same codebook as its first.
+bool same_codebooks(const mth_oil_file* f, const Tensor* t, size_t off, size_t n) {
+    const Block& k0 = f->blocks[t->start];
+    for (uint32_t b = t->start + 1; b < t->start + t->count; b++)
+        if (std::memcmp(f->data + f->blocks[b].cb_off + off, f->data + k0.cb_off + off, n) != 0) return false;
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -202,8 +240,9 @@ int mth_oil_tensor_info(const mth_oil_file* f, const char* name, int* format, in
     return MTH_FILE_OK;
 }
 
-int mth_oil_repack(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, void* indices,
-                   int64_t indices_bytes, void* codebooks, int64_t codebooks_bytes, int64_t* cb_block) {
+int mth_oil_repack(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, int in_major,
+                   void* indices, int64_t indices_bytes, void* codebooks, int64_t codebooks_bytes,
+                   int64_t* cb_block) {
     int fm = 0;
     int64_t nw = 0, nb = 0, bw = 0;
     int rc = mth_oil_tensor_info(f, name, &fm, &nw, &nb, &bw);
@@ -219,22 +258,57 @@ int mth_oil_repack(const mth_oil_file* f, const char* name, int64_t rows, int64_
         return fail(MTH_FILE_EINVAL, "tensor '%s' needs %zu index bytes, buffer has %lld", name, need,
                     (long long)indices_bytes);
     if (cb_block) *cb_block = 0;
+    if ((fm == MTH_OIL_OIL4 || fm == MTH_OIL_TERNARY) && cols % (fm == MTH_OIL_OIL4 ? 2 : 4) != 0)
+        return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': rows of %lld weights do not end on a byte", name,
+                    (long long)cols);
 
-    if (fm == MTH_OIL_OIL4) {
-        if (nb > 1 && (bw <= 0 || bw % 2 != 0 || cols % bw != 0))
+    // codebook checks, shared by both orientations
+    if (fm == MTH_OIL_OIL4 || fm == MTH_OIL_OIL8) {
+        const bool o4 = fm == MTH_OIL_OIL4;
+        const uint32_t magic_want = o4 ? kMagicOil4 : kMagicOil8;
+        const size_t cbn = o4 ? 32 : 1024;
+        for (uint32_t b = t->start; b < t->start + t->count; b++) {
+            uint32_t magic = 0;
+            const Block& k = f->blocks[b];
+            if (k.cb_bytes < 4 + cbn || !f->get(k.cb_off, &magic, 4) || magic != magic_want)
+                return fail(MTH_FILE_EFORMAT, "block %u of '%s': not an %s codebook", b, name, o4 ? "OIL4" : "OIL8");
+        }
+        const bool one = same_codebooks(f, t, 4, cbn);
+        if (!o4 && !one) return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': OIL8 blocks with different codebooks", name);
+        if (o4 && in_major && !one)
+            return fail(MTH_FILE_EUNSUPPORTED,
+                        "tensor '%s': an input-major OIL4 tensor with per-block codebooks has no per-row layout", name);
+        const int64_t ncb = (o4 && !in_major) ? nb : 1;
+        if (!codebooks || codebooks_bytes < ncb * (int64_t)cbn)
+            return fail(MTH_FILE_EINVAL, "tensor '%s' needs %lld codebook bytes", name, (long long)(ncb * cbn));
+        if (o4 && !in_major && nb > 1 && (bw <= 0 || bw % 2 != 0 || cols % bw != 0))
             return fail(MTH_FILE_EUNSUPPORTED,
                         "tensor '%s': OIL4 blocks of %lld weights do not tile rows of %lld (need one length that "
                         "is even and divides the row)", name, (long long)bw, (long long)cols);
-        if (nb == 1 && nw % 2 != 0) return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': odd OIL4 length", name);
-        if (!codebooks || codebooks_bytes < nb * 32)
-            return fail(MTH_FILE_EINVAL, "tensor '%s' needs %lld codebook bytes", name, (long long)(nb * 32));
+    }
+
+    if (fm == MTH_OIL_FP32) {
+        std::vector<float> tmp(in_major ? (size_t)nw : 0);
+        float* dst = in_major ? tmp.data() : (float*)indices;
+        for (uint32_t b = t->start; b < t->start + t->count; b++) {
+            const Block& k = f->blocks[b];
+            if (k.idx_bytes < (size_t)k.nw * 4) return fail(MTH_FILE_EFORMAT, "block %u of '%s': short data", b, name);
+            f->get(k.idx_off, dst, (size_t)k.nw * 4);
+            dst += k.nw;
+        }
+        if (in_major) transpose(tmp.data(), (float*)indices, rows, cols);
+        return MTH_FILE_OK;
+    }
+    if (fm == MTH_OIL_BINARY)
+        return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': binary blocks are not on the quantized path", name);
+
+    if (fm == MTH_OIL_OIL4 && !in_major) {
+        // blocks are whole nibble pairs: copy bytes, one codebook per block
         uint8_t* cbo = (uint8_t*)codebooks;
         for (uint32_t b = t->start; b < t->start + t->count; b++) {
             const Block& k = f->blocks[b];
-            uint32_t magic = 0;
-            if (k.cb_bytes < 36 || !f->get(k.cb_off, &magic, 4) || magic != kMagicOil4)
-                return fail(MTH_FILE_EFORMAT, "block %u of '%s': not an OIL4 codebook", b, name);
-            if (k.idx_bytes < k.nw / 2) return fail(MTH_FILE_EFORMAT, "block %u of '%s': short indices", b, name);
+            if (k.nw % 2 != 0 && nb > 1) return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': odd OIL4 block", name);
+            if (k.idx_bytes < (size_t)k.nw / 2) return fail(MTH_FILE_EFORMAT, "block %u of '%s': short indices", b, name);
             f->get(k.cb_off + 4, cbo, 32);
             cbo += 32;
             f->get(k.idx_off, out, k.nw / 2);
@@ -243,64 +317,55 @@ int mth_oil_repack(const mth_oil_file* f, const char* name, int64_t rows, int64_
         if (cb_block) *cb_block = nb > 1 ? bw : 0;
         return MTH_FILE_OK;
     }
-    if (fm == MTH_OIL_OIL8) {
-        if (!codebooks || codebooks_bytes < 1024)
-            return fail(MTH_FILE_EINVAL, "tensor '%s' needs a 1024-byte codebook buffer", name);
-        const Block& k0 = f->blocks[t->start];
+    if (fm == MTH_OIL_OIL8 && !in_major) {
         for (uint32_t b = t->start; b < t->start + t->count; b++) {
             const Block& k = f->blocks[b];
-            uint32_t magic = 0;
-            if (k.cb_bytes < 1028 || !f->get(k.cb_off, &magic, 4) || magic != kMagicOil8)
-                return fail(MTH_FILE_EFORMAT, "block %u of '%s': not an OIL8 codebook", b, name);
-            if (b != t->start && std::memcmp(f->data + k.cb_off + 4, f->data + k0.cb_off + 4, 1024) != 0)
-                return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': OIL8 blocks with different codebooks", name);
             if (k.idx_bytes < k.nw) return fail(MTH_FILE_EFORMAT, "block %u of '%s': short indices", b, name);
             f->get(k.idx_off, out, k.nw);
             out += k.nw;
         }
-        f->get(k0.cb_off + 4, codebooks, 1024);
+        f->get(f->blocks[t->start].cb_off + 4, codebooks, 1024);
         return MTH_FILE_OK;
     }
-    if (fm == MTH_OIL_TERNARY) {
-        // consecutive blocks concatenate only at whole bytes
-        for (uint32_t b = t->start; b + 1 < t->start + t->count; b++)
-            if (f->blocks[b].nw % 4 != 0)
-                return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': ternary block length not a multiple of 4", name);
-        if (cols % 4 != 0) return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': row length not a multiple of 4", name);
-        for (uint32_t b = t->start; b < t->start + t->count; b++) {
-            const Block& k = f->blocks[b];
-            const size_t n = (k.nw + 3) / 4;
-            if (k.idx_bytes < n) return fail(MTH_FILE_EFORMAT, "block %u of '%s': short indices", b, name);
-            f->get(k.idx_off, out, n);
-            out += n;
-        }
-        if (codebooks && codebooks_bytes >= 12 && f->blocks[t->start].cb_bytes >= 12)
-            f->get(f->blocks[t->start].cb_off, codebooks, 12);
-        return MTH_FILE_OK;
+
+    // element-wise: ternary (either orientation), input-major OIL4 / OIL8
+    std::vector<uint8_t> codes((size_t)nw), tr;
+    rc = gather_codes(f, t, fm, codes.data());
+    if (rc != MTH_FILE_OK) return rc;
+    const uint8_t* c = codes.data();
+    if (in_major) {
+        tr.resize((size_t)nw);
+        transpose(codes.data(), tr.data(), rows, cols);
+        c = tr.data();
     }
-    if (fm == MTH_OIL_FP32) {
-        for (uint32_t b = t->start; b < t->start + t->count; b++) {
-            const Block& k = f->blocks[b];
-            if (k.idx_bytes < (size_t)k.nw * 4) return fail(MTH_FILE_EFORMAT, "block %u of '%s': short data", b, name);
-            f->get(k.idx_off, out, (size_t)k.nw * 4);
-            out += (size_t)k.nw * 4;
-        }
-        return MTH_FILE_OK;
+    if (fm == MTH_OIL_OIL8) {
+        std::memcpy(out, c, (size_t)nw);
+    } else if (fm == MTH_OIL_OIL4) {
+        for (int64_t i = 0; i < nw / 2; i++) out[i] = (uint8_t)(c[2 * i] | (c[2 * i + 1] << 4));
+    } else {
+        for (int64_t i = 0; i < nw / 4; i++)
+            out[i] = (uint8_t)(c[4 * i] | (c[4 * i + 1] << 2) | (c[4 * i + 2] << 4) | (c[4 * i + 3] << 6));
     }
-    return fail(MTH_FILE_EUNSUPPORTED, "tensor '%s': binary blocks are not on the quantized path", name);
+    if (fm == MTH_OIL_OIL4 || fm == MTH_OIL_OIL8)
+        f->get(f->blocks[t->start].cb_off + 4, codebooks, fm == MTH_OIL_OIL4 ? 32 : 1024);
+    else if (codebooks && codebooks_bytes >= 12 && f->blocks[t->start].cb_bytes >= 12)
+        f->get(f->blocks[t->start].cb_off, codebooks, 12);
+    return MTH_FILE_OK;
 }
 
-int mth_oil_upload(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, void* d_indices,
-                   int64_t indices_bytes, void* d_codebooks, int64_t codebooks_bytes, int64_t* cb_block,
-                   void* stream) {
+int mth_oil_upload(const mth_oil_file* f, const char* name, int64_t rows, int64_t cols, int in_major,
+                   void* d_indices, int64_t indices_bytes, void* d_codebooks, int64_t codebooks_bytes,
+                   int64_t* cb_block, void* stream) {
     int fm = 0;
     int64_t nw = 0, nb = 0, bw = 0;
     int rc = mth_oil_tensor_info(f, name, &fm, &nw, &nb, &bw);
     if (rc != MTH_FILE_OK) return rc;
     const size_t ib = idx_need(fm, (uint64_t)(rows * cols > 0 ? rows * cols : 0));
-    const size_t cbb = fm == MTH_OIL_OIL4 ? (size_t)nb * 32 : (fm == MTH_OIL_OIL8 ? 1024 : (fm == MTH_OIL_TERNARY ? 12 : 0));
+    const size_t cbb = fm == MTH_OIL_OIL4 ? (in_major ? 32 : (size_t)nb * 32)
+                                          : (fm == MTH_OIL_OIL8 ? 1024 : (fm == MTH_OIL_TERNARY ? 12 : 0));
     std::vector<uint8_t> hi(ib), hc(cbb ? cbb : 1);
-    rc = mth_oil_repack(f, name, rows, cols, hi.data(), (int64_t)ib, cbb ? hc.data() : nullptr, (int64_t)cbb, cb_block);
+    rc = mth_oil_repack(f, name, rows, cols, in_major, hi.data(), (int64_t)ib, cbb ? hc.data() : nullptr,
+                        (int64_t)cbb, cb_block);
     if (rc != MTH_FILE_OK) return rc;
     if ((size_t)indices_bytes < ib || (cbb && d_codebooks && (size_t)codebooks_bytes < cbb))
         return fail(MTH_FILE_EINVAL, "tensor '%s': device buffers too small (%zu + %zu bytes needed)", name, ib, cbb);

@@ -48,9 +48,9 @@ _lib.mth_oil_tensor_name.argtypes = [VP, I64]
 _lib.mth_oil_tensor_name.restype = C.c_char_p
 _lib.mth_oil_tensor_info.argtypes = [VP, C.c_char_p, C.POINTER(I32), P64, P64, P64]
 _lib.mth_oil_tensor_info.restype = I32
-_lib.mth_oil_repack.argtypes = [VP, C.c_char_p, I64, I64, VP, I64, VP, I64, P64]
+_lib.mth_oil_repack.argtypes = [VP, C.c_char_p, I64, I64, I32, VP, I64, VP, I64, P64]
 _lib.mth_oil_repack.restype = I32
-_lib.mth_oil_upload.argtypes = [VP, C.c_char_p, I64, I64, VP, I64, VP, I64, P64, VP]
+_lib.mth_oil_upload.argtypes = [VP, C.c_char_p, I64, I64, I32, VP, I64, VP, I64, P64, VP]
 _lib.mth_oil_upload.restype = I32
 lib = _lib
 
@@ -64,13 +64,13 @@ def _check(rc: int) -> None:
         raise mythos_oil.MythosError(rc, last_error())
 
 
-def layout_bytes(fmt: int, rows: int, cols: int, num_blocks: int) -> tuple[int, int]:
+def layout_bytes(fmt: int, rows: int, cols: int, num_blocks: int, in_major: bool = False) -> tuple[int, int]:
     """(index bytes, codebook bytes) of a rows x cols tensor in the kernels'
-    layout: OIL4 nibbles + 16 FP16 per block, OIL8 bytes + 256 FP32, ternary
-    2-bit codes + 3 FP32, FP32 floats."""
+    layout: OIL4 nibbles + 16 FP16 per block (one codebook when input-major),
+    OIL8 bytes + 256 FP32, ternary 2-bit codes + 3 FP32, FP32 floats."""
     n = rows * cols
     if fmt == OIL4:
-        return (n + 1) // 2, 32 * num_blocks
+        return (n + 1) // 2, 32 * (1 if in_major else num_blocks)
     if fmt == OIL8:
         return n, 1024
     if fmt == TERNARY:
@@ -126,16 +126,18 @@ class OILReader:
         return {"format": fmt.value, "num_weights": nw.value, "num_blocks": nb.value,
                 "block_weights": bw.value}
 
-    def repack(self, name: str, rows: int, cols: int):
-        """Host copy in the kernels' layout: (indices u8, codebooks, cb_block).
-        codebooks is u16 FP16 bits [blocks][16] for OIL4, f32[256] for OIL8,
-        f32[3] for ternary, None for FP32 (indices then hold the floats)."""
+    def repack(self, name: str, rows: int, cols: int, in_major: bool = False):
+        """Host copy in the kernels' layout: (indices u8, codebooks, cb_block),
+        rows = output features.  codebooks is u16 FP16 bits [blocks][16] for
+        OIL4, f32[256] for OIL8, f32[3] for ternary, None for FP32 (indices
+        then hold the floats).  in_major: the file holds the weight as the
+        reference's Linear does, element (m, k) at k*rows + m."""
         inf = self.info(name)
-        ib, cbb = layout_bytes(inf["format"], rows, cols, inf["num_blocks"])
+        ib, cbb = layout_bytes(inf["format"], rows, cols, inf["num_blocks"], in_major)
         idx = np.zeros(max(ib, 1), np.uint8)
         cbs = np.zeros(max(cbb, 4), np.uint8)
         cbk = I64(0)
-        _check(_lib.mth_oil_repack(self._need(), name.encode(), rows, cols, idx.ctypes.data, ib,
+        _check(_lib.mth_oil_repack(self._need(), name.encode(), rows, cols, int(in_major), idx.ctypes.data, ib,
                                    cbs.ctypes.data if cbb else None, cbb, C.byref(cbk)))
         idx = idx[:ib]
         fmt = inf["format"]
@@ -147,17 +149,17 @@ class OILReader:
             return idx, cbs[:12].view(np.float32), 0
         return idx.view(np.float32).reshape(rows, cols), None, 0
 
-    def upload(self, name: str, rows: int, cols: int, device="cuda", stream=None):
+    def upload(self, name: str, rows: int, cols: int, device="cuda", stream=None, in_major: bool = False):
         """Device tensors (indices, codebooks, cb_block) in the kernels'
         layout, copied on `stream` (torch's current stream by default)."""
         torch = mythos_oil._torch()
         inf = self.info(name)
         fmt = inf["format"]
-        ib, cbb = layout_bytes(fmt, rows, cols, inf["num_blocks"])
+        ib, cbb = layout_bytes(fmt, rows, cols, inf["num_blocks"], in_major)
         idx = torch.empty(ib, dtype=torch.uint8, device=device)
         cbs = torch.empty(max(cbb, 1), dtype=torch.uint8, device=device)
         cbk = I64(0)
-        _check(_lib.mth_oil_upload(self._need(), name.encode(), rows, cols, idx.data_ptr(), ib,
+        _check(_lib.mth_oil_upload(self._need(), name.encode(), rows, cols, int(in_major), idx.data_ptr(), ib,
                                    cbs.data_ptr() if cbb else None, cbb, C.byref(cbk),
                                    mythos_oil._stream(stream)))
         if fmt == OIL4:

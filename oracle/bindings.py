@@ -257,6 +257,7 @@ class Reference:
         sig = {
             "ref_oil8_gemm": [VP, VP, VP, VP, I32, I32, I32],
             "ref_oil4_gemm": [VP, VP, VP, VP, I32, I32, I32],
+            "ref_scalar_gemm": [VP, VP, VP, I32, I32, I32],
             "ref_i2s_init": [],
             "ref_i2s_gemv": [VP, F32, VP, F32, VP, I32],
             "ref_i2s_gemm": [VP, VP, VP, I32, I32, I32],
@@ -301,6 +302,13 @@ class Reference:
         out = np.empty(M * N, np.float32)
         self.lib.ref_oil4_gemm(_p(nib, np.uint8), _p(cb16, np.uint16), _p(act, np.float32),
                                _p(out, np.float32), M, N, K)
+        return out
+
+    def scalar_gemm(self, A, B, M, N, K):
+        """kernel::scalar_gemm: C[M][N] = A[M][K] @ B, B read as B[k*N + n]."""
+        _need(A, M * K, "A"); _need(B, K * N, "B")
+        out = np.empty(M * N, np.float32)
+        self.lib.ref_scalar_gemm(_p(A, np.float32), _p(B, np.float32), _p(out, np.float32), M, N, K)
         return out
 
     def i2s_init(self):

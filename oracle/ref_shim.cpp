@@ -40,6 +40,12 @@ void ref_oil8_gemm(const uint8_t* idx, const float* cb, const float* act, float*
     kernel::oil8_gemm(idx, cb, act, out, M, N, K);
 }
 
+// kernel::scalar_gemm (src/kernel_i2s.cpp:91-102): C[m][n] = sum_k A[m*K+k]*B[k*N+n],
+// the product Linear::forward uses (src/transformer.cpp:62-70).
+void ref_scalar_gemm(const float* A, const float* B, float* C, int M, int N, int K) {
+    kernel::scalar_gemm(A, B, C, M, N, K);
+}
+
 void ref_oil4_gemm(const uint8_t* nib, const uint16_t* cb, const float* act, float* out,
                    int M, int N, int K) {
     kernel::oil4_gemm(nib, cb, act, out, M, N, K);

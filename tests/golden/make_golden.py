@@ -237,6 +237,35 @@ def main() -> None:
          block_start=np.array([t[1] for t in tensors]), num_blocks=np.array([t[2] for t in tensors]),
          **inputs, **reads)
 
+    # ---- Linear weights as the reference's model keeps them ----------------
+    # Linear::forward (src/transformer.cpp:62-70) multiplies with scalar_gemm,
+    # which reads the weight input-major: element (out n, in k) at k*out + n.
+    # A file holding such weights, the reference's read_tensor of each, and
+    # scalar_gemm(x, W) as Linear::forward computes it.
+    out_f, in_f, nb_tok = 48, 64, 3
+    xl = rng.standard_normal((nb_tok, in_f)).astype(np.float32)
+    l8 = rng.integers(0, 256, in_f * out_f, dtype=np.uint8)
+    l4 = rng.integers(0, 16, in_f * out_f)
+    l4cb = normal_cb16(16)
+    lf = (rng.standard_normal(in_f * out_f) * 0.05).astype(np.float32)
+    half = in_f * out_f // 2
+    lblocks = [(3, in_f * out_f, avx2.serialize_oil8(cb8).tobytes(), l8.tobytes()),
+               (2, half, avx2.serialize_oil4(l4cb).tobytes(), pack_nibbles(l4[:half]).tobytes()),
+               (2, half, avx2.serialize_oil4(l4cb).tobytes(), pack_nibbles(l4[half:]).tobytes()),
+               (5, half, b"", lf[:half].tobytes()),                  # DenseModel::save splits FP32
+               (5, half, b"", lf[half:].tobytes())]                  # tensors into blocks
+    ltensors = [("layers.0.attention.q_proj.weight", 0, 1), ("layers.0.ffn.up_proj.weight", 1, 2),
+                ("layers.0.attention.o_proj.weight", 3, 2)]
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "linear.oil")
+        avx2.oil_write(path, b"", lblocks, ltensors)
+        lraw = np.fromfile(path, np.uint8)
+        lw = [avx2.oil_read_tensor(path, t[0], 1 << 16) for t in ltensors]
+    save("oil_linear", oil=lraw, shape=np.array([out_f, in_f, nb_tok]), x=xl, idx8=l8, cb8=cb8,
+         vals4=l4.astype(np.uint8), cb4=l4cb, fp32=lf,
+         **{f"w_{i}": w for i, w in enumerate(lw)},
+         **{f"y_{i}": avx2.scalar_gemm(xl, w, nb_tok, out_f, in_f) for i, w in enumerate(lw)})
+
 
 if __name__ == "__main__":
     main()

@@ -101,3 +101,30 @@ def test_ternary_upload_gemv_bit_exact(model, oracle, mth, dev):
     torch.cuda.synchronize()
     ref = oracle.i2s_gemv_f32(tpk.ravel(), 1.0, x, M, K, 2, threads=8)
     assert np.array_equal(y.cpu().numpy().reshape(2, M), ref)
+
+
+def test_linear_weights_reproduce_reference_forward(oracle, mth, dev, tmp_path):
+    """Input-major Linear weights (the reference model's layout) uploaded with
+    in_major give the reference's Linear::forward outputs (golden y)."""
+    import os
+    import torch
+    import oil_file
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "oil_linear.npz"))
+    p = tmp_path / "linear.oil"
+    g["oil"].tofile(p)
+    M, K, nt = (int(v) for v in g["shape"])
+    print(f"oil upload linear M={M} K={K} batch={nt}", flush=True)
+    x = g["x"]
+    dx = torch.from_numpy(x.copy()).to(dev)
+    with oil_file.OILReader(str(p)) as r:
+        d_idx, d_cb, _ = r.upload("layers.0.attention.q_proj.weight", M, K, dev, in_major=True)
+        d_nib, d_cb4, cbk = r.upload("layers.0.ffn.up_proj.weight", M, K, dev, in_major=True)
+    y8 = torch.full((nt * M,), float("nan"), device=dev)
+    y4 = torch.full((nt * M,), float("nan"), device=dev)
+    mth.oil8_gemv(d_idx, d_cb, dx, y8, M, K, nt)
+    mth.oil4_gemv(d_nib, d_cb4, cbk, dx, y4, M, K, nt)
+    torch.cuda.synchronize()
+    for i, y in ((0, y8), (1, y4)):
+        w = g[f"w_{i}"].reshape(K, M).astype(np.float64)        # reader's tensor, input-major
+        absw = np.abs(x.astype(np.float64)) @ np.abs(w)
+        fp32_close(y.cpu().numpy().reshape(nt, M), g[f"y_{i}"].reshape(nt, M), absw, 1e-5, f"linear {i}")

@@ -216,9 +216,9 @@ def test_argument_errors(of, gold, oil_path, tmp_path):
     # buffers smaller than the layout are refused, not overrun
     idx = np.zeros(8, np.uint8)
     cb = np.zeros(1024, np.uint8)
-    rc = of.lib.mth_oil_repack(r._h, b"blk.0.attn_q.weight", 6, 40, idx.ctypes.data, 8, cb.ctypes.data, 1024, None)
+    rc = of.lib.mth_oil_repack(r._h, b"blk.0.attn_q.weight", 6, 40, 0, idx.ctypes.data, 8, cb.ctypes.data, 1024, None)
     assert rc == of.EINVAL and "index bytes" in of.last_error()
-    rc = of.lib.mth_oil_repack(r._h, b"blk.0.ffn_down.weight", 3, 256, np.zeros(384, np.uint8).ctypes.data, 384,
+    rc = of.lib.mth_oil_repack(r._h, b"blk.0.ffn_down.weight", 3, 256, 0, np.zeros(384, np.uint8).ctypes.data, 384,
                                cb.ctypes.data, 100, None)
     assert rc == of.EINVAL and "codebook bytes" in of.last_error()
     # OIL8 blocks of one tensor with different codebooks
@@ -232,3 +232,61 @@ def test_argument_errors(of, gold, oil_path, tmp_path):
     r.close()
     with pytest.raises(MythosError):
         r.tensor_names()
+
+
+# ---- Linear weights (input-major, as the reference's model holds them) ----
+@pytest.fixture(scope="module")
+def lin(tmp_path_factory):
+    g = np.load(os.path.join(GOLD, "oil_linear.npz"))
+    p = tmp_path_factory.mktemp("lin") / "linear.oil"
+    g["oil"].tofile(p)
+    return g, str(p)
+
+
+def test_linear_orientation_matches_reference_forward(of, oracle, lin):
+    """Repacked with in_major, W[m][k] @ x reproduces the reference's
+    Linear::forward product scalar_gemm(x, W) for OIL8, OIL4 and FP32."""
+    g, path = lin
+    out_f, in_f, nt = (int(v) for v in g["shape"])
+    x = g["x"].astype(np.float64)
+    with of.OILReader(path) as r:
+        idx, cb, _ = r.repack("layers.0.attention.q_proj.weight", out_f, in_f, in_major=True)
+        nib, cb4, cbk = r.repack("layers.0.ffn.up_proj.weight", out_f, in_f, in_major=True)
+        wf, _, _ = r.repack("layers.0.attention.o_proj.weight", out_f, in_f, in_major=True)
+        # the same bytes read output-major are the transpose
+        idx_t, _, _ = r.repack("layers.0.attention.q_proj.weight", in_f, out_f)
+    assert np.array_equal(idx, idx_t.T)
+    assert np.array_equal(idx.T.ravel(), g["idx8"])
+    assert cbk == 0 and cb4.shape == (1, 16) and np.array_equal(cb4[0], g["cb4"])
+    v = np.stack([nib & 15, nib >> 4], -1).reshape(out_f, in_f)
+    assert np.array_equal(v.T.ravel(), g["vals4"])
+    w8 = cb[idx]
+    w4 = np.vectorize(oracle.half_to_float_codebook, otypes=[np.float32])(cb4[0][v])
+    for i, w in enumerate((w8, w4, wf)):
+        # the repacked weight is the reference reader's tensor, transposed
+        assert np.array_equal(w.T.ravel().view(np.uint32), g[f"w_{i}"].view(np.uint32)), i
+        y = (x @ w.astype(np.float64).T).ravel()
+        absw = (np.abs(x) @ np.abs(w.astype(np.float64)).T).ravel()
+        assert np.all(np.abs(y - g[f"y_{i}"]) <= 1e-6 * absw + 1e-30), i
+
+
+def test_linear_oil4_needs_one_codebook(of, gold, oil_path):
+    from mythos_oil import MythosError
+    with of.OILReader(oil_path) as r:
+        with pytest.raises(MythosError, match="input-major OIL4") as e:
+            r.repack("blk.0.ffn_down.weight", 128, 6, in_major=True)
+        assert e.value.code == of.EUNSUPPORTED
+        # a single-codebook OIL4 tensor transposes element by element
+        nib, _, _ = r.repack("output.weight", 48, 2, in_major=True)
+    v = np.stack([nib & 15, nib >> 4], -1).reshape(48, 2)
+    assert np.array_equal(v.T.ravel(), gold["oil4s_vals"])
+
+
+def test_ternary_in_major(of, gold, tmp_path):
+    c = gold["tern_codes"].reshape(16, 20)           # file order [in=16][out=20]
+    p = tmp_path / "t.oil"
+    write_oil(p, b"", [(1, 320, np.array([-1, 0, 1], "<f4").tobytes(), pack_codes(c).tobytes())],
+              [("w", 0, 1)])
+    with of.OILReader(str(p)) as r:
+        codes, _, _ = r.repack("w", 20, 16, in_major=True)
+    assert np.array_equal(codes, pack_codes(c.T))
