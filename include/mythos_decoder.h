@@ -1,0 +1,98 @@
+/*
+ * mythos_decoder.h — the mixed-format decoder stack on one MI355X
+ * (libmythos_oil.so): Q/K/V/O and lm_head OIL8, FFN gate/up OIL4 with
+ * per-block codebooks, FFN down ternary I2_S with per-token int8 activations,
+ * RMSNorm, rotary embedding, attention over an FP32 KV cache, greedy argmax.
+ *
+ * Replaces, for this weight format mix, the reference's inference path
+ * DenseModel::forward (src/model.cpp:45-75) -> TransformerBlock::forward
+ * (src/transformer.cpp:396-406) -> Attention::forward inference branch
+ * (:154-362) / FFN::forward (:373-387), driven token by token as
+ * Generator::generate_tokens does (src/generator.cpp:14-64) with
+ * Sampler::greedy (src/sampler.cpp:12-22).  Semantics that differ on purpose:
+ * every layer rotates at the token's own position (the reference reads layer
+ * 0's cache length, src/kv_cache.cpp:190-192); the softmax uses exp (not the
+ * AVX2 build's Taylor polynomial, src/transformer.cpp:255-276); one KV cache
+ * per sequence of the batch (the reference's is batch-1); weights are
+ * [out][in] rows (the reference Linear holds them input-major).
+ *
+ * The caller owns the weights (device pointers, kernels' layouts as in
+ * mythos_oil.h) and must keep them alive while the decoder runs.  The decoder
+ * owns its KV cache, activations and token history, allocated on the current
+ * device at create.  One step feeds one token per sequence: step s reads
+ * token hist[b][s] (the prompt while s < prompt_len, then the previous step's
+ * argmax), runs the stack at position s, and writes logits[b][vocab] and
+ * hist[b][s + 1].  The step counter lives on the device, so a step is one
+ * fixed launch sequence, replayed as a HIP graph.  Calls on one decoder must
+ * be ordered on one stream.
+ */
+#ifndef MYTHOS_DECODER_H
+#define MYTHOS_DECODER_H
+
+#include <stdint.h>
+
+#include "mythos_oil.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mth_decoder mth_decoder;
+
+typedef struct {
+    int64_t vocab, hidden, layers, heads, kv_heads, head_dim, ffn;
+    int64_t max_seq;   /* KV-cache positions per sequence (prompt + generated) */
+    int64_t cb_block;  /* OIL4 codebook block length (0 = one codebook per tensor) */
+    int64_t max_batch; /* sequences decoded together, 1..16 */
+    float eps, theta;  /* RMSNorm epsilon, RoPE base */
+} mth_decoder_config;
+
+typedef struct {
+    const float* attn_norm;   /* [hidden] */
+    const float* ffn_norm;    /* [hidden] */
+    const uint8_t *wq, *wk, *wv, *wo; /* OIL8 [out][in] indices */
+    const float *cbq, *cbk, *cbv, *cbo; /* 256-entry FP32 codebooks */
+    /* OIL4 [ffn][hidden/2] nibbles and [ffn][hidden/cb_block][16] FP16
+     * codebooks.  When wup directly follows wgate (and cbup cbgate) in memory,
+     * both run as one launch over 2*ffn rows. */
+    const uint8_t *wgate, *wup;
+    const uint16_t *cbgate, *cbup;
+    const uint8_t* wdown;     /* I2_S [hidden][ffn/4] */
+    float down_scale;
+} mth_decoder_layer;
+
+typedef struct {
+    const float* emb;         /* [vocab][hidden] FP32 */
+    const float* final_norm;  /* [hidden] */
+    const uint8_t* lm_idx;    /* OIL8 [vocab][hidden] */
+    const float* lm_cb;
+} mth_decoder_globals;
+
+int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out);
+void mth_decoder_destroy(mth_decoder* d);
+int mth_decoder_set_layer(mth_decoder* d, int64_t layer, const mth_decoder_layer* w);
+int mth_decoder_set_globals(mth_decoder* d, const mth_decoder_globals* g);
+
+/* Starts `batch` sequences: prompts [batch][prompt_len] int32 token ids
+ * (device), 1 <= prompt_len <= max_seq.  Resets the step counter. */
+int mth_decoder_start(mth_decoder* d, const int32_t* prompts, int64_t batch, int64_t prompt_len, mth_stream_t stream);
+
+/* Runs n steps (n + steps already run <= max_seq).  use_graph: capture one
+ * step into a HIP graph on first use and replay it. */
+int mth_decoder_step(mth_decoder* d, int64_t n, int use_graph, mth_stream_t stream);
+
+/* Device buffers: logits [batch][vocab] of the last step, and the token
+ * history [batch][max_seq + 1] (row b: prompt, then generated ids). */
+int mth_decoder_buffers(const mth_decoder* d, float** logits, int32_t** hist, int64_t* hist_stride);
+
+/* Host copies (synchronous, after the stream's queued work): logits
+ * [batch][vocab] and token history [batch][max_seq + 1]; either may be null. */
+int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_stream_t stream);
+
+/* Steps run since the last start (host-side count). */
+int64_t mth_decoder_steps_done(const mth_decoder* d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

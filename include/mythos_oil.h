@@ -146,6 +146,60 @@ int mth_tl2_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int6
  * (w0, w1[, w2]) in {-1,0,1}^group, row-major, = clamp_int8(sum a_i*w_i). */
 int mth_tl_precompute_lut(const int8_t* act, int8_t* lut, int64_t K, int group, mth_stream_t stream);
 
+/* ---- FP32 decode-step operators (config-5 decoder) ----------------------- */
+
+/* oil::math::rms_norm (include/oil/math.h:24, src/math.cpp:182-205) over rows
+ * of dim: double sum of squares, y = (float)(x / sqrt(ss/dim + eps)) * gamma.
+ * y may equal x. */
+int mth_rms_norm(const float* x, const float* gamma, float* y, int64_t rows, int64_t dim, float eps,
+                 mth_stream_t stream);
+
+/* TransformerBlock's residual add then the next RMSNorm (src/transformer.cpp:
+ * 402-405, math::add + math::rms_norm in one pass): x <- t + x, y = rms_norm(x). */
+int mth_add_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim, float eps,
+                     mth_stream_t stream);
+
+/* oil::math::silu (src/math.cpp:119-128): y = x / (1 + exp(-x)). */
+int mth_silu(const float* x, float* y, int64_t n, mth_stream_t stream);
+
+/* FFN::forward's activation (src/transformer.cpp:377-386): silu(g) then
+ * math::mul with u, over rows of n (row r of g at g + r*gstride, of u at
+ * u + r*ustride); y is [rows][n]. */
+int mth_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t n, int64_t gstride,
+                 int64_t ustride, mth_stream_t stream);
+
+/* oil::math::add / mul (src/math.cpp:251-258, :269-276). */
+int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);
+int mth_mul(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);
+
+/* oil::math::softmax over the last axis of [rows][dim] (src/math.cpp:207-249). */
+int mth_softmax(const float* x, float* y, int64_t rows, int64_t dim, mth_stream_t stream);
+
+/* RotaryEmbedding tables (src/transformer.cpp:102-117), computed on the host
+ * in float: cos/sin [max_seq][head_dim/2] (host buffers). */
+int mth_rope_tables(int64_t head_dim, int64_t max_seq, float theta, float* cos_t, float* sin_t);
+
+/* RotaryEmbedding::apply (src/transformer.cpp:119-139) for one token per
+ * sequence at position pos, plus KVCache::append (src/kv_cache.cpp:78-137):
+ * q [batch][heads][head_dim] rotated in place; k rotated and v copied to
+ * kcache/vcache [batch][kv_heads][max_seq][head_dim] at row pos.  cos_t/sin_t
+ * are device copies of mth_rope_tables. */
+int mth_rope_kv(float* q, const float* k, const float* v, const float* cos_t, const float* sin_t, float* kcache,
+                float* vcache, int64_t pos, int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                int64_t max_seq, mth_stream_t stream);
+
+/* Attention::forward's inference branch for one query token per sequence
+ * (src/transformer.cpp:188-348 with S = 1, scalar softmax): head h attends to
+ * cached positions 0..ctx-1 of kv head h % kv_heads, scale 1/sqrt(head_dim);
+ * out [batch][heads][head_dim].  head_dim 64, 128 or 256; ctx <= max_seq <= 16384. */
+int mth_attention_decode(const float* q, const float* kcache, const float* vcache, float* out, int64_t batch,
+                         int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t ctx, int64_t max_seq,
+                         mth_stream_t stream);
+
+/* Sampler::greedy (src/sampler.cpp:12-22) per row of logits [rows][n]: the
+ * first index of the maximum (NaN never wins). */
+int mth_argmax(const float* logits, int32_t* ids, int64_t rows, int64_t n, mth_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,7 @@
 // nothing here throws across the C boundary.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -84,6 +85,17 @@ hipError_t bt_workspace(hipStream_t s, int64_t M, int64_t K, float** partial) {
     } while (0)
 
 }  // namespace
+
+namespace mth {
+int api_fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+int api_ok() { return ok(); }
+}  // namespace mth
 
 extern "C" {
 
@@ -225,6 +237,108 @@ int mth_tl2_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int6
     REQUIRE(M > 0 && N > 0 && K > 0 && M * N < kMaxDim && K < (1ll << 24), "mth_tl2_gemm: bad sizes");
     REQUIRE(K % 3 == 0, "mth_tl2_gemm: K=%lld must be a multiple of 3", (long long)K);
     return check_launch(mth::launch_tl2_gemm(w, act, out, M, N, K, S(stream)), "mth_tl2_gemm");
+}
+
+// ---- FP32 decode-step operators -------------------------------------------
+int mth_rms_norm(const float* x, const float* gamma, float* y, int64_t rows, int64_t dim, float eps,
+                 mth_stream_t stream) {
+    REQUIRE(x && gamma && y, "mth_rms_norm: null pointer");
+    REQUIRE(rows > 0 && rows < (1ll << 31) && dim > 0 && dim < kMaxDim, "mth_rms_norm: bad sizes");
+    REQUIRE(eps >= 0.0f, "mth_rms_norm: eps < 0");
+    return check_launch(mth::launch_rms_norm((float*)x, nullptr, gamma, y, rows, dim, eps, S(stream)),
+                        "mth_rms_norm");
+}
+
+int mth_add_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim, float eps,
+                     mth_stream_t stream) {
+    REQUIRE(x && t && gamma && y, "mth_add_rms_norm: null pointer");
+    REQUIRE(rows > 0 && rows < (1ll << 31) && dim > 0 && dim < kMaxDim, "mth_add_rms_norm: bad sizes");
+    REQUIRE(eps >= 0.0f, "mth_add_rms_norm: eps < 0");
+    return check_launch(mth::launch_rms_norm(x, t, gamma, y, rows, dim, eps, S(stream)), "mth_add_rms_norm");
+}
+
+int mth_silu(const float* x, float* y, int64_t n, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_silu: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_silu: bad size");
+    return check_launch(mth::launch_silu(x, y, n, S(stream)), "mth_silu");
+}
+
+int mth_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t n, int64_t gstride,
+                 int64_t ustride, mth_stream_t stream) {
+    REQUIRE(g && u && y, "mth_silu_mul: null pointer");
+    REQUIRE(rows > 0 && rows <= 65535 && n > 0 && n < (1ll << 31) && gstride >= n && ustride >= n,
+            "mth_silu_mul: bad sizes");
+    return check_launch(mth::launch_silu_mul(g, u, y, rows, n, gstride, ustride, S(stream)), "mth_silu_mul");
+}
+
+int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream) {
+    REQUIRE(a && b && c, "mth_add: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_add: bad size");
+    return check_launch(mth::launch_add(a, b, c, n, S(stream)), "mth_add");
+}
+
+int mth_mul(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream) {
+    REQUIRE(a && b && c, "mth_mul: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_mul: bad size");
+    return check_launch(mth::launch_mul(a, b, c, n, S(stream)), "mth_mul");
+}
+
+int mth_softmax(const float* x, float* y, int64_t rows, int64_t dim, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_softmax: null pointer");
+    REQUIRE(rows > 0 && rows < (1ll << 31) && dim > 0 && dim < kMaxDim, "mth_softmax: bad sizes");
+    return check_launch(mth::launch_softmax(x, y, rows, dim, S(stream)), "mth_softmax");
+}
+
+int mth_rope_tables(int64_t head_dim, int64_t max_seq, float theta, float* cos_t, float* sin_t) {
+    REQUIRE(cos_t && sin_t, "mth_rope_tables: null pointer");
+    REQUIRE(head_dim > 0 && head_dim % 2 == 0 && max_seq > 0 && head_dim * max_seq < kMaxDim,
+            "mth_rope_tables: bad sizes");
+    REQUIRE(theta > 0.0f, "mth_rope_tables: theta <= 0");
+    const int64_t h2 = head_dim / 2;
+    for (int64_t i = 0; i < max_seq; i++)
+        for (int64_t j = 0; j < h2; j++) {
+            const float inv_freq = 1.0f / std::pow(theta, (float)(2 * j) / (float)head_dim);
+            const float val = (float)i * inv_freq;
+            cos_t[i * h2 + j] = std::cos(val);
+            sin_t[i * h2 + j] = std::sin(val);
+        }
+    return ok();
+}
+
+int mth_rope_kv(float* q, const float* k, const float* v, const float* cos_t, const float* sin_t, float* kcache,
+                float* vcache, int64_t pos, int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                int64_t max_seq, mth_stream_t stream) {
+    REQUIRE(q && k && v && cos_t && sin_t && kcache && vcache, "mth_rope_kv: null pointer");
+    REQUIRE(batch > 0 && batch <= 65535 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 &&
+                heads * head_dim < (1ll << 24) && max_seq > 0 && max_seq < (1ll << 24),
+            "mth_rope_kv: bad sizes");
+    REQUIRE(pos >= 0 && pos < max_seq, "mth_rope_kv: pos=%lld outside 0..%lld", (long long)pos,
+            (long long)max_seq - 1);
+    return check_launch(mth::launch_rope_kv(q, k, v, cos_t, sin_t, kcache, vcache, nullptr, (int)pos, batch,
+                                            (int)heads, (int)kv_heads, (int)head_dim, (int)max_seq, S(stream)),
+                        "mth_rope_kv");
+}
+
+int mth_attention_decode(const float* q, const float* kcache, const float* vcache, float* out, int64_t batch,
+                         int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t ctx, int64_t max_seq,
+                         mth_stream_t stream) {
+    REQUIRE(q && kcache && vcache && out, "mth_attention_decode: null pointer");
+    REQUIRE(batch > 0 && batch <= 65535 && heads > 0 && heads <= 65535 && kv_heads > 0 && heads % kv_heads == 0,
+            "mth_attention_decode: bad head counts");
+    REQUIRE(max_seq > 0 && mth::attention_supported((int)head_dim, (int)max_seq),
+            "mth_attention_decode: head_dim=%lld max_seq=%lld (head_dim 64/128/256, max_seq <= 16384)",
+            (long long)head_dim, (long long)max_seq);
+    REQUIRE(ctx >= 1 && ctx <= max_seq, "mth_attention_decode: ctx=%lld outside 1..%lld", (long long)ctx,
+            (long long)max_seq);
+    return check_launch(mth::launch_attention(q, kcache, vcache, out, nullptr, (int)ctx - 1, batch, (int)heads,
+                                              (int)kv_heads, (int)head_dim, (int)max_seq, S(stream)),
+                        "mth_attention_decode");
+}
+
+int mth_argmax(const float* logits, int32_t* ids, int64_t rows, int64_t n, mth_stream_t stream) {
+    REQUIRE(logits && ids, "mth_argmax: null pointer");
+    REQUIRE(rows > 0 && rows < (1ll << 31) && n > 0 && n < (1ll << 31), "mth_argmax: bad sizes");
+    return check_launch(mth::launch_argmax(logits, rows, n, ids, nullptr, nullptr, 0, 0, S(stream)), "mth_argmax");
 }
 
 }  // extern "C"

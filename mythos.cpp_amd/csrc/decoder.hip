@@ -1,0 +1,312 @@
+// decoder.hip — the mixed-format decoder stack (include/mythos_decoder.h).
+//
+// One decode step for B sequences is a fixed sequence of launches on one
+// stream (per layer: RMSNorm, Q/K/V OIL8 GEMVs, RoPE + KV append, attention,
+// O GEMV, residual add fused into the FFN RMSNorm, gate/up OIL4 GEMV (one
+// launch over 2*ffn rows when gate and up are adjacent), SwiGLU, ternary down
+// GEMV with per-token int8 quantisation fused in; the next layer's RMSNorm
+// takes the second residual add).  Everything that changes from step to step
+// (position, input token) is read from device memory: the step counter and
+// the token history.  So the sequence captures into one HIP graph that is
+// replayed for every step.  All buffers are allocated at create; the graph
+// holds no memset nodes and no allocations.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <vector>
+
+#include "launch.h"
+#include "../../include/mythos_decoder.h"
+
+struct mth_decoder {
+    mth_decoder_config c{};
+    int device = 0;
+    std::vector<mth_decoder_layer> layers;
+    std::vector<bool> layer_set;
+    mth_decoder_globals g{};
+    bool globals_set = false;
+
+    void* block = nullptr;  // one device allocation for every buffer below
+    float *x = nullptr, *h = nullptr, *t = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
+    float *gu = nullptr, *a = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr;
+    int *hist = nullptr, *step = nullptr, *ids = nullptr;
+    int64_t hist_stride = 0, layer_kv = 0;
+
+    int64_t batch = 0, prompt_len = 0, steps = 0;
+    hipStream_t cap_stream = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int64_t graph_batch = 0, graph_prompt = 0;
+
+    void drop_graph() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+    }
+};
+
+namespace {
+
+using mth::api_fail;
+using mth::api_ok;
+
+size_t round_up(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// y[B][M] = W x for an OIL4 weight, picking the batched kernel when it applies.
+hipError_t oil4(const mth_decoder* d, const uint8_t* w, const uint16_t* cb, const float* x, float* y, int64_t M,
+                int64_t K, hipStream_t s) {
+    const bool aligned = (((uintptr_t)w | (uintptr_t)cb | (uintptr_t)x) & 15u) == 0;
+    if (aligned && mth::oil4_bt_supported(M, K, d->c.cb_block, d->batch))
+        return mth::launch_oil4_gemv_bt(w, cb, d->c.cb_block, x, y, M, K, d->batch, d->bt_partial, s);
+    return mth::launch_oil4_gemv(w, cb, d->c.cb_block, x, y, M, K, d->batch, s);
+}
+
+hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
+    const mth_decoder_config& c = d->c;
+    const int64_t B = d->batch, H = c.hidden, F = c.ffn, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    hipError_t e;
+#define TRY(call)                        \
+    do {                                 \
+        if ((e = (call)) != hipSuccess) return e; \
+    } while (0)
+    TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, B, (int)H, (int)c.vocab, s));
+    for (int64_t l = 0; l < c.layers; l++) {
+        const mth_decoder_layer& L = d->layers[(size_t)l];
+        float* kc = d->kc + l * d->layer_kv;
+        float* vc = d->vc + l * d->layer_kv;
+        // residual of the previous layer's FFN folded into this norm
+        TRY(mth::launch_rms_norm(d->x, l == 0 ? nullptr : d->t, L.attn_norm, d->h, B, H, c.eps, s));
+        TRY(mth::launch_oil8_gemv(L.wq, L.cbq, d->h, d->q, QD, H, B, s));
+        TRY(mth::launch_oil8_gemv(L.wk, L.cbk, d->h, d->k, KD, H, B, s));
+        TRY(mth::launch_oil8_gemv(L.wv, L.cbv, d->h, d->v, KD, H, B, s));
+        TRY(mth::launch_rope_kv(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, d->step, 0, B, (int)c.heads,
+                                (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
+        TRY(mth::launch_attention(d->q, kc, vc, d->att, d->step, 0, B, (int)c.heads, (int)c.kv_heads,
+                                  (int)c.head_dim, (int)c.max_seq, s));
+        TRY(mth::launch_oil8_gemv(L.wo, L.cbo, d->att, d->t, H, QD, B, s));
+        TRY(mth::launch_rms_norm(d->x, d->t, L.ffn_norm, d->h, B, H, c.eps, s));
+        const int64_t nb = c.cb_block ? H / c.cb_block : 1;
+        const bool fused = L.wup == L.wgate + F * (H / 2) && (c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
+        if (fused) {
+            TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
+            TRY(mth::launch_silu_mul(d->gu, d->gu + F, d->a, B, F, 2 * F, 2 * F, s));
+        } else {
+            TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
+            TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
+            TRY(mth::launch_silu_mul(d->gu, d->gu + B * F, d->a, B, F, F, F, s));
+        }
+        TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, d->a, nullptr, nullptr, d->t, H, F, B, s));
+    }
+    TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
+    TRY(mth::launch_oil8_gemv(d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, B, s));
+    TRY(mth::launch_argmax(d->logits, B, c.vocab, d->ids, d->hist, d->step, (int)d->hist_stride, (int)d->prompt_len,
+                           s));
+    TRY(mth::launch_advance(d->step, s));
+#undef TRY
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
+    if (!cfg || !out) return api_fail(MTH_EINVAL, "mth_decoder_create: null pointer");
+    *out = nullptr;
+    const mth_decoder_config& c = *cfg;
+    if (c.vocab <= 0 || c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 ||
+        c.head_dim <= 0 || c.max_seq <= 0 || c.vocab >= (1ll << 31) || c.hidden >= (1ll << 24) ||
+        c.ffn >= (1ll << 24) || c.layers > 4096)
+        return api_fail(MTH_EINVAL, "mth_decoder_create: bad sizes");
+    if (c.max_batch < 1 || c.max_batch > 16)
+        return api_fail(MTH_EINVAL, "mth_decoder_create: max_batch=%lld outside 1..16", (long long)c.max_batch);
+    if (c.hidden % 4 != 0 || c.ffn % 4 != 0)
+        return api_fail(MTH_EINVAL, "mth_decoder_create: hidden and ffn must be multiples of 4");
+    if (c.heads % c.kv_heads != 0) return api_fail(MTH_EINVAL, "mth_decoder_create: heads %% kv_heads != 0");
+    if (c.cb_block < 0 || (c.cb_block > 0 && c.hidden % c.cb_block != 0))
+        return api_fail(MTH_EINVAL, "mth_decoder_create: cb_block=%lld does not divide hidden", (long long)c.cb_block);
+    if (!mth::attention_supported((int)c.head_dim, (int)c.max_seq))
+        return api_fail(MTH_EUNSUPPORTED, "mth_decoder_create: head_dim=%lld / max_seq=%lld not supported "
+                                          "(head_dim 64, 128 or 256; max_seq <= 16384)",
+                        (long long)c.head_dim, (long long)c.max_seq);
+    if (!(c.eps >= 0.0f) || !(c.theta > 0.0f)) return api_fail(MTH_EINVAL, "mth_decoder_create: bad eps/theta");
+
+    mth_decoder* d = new mth_decoder;
+    d->c = c;
+    d->layers.assign((size_t)c.layers, mth_decoder_layer{});
+    d->layer_set.assign((size_t)c.layers, false);
+    hipError_t e = hipGetDevice(&d->device);
+    const int64_t B = c.max_batch, H = c.hidden, F = c.ffn;
+    const int64_t QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    d->hist_stride = c.max_seq + 1;
+    d->layer_kv = B * KD * c.max_seq;
+    const size_t partial = mth::oil4_bt_partial_bytes(2 * F, H);
+    struct Slot {
+        void** p;
+        size_t bytes;
+    } slots[] = {
+        {(void**)&d->x, (size_t)(B * H) * 4},       {(void**)&d->h, (size_t)(B * H) * 4},
+        {(void**)&d->t, (size_t)(B * H) * 4},       {(void**)&d->q, (size_t)(B * QD) * 4},
+        {(void**)&d->k, (size_t)(B * KD) * 4},      {(void**)&d->v, (size_t)(B * KD) * 4},
+        {(void**)&d->att, (size_t)(B * QD) * 4},    {(void**)&d->gu, (size_t)(B * 2 * F) * 4},
+        {(void**)&d->a, (size_t)(B * F) * 4},       {(void**)&d->logits, (size_t)(B * c.vocab) * 4},
+        {(void**)&d->kc, (size_t)(c.layers * d->layer_kv) * 4},
+        {(void**)&d->vc, (size_t)(c.layers * d->layer_kv) * 4},
+        {(void**)&d->rope_cos, (size_t)(c.max_seq * (c.head_dim / 2)) * 4},
+        {(void**)&d->rope_sin, (size_t)(c.max_seq * (c.head_dim / 2)) * 4},
+        {(void**)&d->bt_partial, partial},
+        {(void**)&d->hist, (size_t)(B * d->hist_stride) * 4},
+        {(void**)&d->step, 4},                      {(void**)&d->ids, (size_t)B * 4},
+    };
+    size_t total = 0;
+    for (const Slot& sl : slots) total += round_up(sl.bytes);
+    if (e == hipSuccess) e = hipMalloc(&d->block, total);
+    if (e != hipSuccess) {
+        delete d;
+        return api_fail(MTH_EDEVICE, "mth_decoder_create: allocating %zu bytes failed: %s", total,
+                        hipGetErrorString(e));
+    }
+    size_t off = 0;
+    for (const Slot& sl : slots) {
+        *sl.p = sl.bytes ? (char*)d->block + off : nullptr;
+        off += round_up(sl.bytes);
+    }
+    // RotaryEmbedding tables (src/transformer.cpp:102-117), float arithmetic
+    // on the host, as the reference computes them
+    const int64_t h2 = c.head_dim / 2;
+    std::vector<float> cs((size_t)(c.max_seq * h2)), sn((size_t)(c.max_seq * h2));
+    for (int64_t i = 0; i < c.max_seq; i++)
+        for (int64_t j = 0; j < h2; j++) {
+            const float inv_freq = 1.0f / std::pow(c.theta, (float)(2 * j) / (float)c.head_dim);
+            const float val = (float)i * inv_freq;
+            cs[(size_t)(i * h2 + j)] = std::cos(val);
+            sn[(size_t)(i * h2 + j)] = std::sin(val);
+        }
+    e = hipMemcpy(d->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&d->cap_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        mth_decoder_destroy(d);
+        return api_fail(MTH_EDEVICE, "mth_decoder_create: %s", hipGetErrorString(e));
+    }
+    *out = d;
+    return api_ok();
+}
+
+void mth_decoder_destroy(mth_decoder* d) {
+    if (!d) return;
+    d->drop_graph();
+    if (d->cap_stream) (void)hipStreamDestroy(d->cap_stream);
+    if (d->block) (void)hipFree(d->block);
+    delete d;
+}
+
+int mth_decoder_set_layer(mth_decoder* d, int64_t layer, const mth_decoder_layer* w) {
+    if (!d || !w) return api_fail(MTH_EINVAL, "mth_decoder_set_layer: null pointer");
+    if (layer < 0 || layer >= d->c.layers)
+        return api_fail(MTH_EINVAL, "mth_decoder_set_layer: layer %lld outside 0..%lld", (long long)layer,
+                        (long long)d->c.layers - 1);
+    if (!w->attn_norm || !w->ffn_norm || !w->wq || !w->wk || !w->wv || !w->wo || !w->cbq || !w->cbk || !w->cbv ||
+        !w->cbo || !w->wgate || !w->wup || !w->cbgate || !w->cbup || !w->wdown)
+        return api_fail(MTH_EINVAL, "mth_decoder_set_layer: null weight pointer in layer %lld", (long long)layer);
+    d->layers[(size_t)layer] = *w;
+    d->layer_set[(size_t)layer] = true;
+    d->drop_graph();
+    return api_ok();
+}
+
+int mth_decoder_set_globals(mth_decoder* d, const mth_decoder_globals* g) {
+    if (!d || !g || !g->emb || !g->final_norm || !g->lm_idx || !g->lm_cb)
+        return api_fail(MTH_EINVAL, "mth_decoder_set_globals: null pointer");
+    d->g = *g;
+    d->globals_set = true;
+    d->drop_graph();
+    return api_ok();
+}
+
+int mth_decoder_start(mth_decoder* d, const int32_t* prompts, int64_t batch, int64_t prompt_len,
+                      mth_stream_t stream) {
+    if (!d || !prompts) return api_fail(MTH_EINVAL, "mth_decoder_start: null pointer");
+    if (batch < 1 || batch > d->c.max_batch)
+        return api_fail(MTH_EINVAL, "mth_decoder_start: batch=%lld outside 1..%lld", (long long)batch,
+                        (long long)d->c.max_batch);
+    if (prompt_len < 1 || prompt_len > d->c.max_seq)
+        return api_fail(MTH_EINVAL, "mth_decoder_start: prompt_len=%lld outside 1..%lld", (long long)prompt_len,
+                        (long long)d->c.max_seq);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipMemcpy2DAsync(d->hist, (size_t)d->hist_stride * 4, prompts, (size_t)prompt_len * 4,
+                                    (size_t)prompt_len * 4, (size_t)batch, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipMemsetAsync(d->step, 0, 4, s);
+    if (e != hipSuccess) return api_fail(MTH_EDEVICE, "mth_decoder_start: %s", hipGetErrorString(e));
+    d->batch = batch;
+    d->prompt_len = prompt_len;
+    d->steps = 0;
+    return api_ok();
+}
+
+int mth_decoder_step(mth_decoder* d, int64_t n, int use_graph, mth_stream_t stream) {
+    if (!d) return api_fail(MTH_EINVAL, "mth_decoder_step: null decoder");
+    if (d->batch == 0) return api_fail(MTH_EINVAL, "mth_decoder_step: no sequences started");
+    for (int64_t l = 0; l < d->c.layers; l++)
+        if (!d->layer_set[(size_t)l]) return api_fail(MTH_EINVAL, "mth_decoder_step: layer %lld has no weights",
+                                                      (long long)l);
+    if (!d->globals_set) return api_fail(MTH_EINVAL, "mth_decoder_step: embedding / lm_head not set");
+    if (n < 0 || d->steps + n > d->c.max_seq)
+        return api_fail(MTH_EINVAL, "mth_decoder_step: %lld steps after %lld exceed max_seq=%lld", (long long)n,
+                        (long long)d->steps, (long long)d->c.max_seq);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    if (use_graph) {
+        if (d->exec && (d->graph_batch != d->batch || d->graph_prompt != d->prompt_len)) d->drop_graph();
+        if (!d->exec) {
+            e = hipStreamBeginCapture(d->cap_stream, hipStreamCaptureModeThreadLocal);
+            if (e == hipSuccess) {
+                const hipError_t le = enqueue_step(d, d->cap_stream);
+                e = hipStreamEndCapture(d->cap_stream, &d->graph);
+                if (le != hipSuccess) e = le;
+            }
+            if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+            if (e != hipSuccess) {
+                d->drop_graph();
+                return api_fail(MTH_EDEVICE, "mth_decoder_step: graph capture failed: %s", hipGetErrorString(e));
+            }
+            d->graph_batch = d->batch;
+            d->graph_prompt = d->prompt_len;
+        }
+        for (int64_t i = 0; i < n && e == hipSuccess; i++) e = hipGraphLaunch(d->exec, s);
+    } else {
+        for (int64_t i = 0; i < n && e == hipSuccess; i++) e = enqueue_step(d, s);
+    }
+    if (e != hipSuccess) return api_fail(MTH_EDEVICE, "mth_decoder_step: %s", hipGetErrorString(e));
+    d->steps += n;
+    return api_ok();
+}
+
+int mth_decoder_buffers(const mth_decoder* d, float** logits, int32_t** hist, int64_t* hist_stride) {
+    if (!d) return api_fail(MTH_EINVAL, "mth_decoder_buffers: null decoder");
+    if (logits) *logits = d->logits;
+    if (hist) *hist = d->hist;
+    if (hist_stride) *hist_stride = d->hist_stride;
+    return api_ok();
+}
+
+int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_stream_t stream) {
+    if (!d) return api_fail(MTH_EINVAL, "mth_decoder_read: null decoder");
+    if (d->batch == 0) return api_fail(MTH_EINVAL, "mth_decoder_read: no sequences started");
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    if (logits) e = hipMemcpyAsync(logits, d->logits, (size_t)(d->batch * d->c.vocab) * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && hist)
+        e = hipMemcpyAsync(hist, d->hist, (size_t)(d->batch * d->hist_stride) * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return api_fail(MTH_EDEVICE, "mth_decoder_read: %s", hipGetErrorString(e));
+    return api_ok();
+}
+
+int64_t mth_decoder_steps_done(const mth_decoder* d) { return d ? d->steps : 0; }
+
+}  // extern "C"

@@ -10,6 +10,10 @@
 
 namespace mth {
 
+// ---- errors of the C ABI (capi.hip): set the calling thread's message ----
+int api_fail(int code, const char* fmt, ...);
+int api_ok();
+
 // ---- OIL8 (gemv.hip) ----------------------------------------------------
 // y[t*M + m] = sum_k cb[idx[m*K + k]] * x[t*K + k]          (t < batch)
 hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x, float* y,
@@ -61,5 +65,30 @@ hipError_t launch_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, 
                                     int64_t cb_block, uint16_t* c_bf16,
                                     int64_t M, int64_t N, int64_t K, hipStream_t s);
 bool oil4_gemm_prefill_supported(int64_t M, int64_t N, int64_t K, int64_t cb_block);
+
+// ---- FP32 decode-step operators (dense.hip) ---------------------------------
+// x <- t + x (when t), then y = rms_norm(x) * gamma per row of dim.
+hipError_t launch_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim,
+                           float eps, hipStream_t s);
+// y[r][i] = silu(g[r*gstride + i]) * u[r*ustride + i], i < n
+hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t n, int64_t gstride,
+                           int64_t ustride, hipStream_t s);
+hipError_t launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
+hipError_t launch_add(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
+hipError_t launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
+hipError_t launch_softmax(const float* x, float* y, int64_t rows, int64_t dim, hipStream_t s);
+// Position pos = (step ? *step : 0) + pos0; caches [batch][kv_heads][max_seq][head_dim].
+hipError_t launch_rope_kv(float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
+                          float* kc, float* vc, const int* step, int pos0, int64_t batch, int heads, int kv_heads,
+                          int head_dim, int max_seq, hipStream_t s);
+// ctx = (step ? *step : 0) + ctx0 + 1 <= max_seq positions.
+bool attention_supported(int head_dim, int max_seq);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
+                            int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s);
+hipError_t launch_argmax(const float* logits, int64_t rows, int64_t n, int* ids, int* hist, const int* step,
+                         int hist_stride, int prompt_len, hipStream_t s);
+hipError_t launch_embed(const float* emb, const int* hist, const int* step, int hist_stride, float* x, int64_t batch,
+                        int dim, int vocab, hipStream_t s);
+hipError_t launch_advance(int* step, hipStream_t s);
 
 }  // namespace mth

@@ -66,6 +66,18 @@ void mth_synth_uniform_int(uint64_t* st, int8_t* out, int64_t n, int lo, int hi)
     }
 }
 
+void mth_synth_uniform_i32(uint64_t* st, int32_t* out, int64_t n, int lo, int hi) {
+    const uint64_t range = (uint64_t)((int64_t)hi - lo + 1);
+    const uint64_t limit = UINT64_MAX - (UINT64_MAX % range);
+    for (int64_t i = 0; i < n; ++i) {
+        uint64_t v;
+        do {
+            v = next_u64(st);
+        } while (v >= limit);
+        out[i] = (int32_t)(lo + (int64_t)(v % range));
+    }
+}
+
 void mth_synth_normal(uint64_t* st, float* out, int64_t n, double mean, double stddev) {
     const double two_pi = 6.283185307179586476925286766559;
     const double inv53 = 1.0 / 9007199254740992.0;  // 2^-53

@@ -25,6 +25,8 @@ EXPORTS = (
     "mth_quantize_per_token", "mth_dequantize_per_tensor",
     "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
     "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
+    "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_add", "mth_mul", "mth_softmax",
+    "mth_rope_tables", "mth_rope_kv", "mth_attention_decode", "mth_argmax",
 )
 
 MTH_OK, MTH_EINVAL, MTH_EDEVICE, MTH_EUNSUPPORTED = 0, -1, -2, -3
@@ -70,6 +72,17 @@ _SIG = {
     "mth_tl1_gemm": [VP, VP, VP, I64, I64, I64, VP],
     "mth_tl2_gemm": [VP, VP, VP, I64, I64, I64, VP],
     "mth_tl_precompute_lut": [VP, VP, I64, I32, VP],
+    "mth_rms_norm": [VP, VP, VP, I64, I64, F32, VP],
+    "mth_add_rms_norm": [VP, VP, VP, VP, I64, I64, F32, VP],
+    "mth_silu": [VP, VP, I64, VP],
+    "mth_silu_mul": [VP, VP, VP, I64, I64, I64, I64, VP],
+    "mth_add": [VP, VP, VP, I64, VP],
+    "mth_mul": [VP, VP, VP, I64, VP],
+    "mth_softmax": [VP, VP, I64, I64, VP],
+    "mth_rope_tables": [I64, I64, F32, VP, VP],
+    "mth_rope_kv": [VP, VP, VP, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP],
+    "mth_attention_decode": [VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP],
+    "mth_argmax": [VP, VP, I64, I64, VP],
 }
 for _n, _a in _SIG.items():
     _f = getattr(_lib, _n)
@@ -224,3 +237,84 @@ def tl_precompute_lut(act, lut, K, group, stream=None):
     n = (K // group) * (9 if group == 2 else 27)
     _check(_lib.mth_tl_precompute_lut(_ptr(act, t.int8, K, "act"), _ptr(lut, t.int8, n, "lut"), K, group,
                                       _stream(stream)))
+
+
+# ---- FP32 decode-step operators ---------------------------------------------
+def rms_norm(x, gamma, y, rows, dim, eps=1e-5, stream=None):
+    t = _torch()
+    _check(_lib.mth_rms_norm(_ptr(x, t.float32, rows * dim, "x"), _ptr(gamma, t.float32, dim, "gamma"),
+                             _ptr(y, t.float32, rows * dim, "y"), rows, dim, eps, _stream(stream)))
+
+
+def add_rms_norm(x, res, gamma, y, rows, dim, eps=1e-5, stream=None):
+    """x <- res + x, y = rms_norm(x) * gamma."""
+    t = _torch()
+    _check(_lib.mth_add_rms_norm(_ptr(x, t.float32, rows * dim, "x"), _ptr(res, t.float32, rows * dim, "res"),
+                                 _ptr(gamma, t.float32, dim, "gamma"), _ptr(y, t.float32, rows * dim, "y"), rows, dim,
+                                 eps, _stream(stream)))
+
+
+def silu(x, y, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_silu(_ptr(x, t.float32, n, "x"), _ptr(y, t.float32, n, "y"), n, _stream(stream)))
+
+
+def silu_mul(g, u, y, rows, n, gstride=None, ustride=None, stream=None):
+    t = _torch()
+    gs, us = gstride or n, ustride or n
+    _check(_lib.mth_silu_mul(_ptr(g, t.float32, (rows - 1) * gs + n, "g"), _ptr(u, t.float32, (rows - 1) * us + n, "u"),
+                             _ptr(y, t.float32, rows * n, "y"), rows, n, gs, us, _stream(stream)))
+
+
+def add(a, b, c, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_add(_ptr(a, t.float32, n, "a"), _ptr(b, t.float32, n, "b"), _ptr(c, t.float32, n, "c"), n,
+                        _stream(stream)))
+
+
+def mul(a, b, c, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_mul(_ptr(a, t.float32, n, "a"), _ptr(b, t.float32, n, "b"), _ptr(c, t.float32, n, "c"), n,
+                        _stream(stream)))
+
+
+def softmax(x, y, rows, dim, stream=None):
+    t = _torch()
+    _check(_lib.mth_softmax(_ptr(x, t.float32, rows * dim, "x"), _ptr(y, t.float32, rows * dim, "y"), rows, dim,
+                            _stream(stream)))
+
+
+def rope_tables(head_dim, max_seq, theta=10000.0):
+    """Host (numpy) cos/sin tables [max_seq][head_dim/2]."""
+    import numpy as np
+    c = np.empty((max_seq, head_dim // 2), np.float32)
+    s = np.empty((max_seq, head_dim // 2), np.float32)
+    _check(_lib.mth_rope_tables(head_dim, max_seq, theta, c.ctypes.data, s.ctypes.data))
+    return c, s
+
+
+def rope_kv(q, k, v, cos_t, sin_t, kcache, vcache, pos, batch, heads, kv_heads, head_dim, max_seq, stream=None):
+    t = _torch()
+    kv = batch * kv_heads * head_dim
+    cache = batch * kv_heads * max_seq * head_dim
+    _check(_lib.mth_rope_kv(_ptr(q, t.float32, batch * heads * head_dim, "q"), _ptr(k, t.float32, kv, "k"),
+                            _ptr(v, t.float32, kv, "v"), _ptr(cos_t, t.float32, max_seq * head_dim // 2, "cos"),
+                            _ptr(sin_t, t.float32, max_seq * head_dim // 2, "sin"),
+                            _ptr(kcache, t.float32, cache, "kcache"), _ptr(vcache, t.float32, cache, "vcache"),
+                            pos, batch, heads, kv_heads, head_dim, max_seq, _stream(stream)))
+
+
+def attention_decode(q, kcache, vcache, out, batch, heads, kv_heads, head_dim, ctx, max_seq, stream=None):
+    t = _torch()
+    cache = batch * kv_heads * max_seq * head_dim
+    _check(_lib.mth_attention_decode(_ptr(q, t.float32, batch * heads * head_dim, "q"),
+                                     _ptr(kcache, t.float32, cache, "kcache"), _ptr(vcache, t.float32, cache, "vcache"),
+                                     _ptr(out, t.float32, batch * heads * head_dim, "out"), batch, heads, kv_heads,
+                                     head_dim, ctx, max_seq, _stream(stream)))
+
+
+def argmax(logits, ids, rows, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_argmax(_ptr(logits, t.float32, rows * n, "logits"), _ptr(ids, t.int32, rows, "ids"), rows, n,
+                           _stream(stream)))
+

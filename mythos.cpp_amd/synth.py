@@ -11,7 +11,10 @@ another from that stream:
   * ternary codes t+1 = uniform_int(0, 2), packed four per byte, element 4i+j
     in bits 2j of byte i (src/kernel_i2s.cpp:13-30, tools/convert.cpp:329-342);
   * activations N(0, 1); normals from a double-precision Box-Muller over
-    next_u64() >> 11.
+    next_u64() >> 11;
+  * the decoder stack (config 5): per layer Q, K, V, O as OIL8, gate and up
+    as OIL4, down as ternary, drawn in that order after the FP32 embedding
+    N(0, 1), then the OIL8 lm_head; prompt ids uniform_int(0, vocab - 1).
 """
 from __future__ import annotations
 
@@ -33,7 +36,9 @@ _lib.mth_synth_u64.argtypes = [_VP, _VP, _I64]
 _lib.mth_synth_bits.argtypes = [_VP, _VP, _I64, C.c_int]
 _lib.mth_synth_uniform_int.argtypes = [_VP, _VP, _I64, C.c_int, C.c_int]
 _lib.mth_synth_normal.argtypes = [_VP, _VP, _I64, C.c_double, C.c_double]
-for _f in ("mth_synth_seed", "mth_synth_u64", "mth_synth_bits", "mth_synth_uniform_int", "mth_synth_normal"):
+_lib.mth_synth_uniform_i32.argtypes = [_VP, _VP, _I64, C.c_int, C.c_int]
+for _f in ("mth_synth_seed", "mth_synth_u64", "mth_synth_bits", "mth_synth_uniform_int", "mth_synth_normal",
+           "mth_synth_uniform_i32"):
     getattr(_lib, _f).restype = None
 
 
@@ -57,6 +62,11 @@ class Stream:
     def uniform_int(self, shape, lo: int, hi: int) -> np.ndarray:
         out = np.empty(shape, np.int8)
         _lib.mth_synth_uniform_int(self.st.ctypes.data, out.ctypes.data, out.size, lo, hi)
+        return out
+
+    def uniform_i32(self, shape, lo: int, hi: int) -> np.ndarray:
+        out = np.empty(shape, np.int32)
+        _lib.mth_synth_uniform_i32(self.st.ctypes.data, out.ctypes.data, out.size, lo, hi)
         return out
 
     def normal(self, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
@@ -162,3 +172,98 @@ def dequant_oil4(packed: np.ndarray, cbs: np.ndarray, rows: int, K: int, block: 
     nb = K // block
     blk = (np.arange(rows)[:, None] * nb + (np.arange(K)[None, :] // block)) * 16
     return table[blk + nib]
+
+
+# ---- config 5: the mixed-format decoder stack ---------------------------------
+DECODER_CONFIG5 = dict(vocab=32000, hidden=4096, layers=32, heads=32, kv_heads=32, head_dim=128, ffn=11008,
+                       max_seq=192, cb_block=128, eps=1e-5, theta=10000.0)
+PROMPT_LEN5, GEN_TOKENS5 = 64, 128
+
+
+def decoder_config(**overrides) -> dict:
+    c = dict(DECODER_CONFIG5)
+    c.update(overrides)
+    return c
+
+
+def decoder_model(cfg: dict, config: int = 5, random_gamma: bool = False) -> dict:
+    """Weights of the decoder stack in the kernels' layouts ([out][in] rows).
+    Norm gains are 1 (the reference's RMSNorm init) unless random_gamma.
+    gate and up are one array of 2*ffn rows (gate first) so that they can run
+    as one GEMV; 'wgate'/'wup' are views of it."""
+    g = stream(config)
+    H, F, V = cfg["hidden"], cfg["ffn"], cfg["vocab"]
+    QD, KD, B = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["cb_block"]
+
+    def gamma():
+        return g.normal(H, 1.0, 0.1) if random_gamma else np.ones(H, np.float32)
+
+    def oil8(rows, cols):
+        return g.bits((rows, cols), 8), np.sort(g.normal(256, 0.0, 0.02)).astype(np.float32)
+
+    model = {"emb": g.normal((V, H)), "layers": []}
+    for _ in range(cfg["layers"]):
+        ly = {"attn_norm": gamma(), "ffn_norm": gamma()}
+        for name, rows, cols in (("q", QD, H), ("k", KD, H), ("v", KD, H), ("o", H, QD)):
+            ly["w" + name], ly["cb" + name] = oil8(rows, cols)
+        gu = np.empty((2 * F, H // 2), np.uint8)
+        half = F * (H // B) if B else 1      # codebooks per tensor
+        cbs = np.empty((2 * half, 16), np.uint16)
+        for i in range(2):
+            gu[i * F:(i + 1) * F] = pack_nibbles(g.bits((F, H), 4))
+            cbs[i * half:(i + 1) * half] = float_to_half_trunc(g.normal((half, 16), 0.0, 0.02))
+        ly["wgate_up"], ly["cbgate_up"] = gu, cbs.reshape(-1)
+        ly["wgate"], ly["wup"] = gu[:F], gu[F:]
+        ly["cbgate"], ly["cbup"] = cbs[:half].reshape(-1), cbs[half:].reshape(-1)
+        ly["wdown"] = pack_ternary(g.uniform_int((H, F), 0, 2) - 1)
+        ly["down_scale"] = np.float32(W_SCALE_TERNARY)
+        model["layers"].append(ly)
+    model["final_norm"] = gamma()
+    model["lm_idx"], model["lm_cb"] = oil8(V, H)
+    return model
+
+
+def decoder_prompts(cfg: dict, batch: int, prompt_len: int, config: int = 5) -> np.ndarray:
+    """[batch][prompt_len] ids uniform in [0, vocab), from the stream after the weights' seed + 100."""
+    return stream(config + 100).uniform_i32((batch, prompt_len), 0, cfg["vocab"] - 1)
+
+
+def dequant_oil8(idx: np.ndarray, cb: np.ndarray) -> np.ndarray:
+    return cb[idx]
+
+
+def dequant_ternary(packed: np.ndarray, rows: int, K: int, w_scale: float) -> np.ndarray:
+    p = packed.reshape(rows, K // 4)
+    codes = np.stack([(p >> (2 * j)) & 3 for j in range(4)], -1).reshape(rows, K).astype(np.int8)
+    t = np.where(codes == 0, -1, np.where(codes == 1, 0, 1)).astype(np.float32)
+    return t * np.float32(w_scale)
+
+
+def decoder_digest(model: dict) -> str:
+    """SHA-256 over every weight array of a decoder model, in a fixed order."""
+    import hashlib
+    h = hashlib.sha256()
+    for k in ("emb", "final_norm", "lm_idx", "lm_cb"):
+        h.update(np.ascontiguousarray(model[k]).tobytes())
+    for ly in model["layers"]:
+        for k in ("attn_norm", "ffn_norm", "wq", "cbq", "wk", "cbk", "wv", "cbv", "wo", "cbo", "wgate_up",
+                  "cbgate_up", "wdown", "down_scale"):
+            h.update(np.ascontiguousarray(ly[k]).tobytes())
+    return h.hexdigest()
+
+
+def decoder_dense(cfg: dict, model: dict) -> dict:
+    """FP32 copies of every weight ([out][in]), for dense reference checks."""
+    H, F, B = cfg["hidden"], cfg["ffn"], cfg["cb_block"]
+    out = {"emb": model["emb"], "final_norm": model["final_norm"],
+           "lm": dequant_oil8(model["lm_idx"], model["lm_cb"]), "layers": []}
+    for ly in model["layers"]:
+        d = {"attn_norm": ly["attn_norm"], "ffn_norm": ly["ffn_norm"]}
+        for n in "qkvo":
+            d[n] = dequant_oil8(ly["w" + n], ly["cb" + n])
+        gu = dequant_oil4(ly["wgate_up"], ly["cbgate_up"], 2 * F, H, B)
+        d["gate"], d["up"] = gu[:F], gu[F:]
+        d["down"] = dequant_ternary(ly["wdown"], H, F, ly["down_scale"])
+        out["layers"].append(d)
+    return out
+

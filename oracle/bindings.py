@@ -54,8 +54,28 @@ I64, I32, F32, U64 = C.c_int64, C.c_int, C.c_float, C.c_uint64
 VP = C.c_void_p
 
 
+class DecoderConfig(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ffn",
+                                         "max_seq", "cb_block")] + [("eps", C.c_float), ("theta", C.c_float)]
+
+
+class DecoderLayer(C.Structure):
+    _fields_ = [("attn_norm", VP), ("ffn_norm", VP), ("wq", VP), ("wk", VP), ("wv", VP), ("wo", VP),
+                ("cbq", VP), ("cbk", VP), ("cbv", VP), ("cbo", VP), ("wgate", VP), ("wup", VP),
+                ("cbgate", VP), ("cbup", VP), ("wdown", VP), ("down_scale", C.c_float)]
+
+
+class DecoderModel(C.Structure):
+    _fields_ = [("emb", VP), ("final_norm", VP), ("lm_idx", VP), ("lm_cb", VP), ("rope_cos", VP),
+                ("rope_sin", VP), ("layers", C.POINTER(DecoderLayer))]
+
+
+DECODER_CONFIG_KEYS = ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ffn", "max_seq",
+                       "cb_block", "eps", "theta")
+
+
 class Oracle:
-    """The C restatement (oracle.c)."""
+    """The C restatement (oracle.c, decoder.c)."""
 
     def __init__(self, path: str | None = None):
         path = path or oracle_lib_path()
@@ -84,6 +104,14 @@ class Oracle:
             "orc_rms_norm": [VP, VP, F32, VP, I64, I64],
             "orc_silu": [VP, VP, I64],
             "orc_oil4_gemm_prefill": [VP, VP, VP, I64, VP, VP, I64, I64, I64, I32],
+            "orc_softmax": [VP, VP, I64, I64],
+            "orc_add": [VP, VP, VP, I64],
+            "orc_mul": [VP, VP, VP, I64],
+            "orc_silu_mul": [VP, VP, VP, I64],
+            "orc_rope_tables": [I64, I64, F32, VP, VP],
+            "orc_rope_apply": [VP, I64, I64, I64, VP, VP],
+            "orc_attention_decode": [VP, VP, VP, VP, I64, I64, I64, I64, I64],
+            "orc_decoder_step": [C.POINTER(DecoderConfig), C.POINTER(DecoderModel), VP, VP, I64, I32, VP, I32, I32],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -104,6 +132,8 @@ class Oracle:
         L.orc_rng_normal.restype = F32
         L.orc_rng_uniform_int.argtypes = [VP, I32, I32]
         L.orc_rng_uniform_int.restype = I32
+        L.orc_argmax.argtypes = [VP, I64]
+        L.orc_argmax.restype = I32
 
     # -- rng ---------------------------------------------------------------
     def _rng(self, seed):
@@ -239,10 +269,85 @@ class Oracle:
         self.lib.orc_rms_norm(_p(x, np.float32), _p(g, np.float32), eps, _p(y, np.float32), rows, dim)
         return y
 
+    # -- config-5 decoder (decoder.c) -------------------------------------
+    def softmax(self, x, rows, dim):
+        y = np.empty((rows, dim), np.float32)
+        self.lib.orc_softmax(_p(x, np.float32), _p(y, np.float32), rows, dim)
+        return y
+
+    def silu_mul(self, g, u):
+        y = np.empty_like(g)
+        self.lib.orc_silu_mul(_p(g, np.float32), _p(u, np.float32), _p(y, np.float32), g.size)
+        return y
+
+    def rope_tables(self, head_dim, max_seq, theta=10000.0):
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty((max_seq, head_dim // 2), np.float32)
+        self.lib.orc_rope_tables(head_dim, max_seq, theta, _p(c, np.float32), _p(s, np.float32))
+        return c, s
+
+    def rope_apply(self, x, heads, head_dim, pos, cos_t, sin_t):
+        y = np.array(x, np.float32, copy=True)
+        self.lib.orc_rope_apply(_p(y, np.float32), heads, head_dim, pos, _p(cos_t, np.float32), _p(sin_t, np.float32))
+        return y
+
+    def attention_decode(self, q, kc, vc, heads, kv_heads, head_dim, ctx, kv_stride):
+        out = np.empty(heads * head_dim, np.float32)
+        self.lib.orc_attention_decode(_p(q, np.float32), _p(kc, np.float32), _p(vc, np.float32),
+                                      _p(out, np.float32), heads, kv_heads, head_dim, ctx, kv_stride)
+        return out
+
+    def argmax(self, logits) -> int:
+        return int(self.lib.orc_argmax(_p(logits, np.float32), logits.size))
+
+    def decoder(self, cfg: dict, model: dict):
+        """A callable decoder over `model` (synth.decoder_model layout):
+        step(kc, vc, pos, token, down_mode=0, threads=8) -> logits."""
+        return _OracleDecoder(self, cfg, model)
+
     def silu(self, x):
         y = np.empty_like(x)
         self.lib.orc_silu(_p(x, np.float32), _p(y, np.float32), x.size)
         return y
+
+
+class _OracleDecoder:
+    def __init__(self, orc: "Oracle", cfg: dict, model: dict):
+        self.orc, self.cfg = orc, cfg
+        self.c = DecoderConfig(*[cfg[k] for k in DECODER_CONFIG_KEYS])
+        keep = []
+
+        def ptr(a, dtype):
+            a = np.ascontiguousarray(a)
+            assert a.dtype == dtype, (a.dtype, dtype)
+            keep.append(a)
+            return a.ctypes.data
+
+        cos_t, sin_t = orc.rope_tables(cfg["head_dim"], cfg["max_seq"], cfg["theta"])
+        L = (DecoderLayer * cfg["layers"])()
+        for i, ly in enumerate(model["layers"]):
+            L[i] = DecoderLayer(ptr(ly["attn_norm"], np.float32), ptr(ly["ffn_norm"], np.float32),
+                                ptr(ly["wq"], np.uint8), ptr(ly["wk"], np.uint8), ptr(ly["wv"], np.uint8),
+                                ptr(ly["wo"], np.uint8), ptr(ly["cbq"], np.float32), ptr(ly["cbk"], np.float32),
+                                ptr(ly["cbv"], np.float32), ptr(ly["cbo"], np.float32), ptr(ly["wgate"], np.uint8),
+                                ptr(ly["wup"], np.uint8), ptr(ly["cbgate"], np.uint16), ptr(ly["cbup"], np.uint16),
+                                ptr(ly["wdown"], np.uint8), float(ly["down_scale"]))
+        self.m = DecoderModel(ptr(model["emb"], np.float32), ptr(model["final_norm"], np.float32),
+                              ptr(model["lm_idx"], np.uint8), ptr(model["lm_cb"], np.float32),
+                              ptr(cos_t, np.float32), ptr(sin_t, np.float32), L)
+        self._keep, self._L = keep, L
+
+    def new_cache(self):
+        c = self.cfg
+        shape = (c["layers"], c["kv_heads"], c["max_seq"], c["head_dim"])
+        return np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+
+    def step(self, kc, vc, pos: int, token: int, down_mode: int = 0, threads: int = 8) -> np.ndarray:
+        assert 0 <= pos < self.cfg["max_seq"]
+        out = np.empty(self.cfg["vocab"], np.float32)
+        self.orc.lib.orc_decoder_step(C.byref(self.c), C.byref(self.m), _p(kc, np.float32), _p(vc, np.float32),
+                                      pos, token, _p(out, np.float32), down_mode, threads)
+        return out
 
 
 class Reference:
@@ -272,6 +377,7 @@ class Reference:
             "ref_gemv": [F32, VP, VP, F32, VP, I64, I64],
             "ref_rms_norm": [VP, VP, F32, VP, I64, I64],
             "ref_silu": [VP, VP, I64],
+            "ref_softmax": [VP, VP, I64, I64],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -425,3 +531,38 @@ class Reference:
         if n < 0:
             raise ValueError(f"reference OILReader rejected {path}")
         return out[:min(n, cap)]
+
+    def softmax(self, x, rows, dim):
+        """math::softmax over the last axis of a [rows][dim] tensor."""
+        y = np.empty((rows, dim), np.float32)
+        self.lib.ref_softmax(_p(np.ascontiguousarray(x, np.float32), np.float32), _p(y, np.float32), rows, dim)
+        return y
+
+
+class ReferenceModel:
+    """The reference's DenseModel (oracle/_ref/libref_model.so)."""
+
+    def __init__(self):
+        path = ref_lib_path("model")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = C.CDLL(path)
+        self.lib.ref_dense_model_run.argtypes = [VP, F32, F32, VP, C.POINTER(VP), VP, VP, VP, I64, VP]
+        self.lib.ref_dense_model_run.restype = None
+
+    def run(self, cfg: dict, emb, layers_inmajor, final_norm, lm_head_inmajor, ids) -> np.ndarray:
+        """layers_inmajor: per layer [attn_norm, ffn_norm, q, k, v, o, gate,
+        up, down] as float32 arrays, Linear weights input-major."""
+        keep = [np.ascontiguousarray(a, np.float32) for ly in layers_inmajor for a in ly]
+        ptrs = (VP * len(keep))(*[a.ctypes.data for a in keep])
+        c = np.array([cfg[k] for k in ("vocab", "hidden", "layers", "heads", "head_dim", "ffn", "max_seq")], np.int64)
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((ids.size, cfg["vocab"]), np.float32)
+        emb = np.ascontiguousarray(emb, np.float32)
+        fn = np.ascontiguousarray(final_norm, np.float32)
+        lm = np.ascontiguousarray(lm_head_inmajor, np.float32)
+        self.lib.ref_dense_model_run(_p(c, np.int64), cfg["eps"], cfg["theta"], _p(emb, np.float32), ptrs,
+                                     _p(fn, np.float32), _p(lm, np.float32), _p(ids, np.int32), ids.size,
+                                     _p(out, np.float32))
+        return out
+

@@ -91,6 +91,53 @@ void orc_rms_norm(const float* x, const float* gamma, float eps, float* y,
                   int64_t rows, int64_t dim);                    /* :182-205 */
 void orc_silu(const float* x, float* y, int64_t n);              /* :119-128 */
 
+/* ---- config-5 decoder (decoder.c) ---------------------------------------- */
+void orc_softmax(const float* x, float* y, int64_t rows, int64_t dim);  /* src/math.cpp:207-249 */
+void orc_add(const float* a, const float* b, float* c, int64_t n);      /* src/math.cpp:251-258 */
+void orc_mul(const float* a, const float* b, float* c, int64_t n);      /* src/math.cpp:269-276 */
+void orc_silu_mul(const float* g, const float* u, float* y, int64_t n); /* transformer.cpp:377-386 */
+void orc_rope_tables(int64_t head_dim, int64_t max_seq, float theta,
+                     float* cos_t, float* sin_t);                       /* transformer.cpp:102-117 */
+void orc_rope_apply(float* x, int64_t heads, int64_t head_dim, int64_t pos,
+                    const float* cos_t, const float* sin_t);            /* transformer.cpp:119-139 */
+void orc_attention_decode(const float* q, const float* kc, const float* vc, float* out,
+                          int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t ctx,
+                          int64_t kv_stride);                           /* transformer.cpp:188-348 */
+int32_t orc_argmax(const float* logits, int64_t n);                    /* src/sampler.cpp:12-22 */
+
+typedef struct {
+    int64_t vocab, hidden, layers, heads, kv_heads, head_dim, ffn, max_seq, cb_block;
+    float eps, theta;
+} orc_decoder_config;
+
+typedef struct {          /* one block; weights in [out][in] rows */
+    const float* attn_norm;
+    const float* ffn_norm;
+    const uint8_t *wq, *wk, *wv, *wo;           /* OIL8 */
+    const float *cbq, *cbk, *cbv, *cbo;
+    const uint8_t *wgate, *wup;                 /* OIL4, codebooks [out][in/cb_block][16] */
+    const uint16_t *cbgate, *cbup;
+    const uint8_t* wdown;                       /* I2_S */
+    float down_scale;
+} orc_decoder_layer;
+
+typedef struct {
+    const float* emb;                           /* [vocab][hidden] FP32 */
+    const float* final_norm;
+    const uint8_t* lm_idx;                      /* OIL8 [vocab][hidden] */
+    const float* lm_cb;
+    const float* rope_cos;                      /* [max_seq][head_dim/2] */
+    const float* rope_sin;
+    const orc_decoder_layer* layers;
+} orc_decoder_model;
+
+/* One token of one sequence at position pos: writes that position's K/V into
+ * kcache/vcache ([layers][kv_heads][max_seq][head_dim]) and the logits
+ * [vocab].  down_mode 0: I2_S with int8 activations; 1: FP32 activations. */
+void orc_decoder_step(const orc_decoder_config* c, const orc_decoder_model* m, float* kcache,
+                      float* vcache, int64_t pos, int32_t token, float* logits, int down_mode,
+                      int nthreads);
+
 /* ---- OIL4 prefill GEMM reference: C[m][n] = bf16(sum_k A[m][k] * W[n][k]) ---- */
 void orc_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cb16,
                            int64_t block, uint16_t* c_bf16, float* c_f32,

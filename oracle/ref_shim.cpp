@@ -137,6 +137,13 @@ void ref_rms_norm(const float* x, const float* g, float eps, float* y, int64_t r
     std::memcpy(y, ty.data(), (size_t)(rows * dim) * 4);
 }
 
+void ref_softmax(const float* x, float* y, int64_t rows, int64_t dim) {
+    Tensor tx = make_f32(x, rows * dim).view(Shape{rows, dim});
+    Tensor ty(Shape{rows, dim}, DType::F32);
+    math::softmax(tx, ty, -1);
+    std::memcpy(y, ty.data(), (size_t)(rows * dim) * 4);
+}
+
 void ref_silu(const float* x, float* y, int64_t n) {
     Tensor tx = make_f32(x, n);
     Tensor ty(Shape{n}, DType::F32);

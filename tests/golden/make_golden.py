@@ -266,6 +266,47 @@ def main() -> None:
          **{f"w_{i}": w for i, w in enumerate(lw)},
          **{f"y_{i}": avx2.scalar_gemm(xl, w, nb_tok, out_f, in_f) for i, w in enumerate(lw)})
 
+    # ---- decoder composition (src/model.cpp DenseModel::forward) -----------
+    # A 2-layer model with the decoder's weight formats, dequantized to FP32
+    # and loaded into the reference's own DenseModel (Linear weights
+    # input-major, as it holds them), fed one token per forward call through
+    # its KVCache; the logits of every step.  The weights are regenerated in
+    # the tests from the seeded stream (synth.decoder_model), checked against
+    # the stored digest.
+    # The reference's attention output is not usable: its P*V loop indexes
+    # V[t][2d] (vptr = vd + v_base + d, then vptr[t*head_dim + d],
+    # src/transformer.cpp:325-342), reading past the cache.  The O projection
+    # is therefore zero here (OIL8 codebook of zeros), which makes the
+    # attention branch contribute exactly 0: the golden pins the embedding,
+    # both residuals, the norms, the FFN and the lm_head; the attention and
+    # RoPE are pinned against float64 definitions in the tests.
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(HERE)), "mythos.cpp_amd"))
+    import synth
+    from oracle import ReferenceModel
+    cfg = synth.decoder_config(vocab=96, hidden=64, layers=2, heads=4, kv_heads=4, head_dim=16, ffn=128,
+                               max_seq=16, cb_block=32)
+    model = synth.decoder_model(cfg, config=50, random_gamma=True)
+    for ly in model["layers"]:
+        ly["cbo"] = np.zeros(256, np.float32)
+    dense = synth.decoder_dense(cfg, model)
+    ids = synth.decoder_prompts(cfg, 1, 12, config=50)[0]
+    ids[3] = cfg["vocab"] + 5          # out of range: Embedding::forward reads row 0
+    layers = [[d["attn_norm"], d["ffn_norm"]] + [np.ascontiguousarray(d[n].T) for n in
+                                                  ("q", "k", "v", "o", "gate", "up", "down")]
+              for d in dense["layers"]]
+    runs = [ReferenceModel().run(cfg, dense["emb"], layers, dense["final_norm"],
+                                 np.ascontiguousarray(dense["lm"].T), ids) for _ in range(2)]
+    assert np.array_equal(runs[0], runs[1]) and np.isfinite(runs[0]).all()
+    logits = runs[0]
+    # math::softmax rows (src/math.cpp:207-249): wide range, ties, -inf entries
+    sx = (rng.standard_normal((6, 75)) * 4).astype(np.float32)
+    sx[1] = 0.0
+    sx[2, ::3] = -np.inf
+    sx[3] *= 30
+    save("decoder", config=np.array(50), digest=np.frombuffer(bytes.fromhex(synth.decoder_digest(model)), np.uint8),
+         ids=ids, logits=logits, softmax_x=sx, softmax=avx2.softmax(sx, 6, 75),
+         **{f"cfg_{k}": np.array(v) for k, v in cfg.items()})
+
 
 if __name__ == "__main__":
     main()

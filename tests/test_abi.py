@@ -17,8 +17,11 @@ PKG = os.path.join(ROOT, "mythos.cpp_amd")
 HDR = os.path.join(ROOT, "include", "mythos_oil.h")
 
 
-def declared():
-    src = open(HDR).read()
+DEC_HDR = os.path.join(ROOT, "include", "mythos_decoder.h")
+
+
+def declared(hdr=HDR):
+    src = open(hdr).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"\b(mth_[a-z0-9_]+)\s*\(", src)))
 
@@ -29,14 +32,16 @@ def dynsyms(path):
 
 
 def test_header_matches_exports(mth):
-    decl = declared()
+    import decoder
+    decl, dec = declared(), declared(DEC_HDR)
     assert decl == sorted(mth.EXPORTS)
+    assert dec == sorted(decoder.EXPORTS)
     syms = dynsyms(mth.LIB_PATH)
-    missing = [d for d in decl if d not in syms]
+    missing = [d for d in decl + dec if d not in syms]
     assert not missing, missing
-    extra = sorted(s for s in syms if s.startswith("mth_") and s not in decl)
+    extra = sorted(s for s in syms if s.startswith("mth_") and s not in decl + dec)
     assert not extra, f"exported but undeclared: {extra}"
-    for d in decl:                       # resolvable through the loader too
+    for d in decl + dec:                 # resolvable through the loader too
         assert getattr(mth.lib, d) is not None
 
 
@@ -75,6 +80,16 @@ CASES = [
     ("mth_tl1_gemm", (NULL, P, P, 4, 1, 8, NULL), (P, P, P, 4, 0, 8, NULL)),
     ("mth_tl2_gemm", (P, NULL, P, 4, 1, 6, NULL), (P, P, P, 4, 1, 8, NULL)),
     ("mth_tl_precompute_lut", (NULL, P, 6, 3, NULL), (P, P, 6, 4, NULL)),
+    ("mth_rms_norm", (P, NULL, P, 1, 8, C.c_float(1e-5), NULL), (P, P, P, 0, 8, C.c_float(1e-5), NULL)),
+    ("mth_add_rms_norm", (P, NULL, P, P, 1, 8, C.c_float(1e-5), NULL), (P, P, P, P, 1, -8, C.c_float(1e-5), NULL)),
+    ("mth_silu", (NULL, P, 8, NULL), (P, P, 0, NULL)),
+    ("mth_silu_mul", (P, NULL, P, 1, 8, 8, 8, NULL), (P, P, P, 1, 8, 4, 8, NULL)),
+    ("mth_add", (P, P, NULL, 8, NULL), (P, P, P, -1, NULL)),
+    ("mth_mul", (NULL, P, P, 8, NULL), (P, P, P, 0, NULL)),
+    ("mth_softmax", (P, NULL, 1, 8, NULL), (P, P, 1, 0, NULL)),
+    ("mth_rope_kv", (P, P, P, P, P, NULL, P, 0, 1, 2, 2, 64, 8, NULL), (P, P, P, P, P, P, P, 8, 1, 2, 2, 64, 8, NULL)),
+    ("mth_attention_decode", (P, P, NULL, P, 1, 2, 2, 64, 1, 8, NULL), (P, P, P, P, 1, 2, 2, 64, 9, 8, NULL)),
+    ("mth_argmax", (P, NULL, 1, 8, NULL), (P, P, 1, 0, NULL)),
 ]
 
 
@@ -137,3 +152,21 @@ def test_facade_compiles_against_reference_headers():
                         f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(PKG, 'host', 'include')}", src],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_decoder_argument_errors(mth):
+    import decoder
+    lib = mth.lib
+    h = C.c_void_p()
+    cfg = decoder.Config(1000, 256, 2, 2, 2, 128, 512, 16, 128, 1, 1e-5, 1e4)
+    bad = [dict(max_batch=17), dict(head_dim=96), dict(heads=3), dict(cb_block=100), dict(hidden=254),
+           dict(max_seq=0)]
+    for b in bad:
+        c = decoder.Config(*[b.get(k, getattr(cfg, k)) for k in decoder.CONFIG_KEYS], cfg.eps, cfg.theta)
+        rc = lib.mth_decoder_create(C.byref(c), C.byref(h))
+        assert rc in (mth.MTH_EINVAL, mth.MTH_EUNSUPPORTED), (b, rc)
+        assert mth.last_error().startswith("mth_decoder_create"), mth.last_error()
+    assert lib.mth_decoder_step(None, 1, 1, None) == mth.MTH_EINVAL
+    assert lib.mth_decoder_start(None, P, 1, 1, None) == mth.MTH_EINVAL
+    assert lib.mth_decoder_read(None, None, None, None) == mth.MTH_EINVAL
+

@@ -1,0 +1,154 @@
+"""GPU parity of the FP32 decode-step operators (dense.hip) through the C ABI
+against the CPU oracle (oracle/decoder.c, oracle.c) on seeded inputs.
+
+Bars: elementwise add/mul, RoPE and the KV append, argmax bit-exact; RMSNorm
+bit-exact up to one ulp (double sums in another order); SiLU/softmax within a
+few ulp (device exp); attention within 1e-5 relative (FP32, reordered sums).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a).copy()).to(dev)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def ulp_diff(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, np.int64(-2**31) - a, a)
+    b = np.where(b < 0, np.int64(-2**31) - b, b)
+    return np.abs(a - b)
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 4096), (16, 4096), (3, 1000), (2, 37)])
+def test_rms_norm(rows, dim, oracle, mth, dev):
+    import torch
+    print(f"rms_norm rows={rows} dim={dim}", flush=True)
+    g = np.random.default_rng(rows * 7 + dim)
+    x = (g.normal(0, 3, (rows, dim))).astype(np.float32)
+    gm = g.uniform(0.5, 1.5, dim).astype(np.float32)
+    dx, dg = dev_t(x, dev), dev_t(gm, dev)
+    y = torch.empty_like(dx)
+    mth.rms_norm(dx, dg, y, rows, dim, 1e-5)
+    want = np.empty_like(x)
+    oracle.lib.orc_rms_norm(x.ctypes.data, gm.ctypes.data, 1e-5, want.ctypes.data, rows, dim)
+    assert ulp_diff(host(y), want).max() <= 1
+    # residual add fused in: x <- t + x exactly, then the norm of the sum
+    t = g.normal(0, 1, (rows, dim)).astype(np.float32)
+    mth.add_rms_norm(dx, dev_t(t, dev), dg, y, rows, dim, 1e-5)
+    s = t + x
+    assert np.array_equal(host(dx), s)
+    oracle.lib.orc_rms_norm(s.ctypes.data, gm.ctypes.data, 1e-5, want.ctypes.data, rows, dim)
+    assert ulp_diff(host(y), want).max() <= 1
+    # in place
+    mth.rms_norm(dx, dg, dx, rows, dim, 1e-5)
+    assert ulp_diff(host(dx), want).max() <= 1
+
+
+def test_elementwise(oracle, mth, dev):
+    import torch
+    g = np.random.default_rng(5)
+    n = 11008 * 3 + 5
+    a = g.normal(0, 4, n).astype(np.float32)
+    b = g.normal(0, 1, n).astype(np.float32)
+    da, db = dev_t(a, dev), dev_t(b, dev)
+    c = torch.empty_like(da)
+    mth.add(da, db, c, n)
+    assert np.array_equal(host(c), a + b)
+    mth.mul(da, db, c, n)
+    assert np.array_equal(host(c), a * b)
+    mth.silu(da, c, n)
+    want = np.empty_like(a)
+    oracle.lib.orc_silu(a.ctypes.data, want.ctypes.data, n)
+    assert ulp_diff(host(c), want).max() <= 4
+    # SwiGLU over rows of a fused [gate | up] output
+    rows, F = 3, 11008
+    gu = g.normal(0, 2, (rows, 2 * F)).astype(np.float32)
+    y = torch.empty((rows, F), dtype=torch.float32, device=dev)
+    dgu = dev_t(gu, dev)
+    mth.silu_mul(dgu.view(-1), dgu.view(-1)[F:], y, rows, F, 2 * F, 2 * F)
+    want = oracle.silu_mul(np.ascontiguousarray(gu[:, :F]), np.ascontiguousarray(gu[:, F:]))
+    assert ulp_diff(host(y), want).max() <= 4
+
+
+@pytest.mark.parametrize("rows,dim", [(4, 192), (2, 32000), (3, 5)])
+def test_softmax(rows, dim, oracle, mth, dev):
+    import torch
+    print(f"softmax rows={rows} dim={dim}", flush=True)
+    g = np.random.default_rng(dim)
+    x = (g.normal(0, 5, (rows, dim))).astype(np.float32)
+    x[0, ::4] = -np.inf
+    y = torch.empty((rows, dim), dtype=torch.float32, device=dev)
+    mth.softmax(dev_t(x, dev), y, rows, dim)
+    want = oracle.softmax(x, rows, dim)
+    got = host(y)
+    assert np.all(got[0, ::4] == 0)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_rope_kv_bit_exact(D, oracle, mth, dev):
+    import torch
+    print(f"rope_kv D={D}", flush=True)
+    B, H, KVH, S, pos = 2, 4, 2, 40, 33
+    g = np.random.default_rng(D)
+    cos_t, sin_t = mth.rope_tables(D, S)
+    oc, os_ = oracle.rope_tables(D, S)
+    assert np.array_equal(cos_t, oc) and np.array_equal(sin_t, os_)   # same float recipe
+    q = g.normal(0, 1, (B, H * D)).astype(np.float32)
+    k = g.normal(0, 1, (B, KVH * D)).astype(np.float32)
+    v = g.normal(0, 1, (B, KVH * D)).astype(np.float32)
+    kc = torch.zeros((B, KVH, S, D), dtype=torch.float32, device=dev)
+    vc = torch.zeros_like(kc)
+    dq = dev_t(q, dev)
+    mth.rope_kv(dq, dev_t(k, dev), dev_t(v, dev), dev_t(cos_t, dev), dev_t(sin_t, dev), kc, vc, pos, B, H, KVH, D, S)
+    for b in range(B):
+        assert np.array_equal(host(dq)[b], oracle.rope_apply(q[b], H, D, pos, oc, os_))
+        assert np.array_equal(host(kc)[b, :, pos].ravel(), oracle.rope_apply(k[b], KVH, D, pos, oc, os_))
+        assert np.array_equal(host(vc)[b, :, pos].ravel(), v[b])
+    assert not host(kc)[:, :, :pos].any() and not host(kc)[:, :, pos + 1:].any()
+
+
+@pytest.mark.parametrize("D,ctx,S", [(128, 1, 192), (128, 37, 192), (128, 192, 192), (64, 100, 128),
+                                     (256, 17, 32)])
+def test_attention(D, ctx, S, oracle, mth, dev):
+    import torch
+    print(f"attention D={D} ctx={ctx} S={S}", flush=True)
+    B, H, KVH = 2, 4, 2
+    g = np.random.default_rng(ctx + D)
+    q = g.normal(0, 1, (B, H * D)).astype(np.float32)
+    kc = g.normal(0, 1, (B, KVH, S, D)).astype(np.float32)
+    vc = g.normal(0, 1, (B, KVH, S, D)).astype(np.float32)
+    out = torch.empty((B, H * D), dtype=torch.float32, device=dev)
+    mth.attention_decode(dev_t(q, dev), dev_t(kc, dev), dev_t(vc, dev), out, B, H, KVH, D, ctx, S)
+    got = host(out)
+    for b in range(B):
+        want = oracle.attention_decode(q[b], np.ascontiguousarray(kc[b]), np.ascontiguousarray(vc[b]), H, KVH, D,
+                                       ctx, S)
+        err = np.linalg.norm(got[b] - want) / np.linalg.norm(want)
+        assert err < 1e-5, (b, err)
+
+
+def test_argmax_rules(oracle, mth, dev):
+    import torch
+    n = 32000
+    g = np.random.default_rng(9)
+    rows = [g.normal(0, 1, n).astype(np.float32) for _ in range(6)]
+    rows[1][[5, 700, 31999]] = 50.0                  # ties: the first wins
+    rows[2][:] = np.nan
+    rows[3][:] = -np.inf
+    rows[4][::2] = np.nan                            # NaNs never win
+    rows[5][31999] = np.inf
+    x = np.stack(rows)
+    ids = torch.empty(6, dtype=torch.int32, device=dev)
+    mth.argmax(dev_t(x, dev), ids, 6, n)
+    assert list(host(ids)) == [oracle.argmax(r) for r in rows]
+    assert host(ids)[1] == 5 and host(ids)[2] == 0 and host(ids)[3] == 0 and host(ids)[5] == 31999
