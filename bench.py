@@ -4,7 +4,8 @@
 One "step" is one launch of the hot-path kernel over one batch of synthetic
 input.  The headline workload is BASELINE config 2 (OIL4 GEMV, W 11008x4096,
 per-128-weight FP16 codebooks, batch 1); the other configs are reported in
-"extra".  Method, per workload:
+"extra", config 5 (the 32-layer decoder, greedy, batch 1 and 16) as tokens
+per second.  Method, per workload:
   * inputs are generated once on the host (seeded) and resident in HBM before
     timing; the weight operand is replicated into >= 1 GiB of distinct copies
     and consecutive steps rotate over them, so every step streams its weights
@@ -143,6 +144,56 @@ def bench_prefill(mth, dev, M, N, K, steps, warmup, block=128):
     return dict(sec=sec, steps=n, flop=flop, copies=n_cp)
 
 
+def bench_decode(dev, batches=(1, 16)):
+    """Config 5: the 32-layer mixed-format decoder, greedy, 64-token random
+    prompts, 128 generated tokens per sequence.  The prompt is fed through the
+    same decode step (64 steps, the last one yielding the first token); the
+    remaining 127 tokens take 127 steps, timed with HIP events on the launch
+    stream.  Each step is one replay of the captured step graph."""
+    import torch
+    import decoder
+    import synth
+    cfg = synth.decoder_config()
+    t0 = time.time()
+    model = synth.decoder_model(cfg, config=5)
+    log(f"decode: weights generated in {time.time() - t0:.1f} s")
+    dec = decoder.Decoder(cfg, max_batch=max(batches))
+    dec.load(model)
+    H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["layers"]
+    layer_bytes = sum(model["layers"][0][k].nbytes for k in ("attn_norm", "ffn_norm", "wq", "cbq", "wk", "cbk", "wv",
+                                                             "cbv", "wo", "cbo", "wgate_up", "cbgate_up", "wdown"))
+    weight_bytes = L * layer_bytes + model["lm_idx"].nbytes + model["lm_cb"].nbytes + model["final_norm"].nbytes
+    del model
+    P, G = synth.PROMPT_LEN5, synth.GEN_TOKENS5
+    out = {}
+    s = torch.cuda.current_stream()
+    for B in batches:
+        prompts = synth.decoder_prompts(cfg, B, P)
+        dec.start(prompts)                 # warm-up: graph capture + one full run
+        dec.step(P + G - 1)
+        torch.cuda.synchronize()
+        dec.start(prompts)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(s)
+        dec.step(P)
+        e[1].record(s)
+        dec.step(G - 1)
+        e[2].record(s)
+        torch.cuda.synchronize()
+        t_prompt, t_dec = e[0].elapsed_time(e[1]) / 1e3, e[1].elapsed_time(e[2]) / 1e3
+        toks = dec.tokens()
+        step_ms = t_dec / (G - 1) * 1e3
+        gbs = weight_bytes / (t_dec / (G - 1)) / 1e9
+        out[f"decode_config5_b{B}"] = dict(
+            tok_per_s=B * (G - 1) / t_dec, ms_per_step=step_ms, prompt_ms=t_prompt * 1e3,
+            end_to_end_tok_per_s=B * G / (t_prompt + t_dec), weight_bytes_per_step=weight_bytes,
+            weight_GBps=gbs, frac=gbs / HBM_PEAK_GBS, generated=int(toks.shape[1] - P),
+            first_tokens=[int(t) for t in toks[0, P:P + 8]])
+        log(f"decode b={B}: {B * (G - 1) / t_dec:.1f} tok/s, {step_ms:.3f} ms/step, weights {gbs:.0f} GB/s")
+    dec.close()
+    return out
+
+
 def cpu_baseline_oil4(packed, cbs, x, M, K, block, budget_s):
     """Oracle (CPU restatement of src/kernel_oil4.cpp:31-54 with per-block
     codebooks), one thread, whole GEMVs repeated for ~budget_s seconds."""
@@ -201,7 +252,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,i2s,prefill (default all)")
+    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,i2s,prefill,decode (default all)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -250,6 +301,9 @@ def main():
         extra["oil4_prefill_gemm_512x14336x4096"] = dict(us=r["sec"] * 1e6, TFLOPs=tf, frac=tf / F16_PEAK_TFLOPS,
                                                          steps=r["steps"])
         log(f"prefill: {r['sec']*1e6:.1f} us/launch, {tf:.0f} TFLOP/s ({tf/F16_PEAK_TFLOPS:.1%})")
+
+    if want("decode"):
+        extra.update(bench_decode(dev))
 
     cpu = None
     if head is not None:

@@ -168,6 +168,13 @@ int mth_silu(const float* x, float* y, int64_t n, mth_stream_t stream);
 int mth_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t n, int64_t gstride,
                  int64_t ustride, mth_stream_t stream);
 
+/* The same activation quantised per token for the ternary down projection
+ * (quantize_per_token, src/int8_quant.cpp:24-31): q [rows][n] int8 and
+ * inv_scale [rows] = max|a|/127, as mth_quantize_per_token of the
+ * mth_silu_mul output.  n <= 12288. */
+int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows, int64_t n,
+                       int64_t gstride, int64_t ustride, mth_stream_t stream);
+
 /* oil::math::add / mul (src/math.cpp:251-258, :269-276). */
 int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);
 int mth_mul(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);

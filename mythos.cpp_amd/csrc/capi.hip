@@ -45,9 +45,9 @@ inline hipStream_t S(mth_stream_t s) { return (hipStream_t)s; }
 // generic kernels index with int64.  Reject sizes whose byte counts overflow.
 constexpr int64_t kMaxDim = (int64_t)1 << 40;
 
-// Device scratch of the batched OIL4 GEMV (partial sums of its K slices),
-// one per (device, stream): calls on one stream are ordered and may share it;
-// another stream gets its own.  Grown on demand, never shrunk.
+// Device scratch (partial sums of the batched OIL4 GEMV's K slices, argmax
+// partials), one per (device, stream): calls on one stream are ordered and
+// may share it; another stream gets its own.  Grown on demand, never shrunk.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
@@ -55,9 +55,8 @@ struct Workspace {
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-hipError_t bt_workspace(hipStream_t s, int64_t M, int64_t K, float** partial) {
-    const size_t need = mth::oil4_bt_partial_bytes(M, K);
-    *partial = nullptr;
+hipError_t workspace(hipStream_t s, size_t need, void** out) {
+    *out = nullptr;
     if (need == 0) return hipSuccess;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -75,8 +74,12 @@ hipError_t bt_workspace(hipStream_t s, int64_t M, int64_t K, float** partial) {
         w.base = p;
         w.bytes = need;
     }
-    *partial = (float*)w.base;
+    *out = w.base;
     return hipSuccess;
+}
+
+hipError_t bt_workspace(hipStream_t s, int64_t M, int64_t K, float** partial) {
+    return workspace(s, mth::oil4_bt_partial_bytes(M, K), (void**)partial);
 }
 
 #define REQUIRE(cond, ...) \
@@ -271,6 +274,15 @@ int mth_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t
     return check_launch(mth::launch_silu_mul(g, u, y, rows, n, gstride, ustride, S(stream)), "mth_silu_mul");
 }
 
+int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows, int64_t n,
+                       int64_t gstride, int64_t ustride, mth_stream_t stream) {
+    REQUIRE(g && u && q && inv_scale, "mth_silu_mul_quant: null pointer");
+    REQUIRE(rows > 0 && rows <= 65535 && gstride >= n && ustride >= n, "mth_silu_mul_quant: bad sizes");
+    REQUIRE(mth::silu_mul_quant_supported(n), "mth_silu_mul_quant: n=%lld outside 1..12288", (long long)n);
+    return check_launch(mth::launch_silu_mul_quant(g, u, q, inv_scale, rows, n, gstride, ustride, S(stream)),
+                        "mth_silu_mul_quant");
+}
+
 int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream) {
     REQUIRE(a && b && c, "mth_add: null pointer");
     REQUIRE(n > 0 && n < kMaxDim, "mth_add: bad size");
@@ -337,8 +349,14 @@ int mth_attention_decode(const float* q, const float* kcache, const float* vcach
 
 int mth_argmax(const float* logits, int32_t* ids, int64_t rows, int64_t n, mth_stream_t stream) {
     REQUIRE(logits && ids, "mth_argmax: null pointer");
-    REQUIRE(rows > 0 && rows < (1ll << 31) && n > 0 && n < (1ll << 31), "mth_argmax: bad sizes");
-    return check_launch(mth::launch_argmax(logits, rows, n, ids, nullptr, nullptr, 0, 0, S(stream)), "mth_argmax");
+    REQUIRE(rows > 0 && rows <= 65535 && n > 0 && n < (1ll << 31), "mth_argmax: bad sizes");
+    void* ws = nullptr;
+    const size_t nc = (size_t)mth::argmax_chunks(n) * (size_t)rows;
+    const hipError_t e = workspace(S(stream), nc * 8, &ws);
+    if (e != hipSuccess) return fail(MTH_EDEVICE, "mth_argmax: workspace allocation failed: %s", hipGetErrorString(e));
+    return check_launch(mth::launch_argmax(logits, rows, n, ids, nullptr, nullptr, 0, 0, (float*)ws,
+                                           (int*)((char*)ws + nc * 4), S(stream)),
+                        "mth_argmax");
 }
 
 }  // extern "C"

@@ -1,11 +1,13 @@
 // decoder.hip — the mixed-format decoder stack (include/mythos_decoder.h).
 //
 // One decode step for B sequences is a fixed sequence of launches on one
-// stream (per layer: RMSNorm, Q/K/V OIL8 GEMVs, RoPE + KV append, attention,
-// O GEMV, residual add fused into the FFN RMSNorm, gate/up OIL4 GEMV (one
-// launch over 2*ffn rows when gate and up are adjacent), SwiGLU, ternary down
-// GEMV with per-token int8 quantisation fused in; the next layer's RMSNorm
-// takes the second residual add).  Everything that changes from step to step
+// stream (per layer: RMSNorm, Q/K/V OIL8 GEMVs, RoPE + KV append + attention
+// in one kernel, O GEMV, residual add fused into the FFN RMSNorm, gate/up
+// OIL4 GEMV (one launch over 2*ffn rows when gate and up are adjacent),
+// SwiGLU fused with the per-token int8 quantisation, ternary down GEMV on the
+// int8 activations; the next layer's RMSNorm takes the second residual add;
+// after the last layer: final norm, lm_head, a two-stage greedy argmax whose
+// last launch also advances the step counter).  Everything that changes from step to step
 // (position, input token) is read from device memory: the step counter and
 // the token history.  So the sequence captures into one HIP graph that is
 // replayed for every step.  All buffers are allocated at create; the graph
@@ -30,9 +32,10 @@ struct mth_decoder {
 
     void* block = nullptr;  // one device allocation for every buffer below
     float *x = nullptr, *h = nullptr, *t = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
-    float *gu = nullptr, *a = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr;
-    float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr;
-    int *hist = nullptr, *step = nullptr, *ids = nullptr;
+    float *gu = nullptr, *a_inv = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr, *arg_v = nullptr;
+    int8_t* aq = nullptr;
+    int *hist = nullptr, *step = nullptr, *ids = nullptr, *arg_i = nullptr;
     int64_t hist_stride = 0, layer_kv = 0;
 
     int64_t batch = 0, prompt_len = 0, steps = 0;
@@ -83,29 +86,29 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         TRY(mth::launch_oil8_gemv(L.wq, L.cbq, d->h, d->q, QD, H, B, s));
         TRY(mth::launch_oil8_gemv(L.wk, L.cbk, d->h, d->k, KD, H, B, s));
         TRY(mth::launch_oil8_gemv(L.wv, L.cbv, d->h, d->v, KD, H, B, s));
-        TRY(mth::launch_rope_kv(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, d->step, 0, B, (int)c.heads,
-                                (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
-        TRY(mth::launch_attention(d->q, kc, vc, d->att, d->step, 0, B, (int)c.heads, (int)c.kv_heads,
-                                  (int)c.head_dim, (int)c.max_seq, s));
+        TRY(mth::launch_rope_attention(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, d->att, d->step, B,
+                                       (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
         TRY(mth::launch_oil8_gemv(L.wo, L.cbo, d->att, d->t, H, QD, B, s));
         TRY(mth::launch_rms_norm(d->x, d->t, L.ffn_norm, d->h, B, H, c.eps, s));
         const int64_t nb = c.cb_block ? H / c.cb_block : 1;
         const bool fused = L.wup == L.wgate + F * (H / 2) && (c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
+        // gate/up, then silu(gate)*up quantised to int8 per token (once, not
+        // per workgroup of the down projection), then the ternary GEMV on the
+        // int8 activations
         if (fused) {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
-            TRY(mth::launch_silu_mul(d->gu, d->gu + F, d->a, B, F, 2 * F, 2 * F, s));
+            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + F, d->aq, d->a_inv, B, F, 2 * F, 2 * F, s));
         } else {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
-            TRY(mth::launch_silu_mul(d->gu, d->gu + B * F, d->a, B, F, F, F, s));
+            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, B, F, F, F, s));
         }
-        TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, d->a, nullptr, nullptr, d->t, H, F, B, s));
+        TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, B, s));
     }
     TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
     TRY(mth::launch_oil8_gemv(d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, B, s));
     TRY(mth::launch_argmax(d->logits, B, c.vocab, d->ids, d->hist, d->step, (int)d->hist_stride, (int)d->prompt_len,
-                           s));
-    TRY(mth::launch_advance(d->step, s));
+                           d->arg_v, d->arg_i, s));
 #undef TRY
     return hipSuccess;
 }
@@ -126,6 +129,8 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         return api_fail(MTH_EINVAL, "mth_decoder_create: max_batch=%lld outside 1..16", (long long)c.max_batch);
     if (c.hidden % 4 != 0 || c.ffn % 4 != 0)
         return api_fail(MTH_EINVAL, "mth_decoder_create: hidden and ffn must be multiples of 4");
+    if (!mth::silu_mul_quant_supported(c.ffn))
+        return api_fail(MTH_EUNSUPPORTED, "mth_decoder_create: ffn=%lld above 12288", (long long)c.ffn);
     if (c.heads % c.kv_heads != 0) return api_fail(MTH_EINVAL, "mth_decoder_create: heads %% kv_heads != 0");
     if (c.cb_block < 0 || (c.cb_block > 0 && c.hidden % c.cb_block != 0))
         return api_fail(MTH_EINVAL, "mth_decoder_create: cb_block=%lld does not divide hidden", (long long)c.cb_block);
@@ -153,7 +158,10 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->t, (size_t)(B * H) * 4},       {(void**)&d->q, (size_t)(B * QD) * 4},
         {(void**)&d->k, (size_t)(B * KD) * 4},      {(void**)&d->v, (size_t)(B * KD) * 4},
         {(void**)&d->att, (size_t)(B * QD) * 4},    {(void**)&d->gu, (size_t)(B * 2 * F) * 4},
-        {(void**)&d->a, (size_t)(B * F) * 4},       {(void**)&d->logits, (size_t)(B * c.vocab) * 4},
+        {(void**)&d->aq, (size_t)(B * F)},          {(void**)&d->a_inv, (size_t)B * 4},
+        {(void**)&d->logits, (size_t)(B * c.vocab) * 4},
+        {(void**)&d->arg_v, (size_t)(B * mth::argmax_chunks(c.vocab)) * 4},
+        {(void**)&d->arg_i, (size_t)(B * mth::argmax_chunks(c.vocab)) * 4},
         {(void**)&d->kc, (size_t)(c.layers * d->layer_kv) * 4},
         {(void**)&d->vc, (size_t)(c.layers * d->layer_kv) * 4},
         {(void**)&d->rope_cos, (size_t)(c.max_seq * (c.head_dim / 2)) * 4},

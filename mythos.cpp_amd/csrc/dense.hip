@@ -33,6 +33,7 @@ namespace mth {
 namespace {
 
 constexpr int kT = 256;  // threads per workgroup (4 waves)
+constexpr int kArgChunk = 2048;  // argmax columns per stage-1 workgroup
 
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
@@ -211,105 +212,228 @@ __global__ __launch_bounds__(kT) void rope_kv_k(float* __restrict__ q, const flo
 }
 
 // ---- decode attention --------------------------------------------------------
-// Workgroup (head h, token b): ctx = *step + ctx0 + 1 cached positions of kv
-// head h % kv_heads.  D = 64 * HPL; each lane holds HPL elements of q.
-// Scores: one position per wave iteration (coalesced K row, wave sum);
-// softmax in LDS; P*V: waves split positions, lanes own HPL columns.
-template <int HPL>
-__global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, const float* __restrict__ kc,
-                                                  const float* __restrict__ vc, float* __restrict__ out,
-                                                  const int* __restrict__ step, int ctx0, int heads, int kv_heads,
-                                                  int max_seq, float scale) {
-    constexpr int D = 64 * HPL;
-    extern __shared__ float sc[];           // [ctx] scores, then probabilities
+// Workgroup (head h, token b) over ctx = *step + ctx0 + 1 positions of kv
+// head kh = h % kv_heads, cache rows [b][kh][t][D].
+// Scores: one position per thread (t = tid, tid + 256, ...), the dot product
+// over d in order with separate multiply and add (the reference's scalar
+// loop, src/transformer.cpp:200-232), K rows as float4 loads, q broadcast
+// from LDS: every thread has its whole row in flight at once.  Softmax in
+// LDS.  P*V: thread = (float4 column group, position slice); slices are
+// summed through LDS in a fixed order.
+// ROPE: the current token's q/k/v (pre-rotation, [B][heads*D] and
+// [B][kv_heads*D]) are rotated here (RotaryEmbedding::apply), the current
+// position's k/v come from LDS, and the workgroup with h < kv_heads writes
+// them to the cache row pos (KVCache::append) -- no workgroup reads that row
+// from memory in this launch.  Without ROPE, q is already rotated and all
+// ctx rows come from the cache.
+template <int D, bool ROPE>
+__global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, const float* __restrict__ kin,
+                                                  const float* __restrict__ vin, const float* __restrict__ cos_t,
+                                                  const float* __restrict__ sin_t, float* kc, float* vc,
+                                                  float* __restrict__ out, const int* __restrict__ step, int ctx0,
+                                                  int heads, int kv_heads, int max_seq, float scale) {
+    constexpr int G = D / 4;        // float4 column groups
+    constexpr int SL = kT / G;      // position slices in P*V
+    extern __shared__ float sc[];   // [max_seq] scores, then probabilities
+    __shared__ __align__(16) float qs[D], ks[D], vs[D];
+    __shared__ float4 part[SL][G];
     __shared__ float redf[4];
-    __shared__ float part[4][D];
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int ctx = (step ? *step : 0) + ctx0 + 1;
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int pos = (step ? *step : 0) + ctx0;  // the last position attended to
+    const int ctx = pos + 1;
     const int kh = h % kv_heads;
+    const int64_t crow = ((int64_t)b * kv_heads + kh) * max_seq;  // cache row of position 0
     const float* qh = q + ((int64_t)b * heads + h) * D;
-    const float* kb = kc + ((int64_t)b * kv_heads + kh) * max_seq * D;
-    const float* vb = vc + ((int64_t)b * kv_heads + kh) * max_seq * D;
-    float qv[HPL];
-#pragma unroll
-    for (int j = 0; j < HPL; ++j) qv[j] = qh[lane + 64 * j];
-    for (int t = wave; t < ctx; t += 4) {
+    if (ROPE) {
+        const float* cr = cos_t + (int64_t)pos * (D / 2);
+        const float* sr = sin_t + (int64_t)pos * (D / 2);
+        const float* kh_in = kin + ((int64_t)b * kv_heads + kh) * D;
+        const float* vh_in = vin + ((int64_t)b * kv_heads + kh) * D;
+        if (tid < D / 2) {
+            const float c = cr[tid], s = sr[tid];
+            const float q1 = qh[tid], q2 = qh[tid + D / 2];
+            qs[tid] = q1 * c - q2 * s;
+            qs[tid + D / 2] = q1 * s + q2 * c;
+            const float k1 = kh_in[tid], k2 = kh_in[tid + D / 2];
+            ks[tid] = k1 * c - k2 * s;
+            ks[tid + D / 2] = k1 * s + k2 * c;
+            vs[tid] = vh_in[tid];
+            vs[tid + D / 2] = vh_in[tid + D / 2];
+        }
+        __syncthreads();
+        if (h < kv_heads && tid < D) {
+            kc[(crow + pos) * D + tid] = ks[tid];
+            vc[(crow + pos) * D + tid] = vs[tid];
+        }
+    } else {
+        if (tid < D) qs[tid] = qh[tid];
+        __syncthreads();
+    }
+    const int nmem = ROPE ? pos : ctx;  // positions read from the cache
+    float mx = -INFINITY;
+    for (int t = tid; t < ctx; t += kT) {
+        const float* kr = t < nmem ? kc + (crow + t) * D : ks;
         float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < HPL; ++j) s = fmaf(qv[j], kb[(int64_t)t * D + lane + 64 * j], s);
-        s = wave_sum_f(s);
-        if (lane == 0) sc[t] = (s * scale);
+        for (int d = 0; d < D; d += 4) {
+            const float4 k4 = *(const float4*)(kr + d);
+            const float4 q4 = *(const float4*)(qs + d);
+            s = s + q4.x * k4.x;
+            s = s + q4.y * k4.y;
+            s = s + q4.z * k4.z;
+            s = s + q4.w * k4.w;
+        }
+        s = s * scale;
+        sc[t] = s;
+        mx = fmaxf(mx, s);
     }
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int t = threadIdx.x; t < ctx; t += kT) mx = fmaxf(mx, sc[t]);
     mx = block_max(mx, redf);
     float sum = 0.0f;
-    for (int t = threadIdx.x; t < ctx; t += kT) {
-        const float e = expf((sc[t] - mx));
+    for (int t = tid; t < ctx; t += kT) {
+        const float e = expf(sc[t] - mx);
         sc[t] = e;
         sum += e;
     }
-    sum = block_sum(sum, redf);
-    const float inv = (1.0f / sum);
-    __syncthreads();
-    float acc[HPL];
-#pragma unroll
-    for (int j = 0; j < HPL; ++j) acc[j] = 0.0f;
-    for (int t = wave; t < ctx; t += 4) {
-        const float p = (sc[t] * inv);
-#pragma unroll
-        for (int j = 0; j < HPL; ++j) acc[j] = fmaf(p, vb[(int64_t)t * D + lane + 64 * j], acc[j]);
+    sum = block_sum(sum, redf);   // its barriers also publish sc[]
+    const float inv = 1.0f / sum;
+    const int g = tid % G, sl = tid / G;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t = sl; t < ctx; t += SL) {
+        const float p = sc[t] * inv;
+        const float4 v4 = t < nmem ? *(const float4*)(vc + (crow + t) * D + 4 * g) : *(const float4*)(vs + 4 * g);
+        acc.x = fmaf(p, v4.x, acc.x);
+        acc.y = fmaf(p, v4.y, acc.y);
+        acc.z = fmaf(p, v4.z, acc.z);
+        acc.w = fmaf(p, v4.w, acc.w);
     }
-#pragma unroll
-    for (int j = 0; j < HPL; ++j) part[wave][lane + 64 * j] = acc[j];
+    part[sl][g] = acc;
     __syncthreads();
-    float* ob = out + ((int64_t)b * heads + h) * D;
-    for (int d = threadIdx.x; d < D; d += kT) ob[d] = (part[0][d] + part[1][d]) + (part[2][d] + part[3][d]);
+    if (tid < G) {
+        float4 r = part[0][tid];
+#pragma unroll
+        for (int j = 1; j < SL; ++j) {
+            const float4 o = part[j][tid];
+            r.x += o.x;
+            r.y += o.y;
+            r.z += o.z;
+            r.w += o.w;
+        }
+        *(float4*)(out + ((int64_t)b * heads + h) * D + 4 * tid) = r;
+    }
+}
+
+// ---- SwiGLU fused with the per-token int8 quantisation ----------------------
+// One workgroup per token: a = silu(g) * u kept in registers, then
+// quantize_per_token (src/int8_quant.cpp:8-31): max|a| (floor 1e-10),
+// scale = 127/max, q = (int8)round_half_away(a * scale), inv = max/127.
+// Writes q [B][n] and inv [B]; n <= kT * kSQ.
+constexpr int kSQ = 48;
+__global__ __launch_bounds__(kT) void silu_mul_quant_k(const float* __restrict__ g, const float* __restrict__ u,
+                                                       int8_t* __restrict__ q, float* __restrict__ inv_scale, int n,
+                                                       int64_t gstride, int64_t ustride) {
+    __shared__ float redf[4];
+    const int r = blockIdx.x;
+    const float* gr = g + r * gstride;
+    const float* ur = u + r * ustride;
+    float a[kSQ];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kSQ; ++j) {
+        const int i = threadIdx.x + j * kT;
+        a[j] = i < n ? silu1(gr[i]) * ur[i] : 0.0f;
+        m = fmaxf(m, fabsf(a[j]));
+    }
+    m = block_max(m, redf);
+    if (m < 1e-10f) m = 1e-10f;
+    const float sc = __fdiv_rn(127.0f, m);
+    int8_t* qr = q + (int64_t)r * n;
+#pragma unroll
+    for (int j = 0; j < kSQ; ++j) {
+        const int i = threadIdx.x + j * kT;
+        if (i < n) qr[i] = (int8_t)quant_i8(a[j], sc);
+    }
+    if (threadIdx.x == 0) inv_scale[r] = __fdiv_rn(m, 127.0f);
 }
 
 // ---- greedy argmax + token bookkeeping ---------------------------------------
-// Row b of logits [B][n]: first index of the maximum (NaN never wins; all-NaN
-// or all -inf rows give 0).  Writes ids[b]; with hist, also the next input
-// token hist[b][s + 1] once the prompt is consumed (s + 1 >= prompt_len).
-__global__ __launch_bounds__(kT) void argmax_k(const float* __restrict__ logits, int64_t n, int* __restrict__ ids,
-                                               int* __restrict__ hist, const int* __restrict__ step, int hist_stride,
-                                               int prompt_len) {
-    __shared__ float bv[kT];
-    __shared__ int bi[kT];
-    const float* r = logits + (int64_t)blockIdx.x * n;
+// Sampler::greedy: first index of the maximum of a row; NaN never wins,
+// all-NaN / all -inf rows give 0.  (value, index) pairs combine by larger
+// value, then smaller index.
+__device__ __forceinline__ void amax_merge(float& v, int& i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+__device__ __forceinline__ void block_amax(float& v, int& i, float* bv, int* bi) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax_merge(v, i, __shfl_xor(v, o, MTH_WAVE), __shfl_xor(i, o, MTH_WAVE));
+    if (lane == 0) {
+        bv[wave] = v;
+        bi[wave] = i;
+    }
+    __syncthreads();
+    v = bv[0];
+    i = bi[0];
+#pragma unroll
+    for (int w = 1; w < kT / 64; ++w) amax_merge(v, i, bv[w], bi[w]);
+}
+
+// Stage 1: workgroup (chunk c, row b) scans columns [c*chunk, (c+1)*chunk)
+// with float4 loads and writes its (value, index) pair.  chunk % 4 == 0.
+__global__ __launch_bounds__(kT) void argmax_part_k(const float* __restrict__ logits, int64_t n, int chunk,
+                                                    float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float bv[kT / 64];
+    __shared__ int bi[kT / 64];
+    const float* r = logits + (int64_t)blockIdx.y * n;
+    const int64_t c0 = (int64_t)blockIdx.x * chunk;
+    const int64_t c1 = c0 + chunk < n ? c0 + chunk : n;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int64_t i = threadIdx.x; i < n; i += kT) {
-        const float x = r[i];
-        if (x > v) {
-            v = x;
-            idx = (int)i;
+    const bool vec = (n % 4) == 0;
+    for (int64_t i = c0 + 4 * threadIdx.x; i < c1; i += 4 * kT) {
+        if (vec && i + 3 < c1) {
+            const float4 x = ldf4(r + i);
+            if (x.x > v) { v = x.x; idx = (int)i; }
+            if (x.y > v) { v = x.y; idx = (int)i + 1; }
+            if (x.z > v) { v = x.z; idx = (int)i + 2; }
+            if (x.w > v) { v = x.w; idx = (int)i + 3; }
+        } else {
+            for (int64_t j = i; j < i + 4 && j < c1; ++j)
+                if (r[j] > v) { v = r[j]; idx = (int)j; }
         }
     }
-    bv[threadIdx.x] = v;
-    bi[threadIdx.x] = idx;
-    __syncthreads();
-    for (int o = kT / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) {
-            const float v2 = bv[threadIdx.x + o];
-            const int i2 = bi[threadIdx.x + o];
-            if (v2 > bv[threadIdx.x] || (v2 == bv[threadIdx.x] && i2 < bi[threadIdx.x])) {
-                bv[threadIdx.x] = v2;
-                bi[threadIdx.x] = i2;
-            }
+    block_amax(v, idx, bv, bi);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.y * gridDim.x + blockIdx.x] = v;
+        pi[blockIdx.y * gridDim.x + blockIdx.x] = idx;
+    }
+}
+
+// Stage 2 (one workgroup): row b's result from its nc partials -> ids[b];
+// with hist, the next input token hist[b][s + 1] once the prompt is consumed
+// (s + 1 >= prompt_len); with step, then advances *step (the last launch of a
+// decode step: every earlier kernel of the step has read it).
+__global__ __launch_bounds__(kT) void argmax_final_k(const float* __restrict__ pv, const int* __restrict__ pi, int nc,
+                                                     int rows, int* __restrict__ ids, int* __restrict__ hist,
+                                                     int* step, int hist_stride, int prompt_len) {
+    __shared__ float bv[kT / 64];
+    __shared__ int bi[kT / 64];
+    const int s = step ? *step : 0;
+    for (int b = 0; b < rows; ++b) {
+        float v = -INFINITY;
+        int idx = 0x7fffffff;
+        for (int c = threadIdx.x; c < nc; c += kT) amax_merge(v, idx, pv[b * nc + c], pi[b * nc + c]);
+        block_amax(v, idx, bv, bi);
+        if (threadIdx.x == 0) {
+            const int best = idx == 0x7fffffff ? 0 : idx;
+            if (ids) ids[b] = best;
+            if (hist && s + 1 >= prompt_len && s + 1 < hist_stride) hist[(int64_t)b * hist_stride + s + 1] = best;
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
-        const int best = bi[0] == 0x7fffffff ? 0 : bi[0];
-        if (ids) ids[blockIdx.x] = best;
-        if (hist) {
-            const int s = *step;
-            if (s + 1 >= prompt_len && s + 1 < hist_stride) hist[(int64_t)blockIdx.x * hist_stride + s + 1] = best;
-        }
-    }
+    if (step && threadIdx.x == 0) *step = s + 1;
 }
 
 // x[b] = emb[id] with id = hist[b][*step] (ids outside [0, vocab) -> 0).
@@ -322,10 +446,6 @@ __global__ __launch_bounds__(kT) void embed_k(const float* __restrict__ emb, con
     const float* src = emb + (int64_t)id * dim;
     float* dst = x + (int64_t)b * dim;
     for (int i = threadIdx.x * 4; i < dim; i += kT * 4) *(float4*)(dst + i) = ldf4(src + i);
-}
-
-__global__ void advance_k(int* step) {
-    if (threadIdx.x == 0) *step += 1;
 }
 
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + kT - 1) / kT); }
@@ -380,34 +500,59 @@ bool attention_supported(int head_dim, int max_seq) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) && max_seq > 0 && max_seq <= 16384;
 }
 
-hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
-                            int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
+template <bool ROPE>
+static hipError_t run_attention(const float* q, const float* k, const float* v, const float* cos_t,
+                                const float* sin_t, float* kc, float* vc, float* out, const int* step, int ctx0,
+                                int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
     const dim3 grid((unsigned)heads, (unsigned)batch);
     if (head_dim == 64)
-        attention_k<1><<<grid, kT, lds, s>>>(q, kc, vc, out, step, ctx0, heads, kv_heads, max_seq, scale);
+        attention_k<64, ROPE><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads, kv_heads,
+                                                    max_seq, scale);
     else if (head_dim == 128)
-        attention_k<2><<<grid, kT, lds, s>>>(q, kc, vc, out, step, ctx0, heads, kv_heads, max_seq, scale);
+        attention_k<128, ROPE><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+                                                     kv_heads, max_seq, scale);
     else
-        attention_k<4><<<grid, kT, lds, s>>>(q, kc, vc, out, step, ctx0, heads, kv_heads, max_seq, scale);
+        attention_k<256, ROPE><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+                                                     kv_heads, max_seq, scale);
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* logits, int64_t rows, int64_t n, int* ids, int* hist, const int* step,
-                         int hist_stride, int prompt_len, hipStream_t s) {
-    argmax_k<<<(unsigned)rows, kT, 0, s>>>(logits, n, ids, hist, step, hist_stride, prompt_len);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
+                            int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
+    return run_attention<false>(q, nullptr, nullptr, nullptr, nullptr, (float*)kc, (float*)vc, out, step, ctx0,
+                                batch, heads, kv_heads, head_dim, max_seq, s);
+}
+
+hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
+                                 const float* sin_t, float* kc, float* vc, float* out, const int* step,
+                                 int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
+    return run_attention<true>(q, k, v, cos_t, sin_t, kc, vc, out, step, 0, batch, heads, kv_heads, head_dim,
+                               max_seq, s);
+}
+
+bool silu_mul_quant_supported(int64_t n) { return n > 0 && n <= (int64_t)kT * kSQ; }
+
+hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows,
+                                 int64_t n, int64_t gstride, int64_t ustride, hipStream_t s) {
+    silu_mul_quant_k<<<(unsigned)rows, kT, 0, s>>>(g, u, q, inv_scale, (int)n, gstride, ustride);
+    return hipGetLastError();
+}
+
+int argmax_chunks(int64_t n) { return (int)((n + kArgChunk - 1) / kArgChunk); }
+
+hipError_t launch_argmax(const float* logits, int64_t rows, int64_t n, int* ids, int* hist, int* step,
+                         int hist_stride, int prompt_len, float* pv, int* pi, hipStream_t s) {
+    const int nc = argmax_chunks(n);
+    argmax_part_k<<<dim3((unsigned)nc, (unsigned)rows), kT, 0, s>>>(logits, n, kArgChunk, pv, pi);
+    argmax_final_k<<<1, kT, 0, s>>>(pv, pi, nc, (int)rows, ids, hist, step, hist_stride, prompt_len);
     return hipGetLastError();
 }
 
 hipError_t launch_embed(const float* emb, const int* hist, const int* step, int hist_stride, float* x, int64_t batch,
                         int dim, int vocab, hipStream_t s) {
     embed_k<<<(unsigned)batch, kT, 0, s>>>(emb, hist, step, hist_stride, x, dim, vocab);
-    return hipGetLastError();
-}
-
-hipError_t launch_advance(int* step, hipStream_t s) {
-    advance_k<<<1, 64, 0, s>>>(step);
     return hipGetLastError();
 }
 

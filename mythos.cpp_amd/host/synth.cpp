@@ -13,6 +13,7 @@
 // drawn one after another continue a single stream.
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 
 namespace {
 
@@ -33,6 +34,24 @@ inline uint64_t next_u64(uint64_t* st) {
     st[0] = rotl(s0, 24) ^ s1 ^ (s1 << 16);
     st[1] = rotl(s1, 37);
     return r;
+}
+
+// FP32 -> FP16 bits, rounding toward zero (the reference's float_to_half,
+// src/codebook.cpp:16-34): exponent rebias, mantissa truncated; values past
+// the FP16 range become infinity, NaN stays NaN; subnormal results keep the
+// shifted mantissa, smaller magnitudes flush to a signed zero.
+inline uint16_t f32_to_f16_trunc(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const int e = (int)((u >> 23) & 0xFF) - 127 + 15;
+    const uint32_t mant = u & 0x007FFFFFu;
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        return (uint16_t)(sign | (((mant | 0x00800000u) >> (1 - e)) >> 13));
+    }
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u | (mant ? 0x0200u : 0u));
+    return (uint16_t)(sign | ((uint32_t)e << 10) | (mant >> 13));
 }
 
 }  // namespace
@@ -66,6 +85,34 @@ void mth_synth_uniform_int(uint64_t* st, int8_t* out, int64_t n, int lo, int hi)
     }
 }
 
+// OIL4 nibbles packed two per byte: element 2i (low nibble) then 2i+1, each
+// the top 4 bits of one next_u64() (the same draws as mth_synth_bits(.., 4)
+// followed by packing).
+void mth_synth_nibbles(uint64_t* st, uint8_t* out, int64_t nbytes) {
+    for (int64_t i = 0; i < nbytes; ++i) {
+        const uint8_t lo = (uint8_t)(next_u64(st) >> 60);
+        const uint8_t hi = (uint8_t)(next_u64(st) >> 60);
+        out[i] = (uint8_t)(lo | (hi << 4));
+    }
+}
+
+// Ternary codes t+1 = uniform_int(0, 2) packed four per byte, element 4i+j
+// in bits 2j (the same draws as mth_synth_uniform_int(.., 0, 2) + packing).
+void mth_synth_ternary(uint64_t* st, uint8_t* out, int64_t nbytes) {
+    const uint64_t limit = UINT64_MAX - (UINT64_MAX % 3);
+    for (int64_t i = 0; i < nbytes; ++i) {
+        uint32_t b = 0;
+        for (int j = 0; j < 4; ++j) {
+            uint64_t v;
+            do {
+                v = next_u64(st);
+            } while (v >= limit);
+            b |= (uint32_t)(v % 3) << (2 * j);
+        }
+        out[i] = (uint8_t)b;
+    }
+}
+
 void mth_synth_uniform_i32(uint64_t* st, int32_t* out, int64_t n, int lo, int hi) {
     const uint64_t range = (uint64_t)((int64_t)hi - lo + 1);
     const uint64_t limit = UINT64_MAX - (UINT64_MAX % range);
@@ -88,6 +135,16 @@ void mth_synth_normal(uint64_t* st, float* out, int64_t n, double mean, double s
         const double r = std::sqrt(-2.0 * std::log(u1));
         out[i] = (float)(mean + stddev * r * std::cos(two_pi * u2));
         if (i + 1 < n) out[i + 1] = (float)(mean + stddev * r * std::sin(two_pi * u2));
+    }
+}
+
+// normals as mth_synth_normal draws them, stored as truncated FP16 bits
+void mth_synth_normal_f16(uint64_t* st, uint16_t* out, int64_t n, double mean, double stddev) {
+    float buf[256];
+    for (int64_t i = 0; i < n; i += 256) {
+        const int64_t m = n - i < 256 ? n - i : 256;
+        mth_synth_normal(st, buf, m, mean, stddev);
+        for (int64_t j = 0; j < m; ++j) out[i + j] = f32_to_f16_trunc(buf[j]);
     }
 }
 

@@ -25,7 +25,8 @@ EXPORTS = (
     "mth_quantize_per_token", "mth_dequantize_per_tensor",
     "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
     "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
-    "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_add", "mth_mul", "mth_softmax",
+    "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_silu_mul_quant", "mth_add", "mth_mul",
+    "mth_softmax",
     "mth_rope_tables", "mth_rope_kv", "mth_attention_decode", "mth_argmax",
 )
 
@@ -76,6 +77,7 @@ _SIG = {
     "mth_add_rms_norm": [VP, VP, VP, VP, I64, I64, F32, VP],
     "mth_silu": [VP, VP, I64, VP],
     "mth_silu_mul": [VP, VP, VP, I64, I64, I64, I64, VP],
+    "mth_silu_mul_quant": [VP, VP, VP, VP, I64, I64, I64, I64, VP],
     "mth_add": [VP, VP, VP, I64, VP],
     "mth_mul": [VP, VP, VP, I64, VP],
     "mth_softmax": [VP, VP, I64, I64, VP],
@@ -264,6 +266,14 @@ def silu_mul(g, u, y, rows, n, gstride=None, ustride=None, stream=None):
     gs, us = gstride or n, ustride or n
     _check(_lib.mth_silu_mul(_ptr(g, t.float32, (rows - 1) * gs + n, "g"), _ptr(u, t.float32, (rows - 1) * us + n, "u"),
                              _ptr(y, t.float32, rows * n, "y"), rows, n, gs, us, _stream(stream)))
+
+
+def silu_mul_quant(g, u, q, inv_scale, rows, n, gstride=None, ustride=None, stream=None):
+    t = _torch()
+    gs, us = gstride or n, ustride or n
+    _check(_lib.mth_silu_mul_quant(_ptr(g, t.float32, (rows - 1) * gs + n, "g"),
+                                   _ptr(u, t.float32, (rows - 1) * us + n, "u"), _ptr(q, t.int8, rows * n, "q"),
+                                   _ptr(inv_scale, t.float32, rows, "inv_scale"), rows, n, gs, us, _stream(stream)))
 
 
 def add(a, b, c, n, stream=None):

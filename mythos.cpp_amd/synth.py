@@ -37,8 +37,11 @@ _lib.mth_synth_bits.argtypes = [_VP, _VP, _I64, C.c_int]
 _lib.mth_synth_uniform_int.argtypes = [_VP, _VP, _I64, C.c_int, C.c_int]
 _lib.mth_synth_normal.argtypes = [_VP, _VP, _I64, C.c_double, C.c_double]
 _lib.mth_synth_uniform_i32.argtypes = [_VP, _VP, _I64, C.c_int, C.c_int]
+_lib.mth_synth_nibbles.argtypes = [_VP, _VP, _I64]
+_lib.mth_synth_ternary.argtypes = [_VP, _VP, _I64]
+_lib.mth_synth_normal_f16.argtypes = [_VP, _VP, _I64, C.c_double, C.c_double]
 for _f in ("mth_synth_seed", "mth_synth_u64", "mth_synth_bits", "mth_synth_uniform_int", "mth_synth_normal",
-           "mth_synth_uniform_i32"):
+           "mth_synth_uniform_i32", "mth_synth_nibbles", "mth_synth_ternary", "mth_synth_normal_f16"):
     getattr(_lib, _f).restype = None
 
 
@@ -67,6 +70,24 @@ class Stream:
     def uniform_i32(self, shape, lo: int, hi: int) -> np.ndarray:
         out = np.empty(shape, np.int32)
         _lib.mth_synth_uniform_i32(self.st.ctypes.data, out.ctypes.data, out.size, lo, hi)
+        return out
+
+    def nibbles(self, rows: int, cols: int) -> np.ndarray:
+        """[rows][cols/2] packed 4-bit indices (= pack_nibbles(bits(.., 4)))."""
+        out = np.empty((rows, cols // 2), np.uint8)
+        _lib.mth_synth_nibbles(self.st.ctypes.data, out.ctypes.data, out.size)
+        return out
+
+    def ternary(self, rows: int, cols: int) -> np.ndarray:
+        """[rows][cols/4] packed codes t+1 (= pack_ternary(uniform_int(.., 0, 2) - 1))."""
+        out = np.empty((rows, cols // 4), np.uint8)
+        _lib.mth_synth_ternary(self.st.ctypes.data, out.ctypes.data, out.size)
+        return out
+
+    def normal_f16(self, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+        """FP16 bits of normal(shape) by the truncating float_to_half."""
+        out = np.empty(shape, np.uint16)
+        _lib.mth_synth_normal_f16(self.st.ctypes.data, out.ctypes.data, out.size, mean, std)
         return out
 
     def normal(self, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
@@ -123,7 +144,7 @@ def oil4(M: int, K: int, batch: int, block: int = 128, config: int = 2):
     g = stream(config)
     packed = pack_nibbles(g.bits((M, K), 4))
     ncb = M * (K // block) if block else 1
-    cbs = float_to_half_trunc(g.normal((ncb, 16), 0.0, 0.02))
+    cbs = g.normal_f16((ncb, 16), 0.0, 0.02)
     x = g.normal((batch, K))
     return packed, cbs.reshape(-1), x
 
@@ -151,7 +172,7 @@ def prefill(M: int, N: int, K: int, block: int = 128, config: int = 4):
     g = stream(config)
     a = bf16_bits(g.normal((M, K)))
     packed = pack_nibbles(g.bits((N, K), 4))
-    cbs = float_to_half_trunc(g.normal((N * (K // block), 16), 0.0, 0.02))
+    cbs = g.normal_f16((N * (K // block), 16), 0.0, 0.02)
     return a, packed, cbs.reshape(-1)
 
 
@@ -210,12 +231,12 @@ def decoder_model(cfg: dict, config: int = 5, random_gamma: bool = False) -> dic
         half = F * (H // B) if B else 1      # codebooks per tensor
         cbs = np.empty((2 * half, 16), np.uint16)
         for i in range(2):
-            gu[i * F:(i + 1) * F] = pack_nibbles(g.bits((F, H), 4))
-            cbs[i * half:(i + 1) * half] = float_to_half_trunc(g.normal((half, 16), 0.0, 0.02))
+            gu[i * F:(i + 1) * F] = g.nibbles(F, H)
+            cbs[i * half:(i + 1) * half] = g.normal_f16((half, 16), 0.0, 0.02)
         ly["wgate_up"], ly["cbgate_up"] = gu, cbs.reshape(-1)
         ly["wgate"], ly["wup"] = gu[:F], gu[F:]
         ly["cbgate"], ly["cbup"] = cbs[:half].reshape(-1), cbs[half:].reshape(-1)
-        ly["wdown"] = pack_ternary(g.uniform_int((H, F), 0, 2) - 1)
+        ly["wdown"] = g.ternary(H, F)
         ly["down_scale"] = np.float32(W_SCALE_TERNARY)
         model["layers"].append(ly)
     model["final_norm"] = gamma()

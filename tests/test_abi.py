@@ -84,6 +84,7 @@ CASES = [
     ("mth_add_rms_norm", (P, NULL, P, P, 1, 8, C.c_float(1e-5), NULL), (P, P, P, P, 1, -8, C.c_float(1e-5), NULL)),
     ("mth_silu", (NULL, P, 8, NULL), (P, P, 0, NULL)),
     ("mth_silu_mul", (P, NULL, P, 1, 8, 8, 8, NULL), (P, P, P, 1, 8, 4, 8, NULL)),
+    ("mth_silu_mul_quant", (P, P, NULL, P, 1, 8, 8, 8, NULL), (P, P, P, P, 1, 12289, 12289, 12289, NULL)),
     ("mth_add", (P, P, NULL, 8, NULL), (P, P, P, -1, NULL)),
     ("mth_mul", (NULL, P, P, 8, NULL), (P, P, P, 0, NULL)),
     ("mth_softmax", (P, NULL, 1, 8, NULL), (P, P, 1, 0, NULL)),

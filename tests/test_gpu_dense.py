@@ -79,6 +79,31 @@ def test_elementwise(oracle, mth, dev):
     assert ulp_diff(host(y), want).max() <= 4
 
 
+@pytest.mark.parametrize("rows,n", [(1, 11008), (16, 11008), (2, 100), (3, 12288)])
+def test_silu_mul_quant_bit_exact(rows, n, oracle, mth, dev):
+    """The int8 activations and scales equal quantize_per_token of the
+    device's own SwiGLU output (bit for bit); that output is checked against
+    the oracle in test_elementwise."""
+    import torch
+    print(f"silu_mul_quant rows={rows} n={n}", flush=True)
+    g = np.random.default_rng(n + rows)
+    gu = g.normal(0, 2, (rows, 2 * n)).astype(np.float32)
+    if rows > 1:
+        gu[1] = 0.0                                   # all-zero row: max_abs floor 1e-10
+    dgu = dev_t(gu, dev).view(-1)
+    a = torch.empty((rows, n), dtype=torch.float32, device=dev)
+    mth.silu_mul(dgu, dgu[n:], a, rows, n, 2 * n, 2 * n)
+    q = torch.empty((rows, n), dtype=torch.int8, device=dev)
+    inv = torch.empty(rows, dtype=torch.float32, device=dev)
+    mth.silu_mul_quant(dgu, dgu[n:], q, inv, rows, n, 2 * n, 2 * n)
+    ha = host(a)
+    wq = np.empty((rows, n), np.int8)
+    winv = np.empty(rows, np.float32)
+    oracle.lib.orc_quantize_per_token(ha.ctypes.data, wq.ctypes.data, rows, n, None, winv.ctypes.data)
+    assert np.array_equal(host(q), wq)
+    assert np.array_equal(host(inv), winv)
+
+
 @pytest.mark.parametrize("rows,dim", [(4, 192), (2, 32000), (3, 5)])
 def test_softmax(rows, dim, oracle, mth, dev):
     import torch
@@ -135,6 +160,17 @@ def test_attention(D, ctx, S, oracle, mth, dev):
                                        ctx, S)
         err = np.linalg.norm(got[b] - want) / np.linalg.norm(want)
         assert err < 1e-5, (b, err)
+
+
+@pytest.mark.parametrize("rows,n", [(16, 32000), (1, 5), (2, 2049), (3, 6143)])
+def test_argmax_shapes(rows, n, oracle, mth, dev):
+    import torch
+    g = np.random.default_rng(n)
+    x = g.normal(0, 1, (rows, n)).astype(np.float32)
+    x[0, n // 2] = x[0, n - 1] = 9.0                 # tie across chunks: the first wins
+    ids = torch.empty(rows, dtype=torch.int32, device=dev)
+    mth.argmax(dev_t(x, dev), ids, rows, n)
+    assert list(host(ids)) == [oracle.argmax(r) for r in x]
 
 
 def test_argmax_rules(oracle, mth, dev):

@@ -63,3 +63,21 @@ def test_config_generators_shapes_and_ranges():
     pk, ws, x = synth.ternary(16, 64, 1)
     codes = np.stack([(pk >> (2 * j)) & 3 for j in range(4)], -1)
     assert codes.max() <= 2 and ws == np.float32(0.0159577)
+
+
+def test_packed_draws_equal_unpacked():
+    a, b = synth.Stream(21), synth.Stream(21)
+    assert np.array_equal(a.nibbles(7, 64), synth.pack_nibbles(b.bits((7, 64), 4)))
+    assert np.array_equal(a.ternary(5, 48), synth.pack_ternary(b.uniform_int((5, 48), 0, 2) - 1))
+    assert np.array_equal(a.u64(10), b.u64(10))      # both streams advanced alike
+
+
+def test_normal_f16_is_truncated_normal():
+    a, b = synth.Stream(33), synth.Stream(33)
+    for shape in ((1001,), (64, 16)):
+        want = synth.float_to_half_trunc(b.normal(shape, 0.0, 0.02))
+        assert np.array_equal(a.normal_f16(shape, 0.0, 0.02), want)
+    f = np.concatenate([synth.Stream(34).normal(4000, 0, 1e4), synth.Stream(35).normal(4000, 0, 1e-6)])
+    c = synth.Stream(36)
+    assert np.array_equal(c.normal_f16(5, 0, 1e5), synth.float_to_half_trunc(synth.Stream(36).normal(5, 0, 1e5)))
+
