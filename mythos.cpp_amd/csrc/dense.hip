@@ -73,14 +73,15 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // residual, src/transformer.cpp:402,405), written back.  dim % 4 == 0.
 // x and y may be the same array (in-place normalisation): each thread reads
 // its own elements before it writes them.
-__global__ __launch_bounds__(kT) void rms_norm_k(float* x, const float* __restrict__ t,
-                                                 const float* __restrict__ gamma, float* y, int dim, float eps) {
-    __shared__ double red[4];
+constexpr int kRN = 1024;  // threads of the float4 RMSNorm (one float4 each at dim 4096)
+__global__ __launch_bounds__(kRN) void rms_norm_k(float* x, const float* __restrict__ t,
+                                                  const float* __restrict__ gamma, float* y, int dim, float eps) {
+    __shared__ double red[kRN / 64];
     float* xr = x + (int64_t)blockIdx.x * dim;
     const float* tr = t ? t + (int64_t)blockIdx.x * dim : nullptr;
     float* yr = y + (int64_t)blockIdx.x * dim;
     double ss = 0.0;
-    for (int i = threadIdx.x * 4; i < dim; i += kT * 4) {
+    for (int i = threadIdx.x * 4; i < dim; i += kRN * 4) {
         float4 v = ldf4(xr + i);
         if (tr) {
             const float4 a = ldf4(tr + i);
@@ -89,9 +90,14 @@ __global__ __launch_bounds__(kT) void rms_norm_k(float* x, const float* __restri
         }
         ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
     }
-    ss = block_sum(ss, red);
+    ss = wave_sum_d(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = 0.0;
+#pragma unroll
+    for (int w = 0; w < kRN / 64; ++w) ss += red[w];
     const double inv = 1.0 / sqrt(ss / (double)dim + (double)eps);
-    for (int i = threadIdx.x * 4; i < dim; i += kT * 4) {
+    for (int i = threadIdx.x * 4; i < dim; i += kRN * 4) {
         const float4 v = ldf4(xr + i);  // this thread's own elements (written above)
         const float4 g = ldf4(gamma + i);
         float4 o;
@@ -270,9 +276,7 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
         __syncthreads();
     }
     const int nmem = ROPE ? pos : ctx;  // positions read from the cache
-    float mx = -INFINITY;
-    for (int t = tid; t < ctx; t += kT) {
-        const float* kr = t < nmem ? kc + (crow + t) * D : ks;
+    auto dot = [&](const float* kr) {
         float s = 0.0f;
 #pragma unroll
         for (int d = 0; d < D; d += 4) {
@@ -283,8 +287,17 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
             s = s + q4.z * k4.z;
             s = s + q4.w * k4.w;
         }
-        s = s * scale;
+        return s * scale;
+    };
+    float mx = -INFINITY;
+    for (int t = tid; t < nmem; t += kT) {
+        const float s = dot(kc + (crow + t) * D);
         sc[t] = s;
+        mx = fmaxf(mx, s);
+    }
+    if (ROPE && tid == (pos % kT)) {  // the current position, from LDS
+        const float s = dot(ks);
+        sc[pos] = s;
         mx = fmaxf(mx, s);
     }
     mx = block_max(mx, redf);
@@ -297,16 +310,31 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
     sum = block_sum(sum, redf);   // its barriers also publish sc[]
     const float inv = 1.0f / sum;
     const int g = tid % G, sl = tid / G;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int t = sl; t < ctx; t += SL) {
-        const float p = sc[t] * inv;
-        const float4 v4 = t < nmem ? *(const float4*)(vc + (crow + t) * D + 4 * g) : *(const float4*)(vs + 4 * g);
-        acc.x = fmaf(p, v4.x, acc.x);
-        acc.y = fmaf(p, v4.y, acc.y);
-        acc.z = fmaf(p, v4.z, acc.z);
-        acc.w = fmaf(p, v4.w, acc.w);
+    // four independent accumulators keep four rows of V in flight per thread
+    float4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto axpy = [](float4& a, float p, const float4& v) {
+        a.x = fmaf(p, v.x, a.x);
+        a.y = fmaf(p, v.y, a.y);
+        a.z = fmaf(p, v.z, a.z);
+        a.w = fmaf(p, v.w, a.w);
+    };
+    const float* vcol = vc + crow * D + 4 * g;
+    int t = sl;
+    for (; t + 3 * SL < nmem; t += 4 * SL) {
+        float4 v4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v4[j] = *(const float4*)(vcol + (int64_t)(t + j * SL) * D);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) axpy(acc[j], sc[t + j * SL] * inv, v4[j]);
     }
-    part[sl][g] = acc;
+    for (; t < nmem; t += SL) axpy(acc[0], sc[t] * inv, *(const float4*)(vcol + (int64_t)t * D));
+    if (ROPE && sl == (pos % SL)) axpy(acc[1], sc[pos] * inv, *(const float4*)(vs + 4 * g));
+    acc[0].x += acc[1].x; acc[0].y += acc[1].y; acc[0].z += acc[1].z; acc[0].w += acc[1].w;
+    acc[2].x += acc[3].x; acc[2].y += acc[3].y; acc[2].z += acc[3].z; acc[2].w += acc[3].w;
+    acc[0].x += acc[2].x; acc[0].y += acc[2].y; acc[0].z += acc[2].z; acc[0].w += acc[2].w;
+    part[sl][g] = acc[0];
     __syncthreads();
     if (tid < G) {
         float4 r = part[0][tid];
@@ -323,36 +351,46 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
 }
 
 // ---- SwiGLU fused with the per-token int8 quantisation ----------------------
-// One workgroup per token: a = silu(g) * u kept in registers, then
-// quantize_per_token (src/int8_quant.cpp:8-31): max|a| (floor 1e-10),
-// scale = 127/max, q = (int8)round_half_away(a * scale), inv = max/127.
-// Writes q [B][n] and inv [B]; n <= kT * kSQ.
-constexpr int kSQ = 48;
-__global__ __launch_bounds__(kT) void silu_mul_quant_k(const float* __restrict__ g, const float* __restrict__ u,
-                                                       int8_t* __restrict__ q, float* __restrict__ inv_scale, int n,
-                                                       int64_t gstride, int64_t ustride) {
-    __shared__ float redf[4];
-    const int r = blockIdx.x;
+// One workgroup of 1024 threads per token: a = silu(g) * u kept in registers
+// (kSQ per thread, all loads issued before any use), then quantize_per_token
+// (src/int8_quant.cpp:8-31): max|a| (floor 1e-10), scale = 127/max,
+// q = (int8)round_half_away(a * scale), inv = max/127.  n <= kSQT * kSQ.
+constexpr int kSQT = 1024, kSQ = 12;
+__global__ __launch_bounds__(kSQT) void silu_mul_quant_k(const float* __restrict__ g, const float* __restrict__ u,
+                                                         int8_t* __restrict__ q, float* __restrict__ inv_scale, int n,
+                                                         int64_t gstride, int64_t ustride) {
+    __shared__ float red[kSQT / 64];
+    const int r = blockIdx.x, tid = threadIdx.x;
     const float* gr = g + r * gstride;
     const float* ur = u + r * ustride;
-    float a[kSQ];
+    float gv[kSQ], uv[kSQ];
+#pragma unroll
+    for (int j = 0; j < kSQ; ++j) {
+        const int i = tid + j * kSQT;
+        gv[j] = i < n ? gr[i] : 0.0f;
+        uv[j] = i < n ? ur[i] : 0.0f;
+    }
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < kSQ; ++j) {
-        const int i = threadIdx.x + j * kT;
-        a[j] = i < n ? silu1(gr[i]) * ur[i] : 0.0f;
-        m = fmaxf(m, fabsf(a[j]));
+        gv[j] = silu1(gv[j]) * uv[j];
+        m = fmaxf(m, fabsf(gv[j]));
     }
-    m = block_max(m, redf);
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kSQT / 64; ++w) m = fmaxf(m, red[w]);
     if (m < 1e-10f) m = 1e-10f;
     const float sc = __fdiv_rn(127.0f, m);
     int8_t* qr = q + (int64_t)r * n;
 #pragma unroll
     for (int j = 0; j < kSQ; ++j) {
-        const int i = threadIdx.x + j * kT;
-        if (i < n) qr[i] = (int8_t)quant_i8(a[j], sc);
+        const int i = tid + j * kSQT;
+        if (i < n) qr[i] = (int8_t)quant_i8(gv[j], sc);
     }
-    if (threadIdx.x == 0) inv_scale[r] = __fdiv_rn(m, 127.0f);
+    if (tid == 0) inv_scale[r] = __fdiv_rn(m, 127.0f);
 }
 
 // ---- greedy argmax + token bookkeeping ---------------------------------------
@@ -456,7 +494,7 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 hipError_t launch_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim,
                            float eps, hipStream_t s) {
     if (dim % 4 == 0 && dim < (1ll << 31) && al16(x) && al16(y) && al16(gamma) && (!t || al16(t)))
-        rms_norm_k<<<(unsigned)rows, kT, 0, s>>>(x, t, gamma, y, (int)dim, eps);
+        rms_norm_k<<<(unsigned)rows, kRN, 0, s>>>(x, t, gamma, y, (int)dim, eps);
     else
         rms_norm_any_k<<<(unsigned)rows, kT, 0, s>>>(x, t, gamma, y, dim, eps);
     return hipGetLastError();
@@ -532,11 +570,11 @@ hipError_t launch_rope_attention(const float* q, const float* k, const float* v,
                                max_seq, s);
 }
 
-bool silu_mul_quant_supported(int64_t n) { return n > 0 && n <= (int64_t)kT * kSQ; }
+bool silu_mul_quant_supported(int64_t n) { return n > 0 && n <= (int64_t)kSQT * kSQ; }
 
 hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows,
                                  int64_t n, int64_t gstride, int64_t ustride, hipStream_t s) {
-    silu_mul_quant_k<<<(unsigned)rows, kT, 0, s>>>(g, u, q, inv_scale, (int)n, gstride, ustride);
+    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, q, inv_scale, (int)n, gstride, ustride);
     return hipGetLastError();
 }
 
