@@ -118,6 +118,15 @@ int mth_oil8_gemv(const uint8_t* indices, const float* codebook, const float* x,
     REQUIRE(indices && codebook && x && y, "mth_oil8_gemv: null pointer");
     REQUIRE(M > 0 && K > 0 && batch > 0 && M < kMaxDim && K < kMaxDim && batch <= 65536,
             "mth_oil8_gemv: bad sizes M=%lld K=%lld batch=%lld", (long long)M, (long long)K, (long long)batch);
+    const bool aligned = (((uintptr_t)indices | (uintptr_t)x) & 15u) == 0;
+    if (aligned && mth::oil8_bt_supported(M, K, batch)) {
+        void* partial = nullptr;
+        const hipError_t e = workspace(S(stream), mth::oil8_bt_partial_bytes(M, K), &partial);
+        if (e != hipSuccess)
+            return fail(MTH_EDEVICE, "mth_oil8_gemv: workspace allocation failed: %s", hipGetErrorString(e));
+        return check_launch(mth::launch_oil8_gemv_bt(indices, codebook, x, y, M, K, batch, (float*)partial, S(stream)),
+                            "mth_oil8_gemv");
+    }
     return check_launch(mth::launch_oil8_gemv(indices, codebook, x, y, M, K, batch, S(stream)), "mth_oil8_gemv");
 }
 

@@ -14,6 +14,7 @@
 // holds no memset nodes and no allocations.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -68,6 +69,15 @@ hipError_t oil4(const mth_decoder* d, const uint8_t* w, const uint16_t* cb, cons
     return mth::launch_oil4_gemv(w, cb, d->c.cb_block, x, y, M, K, d->batch, s);
 }
 
+// y[B][M] = W x for an OIL8 weight: MFMA kernel for batches of 2 and more.
+hipError_t oil8(const mth_decoder* d, const uint8_t* w, const float* cb, const float* x, float* y, int64_t M,
+                int64_t K, hipStream_t s) {
+    const bool aligned = (((uintptr_t)w | (uintptr_t)x) & 15u) == 0;
+    if (aligned && mth::oil8_bt_supported(M, K, d->batch))
+        return mth::launch_oil8_gemv_bt(w, cb, x, y, M, K, d->batch, d->bt_partial, s);
+    return mth::launch_oil8_gemv(w, cb, x, y, M, K, d->batch, s);
+}
+
 hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     const mth_decoder_config& c = d->c;
     const int64_t B = d->batch, H = c.hidden, F = c.ffn, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
@@ -83,12 +93,12 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         float* vc = d->vc + l * d->layer_kv;
         // residual of the previous layer's FFN folded into this norm
         TRY(mth::launch_rms_norm(d->x, l == 0 ? nullptr : d->t, L.attn_norm, d->h, B, H, c.eps, s));
-        TRY(mth::launch_oil8_gemv(L.wq, L.cbq, d->h, d->q, QD, H, B, s));
-        TRY(mth::launch_oil8_gemv(L.wk, L.cbk, d->h, d->k, KD, H, B, s));
-        TRY(mth::launch_oil8_gemv(L.wv, L.cbv, d->h, d->v, KD, H, B, s));
+        TRY(oil8(d, L.wq, L.cbq, d->h, d->q, QD, H, s));
+        TRY(oil8(d, L.wk, L.cbk, d->h, d->k, KD, H, s));
+        TRY(oil8(d, L.wv, L.cbv, d->h, d->v, KD, H, s));
         TRY(mth::launch_rope_attention(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, d->att, d->step, B,
                                        (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
-        TRY(mth::launch_oil8_gemv(L.wo, L.cbo, d->att, d->t, H, QD, B, s));
+        TRY(oil8(d, L.wo, L.cbo, d->att, d->t, H, QD, s));
         TRY(mth::launch_rms_norm(d->x, d->t, L.ffn_norm, d->h, B, H, c.eps, s));
         const int64_t nb = c.cb_block ? H / c.cb_block : 1;
         const bool fused = L.wup == L.wgate + F * (H / 2) && (c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
@@ -106,7 +116,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, B, s));
     }
     TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
-    TRY(mth::launch_oil8_gemv(d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, B, s));
+    TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
     TRY(mth::launch_argmax(d->logits, B, c.vocab, d->ids, d->hist, d->step, (int)d->hist_stride, (int)d->prompt_len,
                            d->arg_v, d->arg_i, s));
 #undef TRY
@@ -149,7 +159,10 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     const int64_t QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
     d->hist_stride = c.max_seq + 1;
     d->layer_kv = B * KD * c.max_seq;
-    const size_t partial = mth::oil4_bt_partial_bytes(2 * F, H);
+    // workspace of the batched GEMVs: the largest of every projection's need
+    const size_t partial = std::max({mth::oil4_bt_partial_bytes(2 * F, H), mth::oil8_bt_partial_bytes(QD, H),
+                                     mth::oil8_bt_partial_bytes(KD, H), mth::oil8_bt_partial_bytes(H, QD),
+                                     mth::oil8_bt_partial_bytes(c.vocab, H)});
     struct Slot {
         void** p;
         size_t bytes;

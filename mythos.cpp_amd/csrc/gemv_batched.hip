@@ -1,4 +1,5 @@
-// gemv_batched.hip — OIL4 GEMV for decode batches of 2..16 tokens on gfx950.
+// gemv_batched.hip — OIL4 and OIL8 GEMVs for decode batches of 2..16 tokens
+// on gfx950 (the OIL8 kernel is described at its definition).
 //
 //   y[t][m] = sum_k cb[m][k/128][nib(m, k)] * x[t][k]   (t < batch <= 16)
 //
@@ -173,6 +174,87 @@ __global__ __launch_bounds__(256) void oil4_bt_reduce(const float* __restrict__ 
 
 inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+// ===================================================================
+// OIL8, batch 2..16, on FP32 MFMA (v_mfma_f32_16x16x4_f32)
+// ===================================================================
+//   y[t][m] = sum_k cb[idx[m][k]] * x[t][k]
+// Workgroup = 4 waves x 16 rows and one K slice of ks columns (a multiple of
+// 64); grid = (ceil(M / 64), K / ks).  Per 64-column chunk, lane l (row
+// r = l % 16, k group g = l / 16) loads the 16 index bytes of its row at
+// chunk columns 16g .. 16g + 15 (one 128-bit load), gathers their FP32
+// codebook values from LDS and feeds them to 16 MFMAs: in MFMA j the lane's
+// A element is W[r][16g + j] and its B element x[t = r][16g + j], i.e. the k
+// order inside the chunk is permuted alike on both operands.  Products and
+// sums are FP32.  The chunk's x for 16 tokens ([16][64] floats, rows padded
+// to 68 floats against bank conflicts) is staged in LDS once per workgroup
+// (double buffered) and read by all four waves.  Slices are added by
+// oil4_bt_reduce (same [slice][16][M] partial layout).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kO8Pad = 68;
+
+__global__ __launch_bounds__(256) void oil8_gemv_bt(const uint8_t* idx, const float* __restrict__ cb, const float* x,
+                                                    float* __restrict__ y, float* __restrict__ partial, int M, int K,
+                                                    int batch, int ks) {
+    __shared__ float tab[256];
+    __shared__ __align__(16) float xs[2][kBtTok * kO8Pad];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.x * kBtRows + wave * 16;
+    const int k0 = blockIdx.y * ks;
+    const int nch = ks / 64;
+    const uint8_t* wrow = idx + (int64_t)min(m0 + r, M - 1) * K + k0 + 16 * g;  // clamped rows
+    const int xt = tid >> 4, xc = (tid & 15) * 4;  // staging: token xt, 4 columns at xc
+    const bool xv = xt < batch;
+    const float* xrow = x + (int64_t)(xv ? xt : 0) * K + k0 + xc;
+    float4 xn = xv ? ldf4(xrow) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    tab[tid] = cb[tid];
+    uint4 wn = ld_stream(wrow);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < nch; ++c) {
+        float* xb = xs[c & 1];
+        *(float4*)(xb + xt * kO8Pad + xc) = xn;
+        __syncthreads();  // the buffer written two chunks ago has been read by all
+        const uint4 w = wn;
+        if (c + 1 < nch) {
+            wn = ld_stream(wrow + (c + 1) * 64);
+            if (xv) xn = ldf4(xrow + (c + 1) * 64);
+        }
+        const float* xp = xb + r * kO8Pad + 16 * g;
+        float4 xb4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xb4[q] = *(const float4*)(xp + 4 * q);
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float xq[4] = {xb4[q].x, xb4[q].y, xb4[q].z, xb4[q].w};
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(tab[(wd[q] >> (8 * b)) & 0xffu], xq[b], acc, 0, 0, 0);
+        }
+    }
+    // D: lane l holds rows 4g + i, token r
+    const int t = r;
+    if (t >= batch) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * g + i;
+        if (m >= M) continue;
+        if (gridDim.y == 1)
+            y[(int64_t)t * M + m] = acc[i];
+        else
+            partial[((int64_t)blockIdx.y * kBtTok + t) * M + m] = acc[i];
+    }
+}
+
+// K slices for the OIL8 batched GEMV: enough workgroups to cover the CUs,
+// at most 16, each a multiple of 64 columns.
+inline int o8_slices(int64_t M, int64_t K) {
+    const int64_t groups = (M + kBtRows - 1) / kBtRows;
+    int S = 1;
+    while (S < 16 && groups * S < 256 && K % (64 * S * 2) == 0) S *= 2;
+    return S;
+}
+
 // phases of 256 columns per K slice: 4 (K a multiple of 1024, K >= 2048) or 2
 inline int bt_nph(int64_t K) { return (K >= 2048 && K % 1024 == 0) ? 4 : 2; }
 
@@ -197,6 +279,31 @@ bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch) {
 size_t oil4_bt_partial_bytes(int64_t M, int64_t K) {
     const int64_t S = K / (256 * bt_nph(K));
     return S > 1 ? (size_t)(S * kBtTok * M * 4) : 0;
+}
+
+bool oil8_bt_supported(int64_t M, int64_t K, int64_t batch) {
+    return batch >= 2 && K >= 64 && K % 64 == 0 && M < (1ll << 31) && M * K < (1ll << 40);
+}
+
+size_t oil8_bt_partial_bytes(int64_t M, int64_t K) {
+    const int S = o8_slices(M, K);
+    return S > 1 ? (size_t)(S * kBtTok * M * 4) : 0;
+}
+
+hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
+                               int64_t batch, float* partial, hipStream_t s) {
+    const int S = o8_slices(M, K);
+    const dim3 grid(ceil_div_i(M, kBtRows), (unsigned)S);
+    for (int64_t t0 = 0; t0 < batch; t0 += kBtTok) {
+        const int b = (int)(batch - t0 < kBtTok ? batch - t0 : kBtTok);
+        oil8_gemv_bt<<<grid, 256, 0, s>>>(idx, cb, x + t0 * K, y + t0 * M, partial, (int)M, (int)K, b,
+                                          (int)(K / S));
+        if (S > 1)
+            oil4_bt_reduce<<<ceil_div_i((int64_t)b * M, 256), 256, 0, s>>>(partial, y + t0 * M, (int)M, b, S);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y,

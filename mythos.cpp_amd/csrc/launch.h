@@ -36,6 +36,12 @@ bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch);
 size_t oil4_bt_partial_bytes(int64_t M, int64_t K);
 hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y,
                                int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
+// OIL8 for batches of 2 and more (gemv_batched.hip, FP32 MFMA); same
+// workspace contract as the OIL4 batched kernel.
+bool oil8_bt_supported(int64_t M, int64_t K, int64_t batch);
+size_t oil8_bt_partial_bytes(int64_t M, int64_t K);
+hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
+                               int64_t batch, float* partial, hipStream_t s);
 // Reference per-(m,n) indexing with one codebook (src/kernel_oil4.cpp:41-52).
 hipError_t launch_oil4_gemm_mn(const uint8_t* nib, const uint16_t* cb, const float* act, float* out,
                                int64_t M, int64_t N, int64_t K, hipStream_t s);

@@ -37,6 +37,10 @@ def empty(n, dtype, dev):
     (4096, 4096, 16),    # decode batch 16
     (33, 1000, 2),       # K % 16 != 0 -> generic kernel
     (5, 4112, 1),        # K > 4096 -> generic kernel
+    (32000, 4096, 16),   # lm_head of the decoder, one K slice
+    (100, 512, 5),       # batched MFMA kernel, rows not a multiple of 64
+    (4096, 4096, 2),
+    (70, 4160, 17),      # two groups of tokens
 ])
 def test_oil8_gemv(M, K, batch, oracle, mth, dev):
     import torch
