@@ -208,6 +208,16 @@ int mth_i2s_gemv(const uint8_t* packed, float w_scale, const int8_t* act, const 
     REQUIRE(M > 0 && K > 0 && batch > 0 && M < kMaxDim && K < (1ll << 24) && batch <= 65536,
             "mth_i2s_gemv: bad sizes M=%lld K=%lld batch=%lld", (long long)M, (long long)K, (long long)batch);
     REQUIRE(K % 4 == 0, "mth_i2s_gemv: K=%lld must be a multiple of 4", (long long)K);
+    const bool aligned = (((uintptr_t)packed | (uintptr_t)act) & 15u) == 0;
+    if (aligned && mth::i2s_bt_supported(M, K, batch)) {
+        void* partial = nullptr;
+        const hipError_t e = workspace(S(stream), mth::i2s_bt_partial_bytes(M, K), &partial);
+        if (e != hipSuccess)
+            return fail(MTH_EDEVICE, "mth_i2s_gemv: workspace allocation failed: %s", hipGetErrorString(e));
+        return check_launch(mth::launch_i2s_gemv_bt(packed, w_scale, act, act_scale, y, M, K, batch, (float*)partial,
+                                                    S(stream)),
+                            "mth_i2s_gemv");
+    }
     return check_launch(mth::launch_i2s_gemv(packed, w_scale, nullptr, act, act_scale, y, M, K, batch, S(stream)),
                         "mth_i2s_gemv");
 }

@@ -113,7 +113,10 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
             TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, B, F, F, F, s));
         }
-        TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, B, s));
+        if ((((uintptr_t)L.wdown | (uintptr_t)d->aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, B))
+            TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->aq, d->a_inv, d->t, H, F, B, d->bt_partial, s));
+        else
+            TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, B, s));
     }
     TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
     TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
@@ -162,7 +165,7 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     // workspace of the batched GEMVs: the largest of every projection's need
     const size_t partial = std::max({mth::oil4_bt_partial_bytes(2 * F, H), mth::oil8_bt_partial_bytes(QD, H),
                                      mth::oil8_bt_partial_bytes(KD, H), mth::oil8_bt_partial_bytes(H, QD),
-                                     mth::oil8_bt_partial_bytes(c.vocab, H)});
+                                     mth::oil8_bt_partial_bytes(c.vocab, H), mth::i2s_bt_partial_bytes(H, F)});
     struct Slot {
         void** p;
         size_t bytes;

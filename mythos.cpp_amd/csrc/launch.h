@@ -57,6 +57,12 @@ hipError_t launch_tl_precompute_lut(const int8_t* act, int8_t* lut, int64_t K, i
 hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x,
                            const int8_t* act, const float* act_scale, float* y,
                            int64_t M, int64_t K, int64_t batch, hipStream_t s);
+// Unfused (int8 activations) batches of 2..16 per launch group on int8 MFMA;
+// workspace contract as the batched OIL4/OIL8 kernels.
+bool i2s_bt_supported(int64_t M, int64_t K, int64_t batch);
+size_t i2s_bt_partial_bytes(int64_t M, int64_t K);
+hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale, float* y,
+                              int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o,

@@ -363,6 +363,115 @@ __global__ __launch_bounds__(kWG) void tl_lut_k(const int8_t* __restrict__ act, 
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ---------------------------------------------------------------------------
+// I2_S GEMV for batches of 2..16 on int8 MFMA (v_mfma_i32_16x16x64_i8).
+// ---------------------------------------------------------------------------
+// y[t][m] = ((float)sum_k t(m,k) * q[t][k] * w_scale) * act_scale[t], the
+// sum exact in int32, as src/kernel_i2s.cpp:32-40 per row and token.
+// Workgroup = 4 waves x 16 rows and a K slice of whole 256-column
+// super-chunks; grid = (ceil(M / 64), S).  Per super-chunk, lane l (row
+// r = l % 16, group g = l / 16) loads the 16 code bytes of its row at
+// columns 64g .. 64g + 63 and feeds 4 MFMAs; in MFMA j its A operand is the
+// u-codes (t + 1, code 3 read as 2) of columns 64g + 16j .. +15 in the byte
+// order (col 4i + s at byte i of dword s), and its B operand the activations
+// of token r at the same columns in the same order (transposed once per
+// workgroup while staging into LDS).  So D = sum (t + 1) q, and the kernel
+// subtracts sum q (accumulated while staging) to get sum t q.  With S > 1
+// every slice writes its exact integer partial (|sum| < 2^24, exact in
+// FP32) and i2s_bt_reduce adds them in order and applies the epilogue.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr int kIbRows = 64, kIbTok = 16;
+
+__device__ __forceinline__ uint32_t byte_t4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, int s) {
+    // byte i of the result = byte s of the i-th input
+    return ((a >> (8 * s)) & 0xffu) | (((b >> (8 * s)) & 0xffu) << 8) | (((c >> (8 * s)) & 0xffu) << 16) |
+           (((d >> (8 * s)) & 0xffu) << 24);
+}
+
+__global__ __launch_bounds__(kWG) void i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act,
+                                                   const float* __restrict__ act_scale, float* __restrict__ y,
+                                                   float* __restrict__ partial, int M, int K, int batch) {
+    __shared__ __align__(16) uint32_t qs[2][kIbTok * 16 * 4];  // [token][16-col group][4 dwords]
+    __shared__ int asum_p[kIbTok][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.x * kIbRows + wave * 16;
+    const int nsc = K / 256, S = gridDim.y;
+    const int sc0 = (int)((int64_t)blockIdx.y * nsc / S), sc1 = (int)((int64_t)(blockIdx.y + 1) * nsc / S);
+    const int bpr = K / 4;
+    const uint8_t* wrow = packed + (int64_t)min(m0 + r, M - 1) * bpr + 16 * g;  // clamped rows
+    // staging: thread = (token st, 16-column group sg)
+    const int st = tid >> 4, sg = tid & 15;
+    const bool sv = st < batch;
+    const int8_t* arow = act + (int64_t)(sv ? st : 0) * K + 16 * sg;
+    uint4 an = sv ? ld16(arow + sc0 * 256) : make_uint4(0, 0, 0, 0);
+    uint4 wn = ld_stream(wrow + sc0 * 64);
+    int asum = 0;
+    i32x4 acc = {0, 0, 0, 0};
+    for (int c = sc0; c < sc1; ++c) {
+        uint32_t* qb = qs[c & 1];
+        {
+            const uint32_t a4[4] = {an.x, an.y, an.z, an.w};  // columns 16sg + 4i + s at byte s of a4[i]
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) qb[(st * 16 + sg) * 4 + s2] = byte_t4x4(a4[0], a4[1], a4[2], a4[3], s2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asum = dot4(a4[i], 0x01010101u, asum);
+        }
+        __syncthreads();
+        const uint4 w = wn;
+        if (c + 1 < sc1) {
+            wn = ld_stream(wrow + (c + 1) * 64);
+            if (sv) an = ld16(arow + (c + 1) * 256);
+        }
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t u = ucode(wd[j]);
+            const i32x4 a = {(int)(u & 0x03030303u), (int)((u >> 2) & 0x03030303u), (int)((u >> 4) & 0x03030303u),
+                             (int)((u >> 6) & 0x03030303u)};
+            const i32x4 b = *(const i32x4*)(qb + (r * 16 + 4 * g + j) * 4);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+        }
+    }
+    asum_p[st][sg] = asum;
+    __syncthreads();
+    // D: lane l holds rows 4g + i for token r
+    const int t = r;
+    if (t >= batch) return;
+    int as = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) as += asum_p[t][j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * g + i;
+        if (m >= M) continue;
+        const int v = acc[i] - as;
+        if (S == 1)
+            y[(int64_t)t * M + m] = __fmul_rn(__fmul_rn((float)v, w_scale), act_scale[t]);
+        else
+            partial[((int64_t)blockIdx.y * kIbTok + t) * M + m] = (float)v;
+    }
+}
+
+__global__ __launch_bounds__(kWG) void i2s_bt_reduce(const float* __restrict__ partial, float w_scale,
+                                                     const float* __restrict__ act_scale, float* __restrict__ y, int M,
+                                                     int batch, int nslice) {
+    const int64_t i = (int64_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= (int64_t)batch * M) return;
+    const int64_t t = i / M, m = i - t * M;
+    const float* p = partial + t * M + m;
+    float s = 0.0f;  // integers below 2^24: exact in any order
+    for (int z = 0; z < nslice; ++z) s += p[(int64_t)z * kIbTok * M];
+    y[i] = __fmul_rn(__fmul_rn(s, w_scale), act_scale[t]);
+}
+
+inline int ib_slices(int64_t M, int64_t K) {
+    const int64_t groups = (M + kIbRows - 1) / kIbRows, nsc = K / 256;
+    int S = 1;
+    while (S < 16 && groups * S < 256 && 2 * S <= nsc) S *= 2;
+    return S;
+}
+
 template <int LPR, int NSEG>
 hipError_t run_i2s_fast(const uint8_t* packed, float w_scale, const float* x, const int8_t* act,
                         const float* act_scale, float* y, int64_t M, int64_t K, int64_t batch, hipStream_t s) {
@@ -418,6 +527,32 @@ hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x,
     else
         i2s_gemv_generic<false><<<ceil_div(M, kWaves), kWG, 0, s>>>(packed, w_scale, x, act, act_scale, y, M, K, batch);
     return hipGetLastError();
+}
+
+bool i2s_bt_supported(int64_t M, int64_t K, int64_t batch) {
+    return batch >= 2 && K >= 256 && K % 256 == 0 && K < (1 << 24) / 128 && M < (1ll << 31);
+}
+
+size_t i2s_bt_partial_bytes(int64_t M, int64_t K) {
+    const int S = ib_slices(M, K);
+    return S > 1 ? (size_t)(S * kIbTok * M * 4) : 0;
+}
+
+hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale, float* y,
+                              int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s) {
+    const int S = ib_slices(M, K);
+    const dim3 grid(ceil_div(M, kIbRows), (unsigned)S);
+    for (int64_t t0 = 0; t0 < batch; t0 += kIbTok) {
+        const int b = (int)(batch - t0 < kIbTok ? batch - t0 : kIbTok);
+        i2s_gemv_bt<<<grid, kWG, 0, s>>>(packed, w_scale, act + t0 * K, act_scale + t0, y + t0 * M, partial, (int)M,
+                                         (int)K, b);
+        if (S > 1)
+            i2s_bt_reduce<<<ceil_div((int64_t)b * M, kWG), kWG, 0, s>>>(partial, w_scale, act_scale + t0, y + t0 * M,
+                                                                        (int)M, b, S);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o, int64_t M, int64_t N, int64_t K,

@@ -240,3 +240,27 @@ def test_i2s_code3_and_unfused_bit_exact(oracle, mth, dev):
     mth.i2s_gemv_f32(to_dev(packed, dev), 0.75, to_dev(x, dev), y2, M, K, batch)
     torch.cuda.synchronize()
     assert np.array_equal(y2.cpu().numpy().reshape(batch, M), ref)
+
+
+@pytest.mark.parametrize("M,K,batch", [
+    (4096, 11008, 16),   # decoder down projection, batch 16 (int8 MFMA kernel, 4 K slices)
+    (4096, 11008, 2),
+    (100, 512, 5),       # rows not a multiple of 64, 2 slices
+    (64, 256, 17),       # one super-chunk, two groups of tokens
+    (33, 1000, 3),       # K % 256 != 0 -> per-token kernel
+])
+def test_i2s_gemv_batched_bit_exact(M, K, batch, oracle, mth, dev):
+    """int8 activations + act_scale (the unfused entry point, as the decoder
+    calls it) for batches: bit-exact against quantize_per_token + i2s_gemv."""
+    import torch
+    print(f"i2s_gemv batched M={M} K={K} batch={batch}", flush=True)
+    g = np.random.default_rng(M + K + batch)
+    packed = g.integers(0, 256, (M, K // 4), dtype=np.uint8)  # all four codes
+    x = g.normal(0, 1, (batch, K)).astype(np.float32)
+    x[batch // 2] *= 1e-3
+    q, _, inv = oracle.quantize_per_token(x, batch, K)
+    y = empty(batch * M, torch.float32, dev)
+    mth.i2s_gemv(to_dev(packed, dev), 0.0159577, to_dev(q, dev), to_dev(inv, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    ref = oracle.i2s_gemv_f32(packed.ravel(), 0.0159577, x, M, K, batch, threads=8)
+    assert np.array_equal(y.cpu().numpy().reshape(batch, M), ref)
