@@ -2,7 +2,8 @@
  * mythos_decoder.h — the mixed-format decoder stack on one MI355X
  * (libmythos_oil.so): Q/K/V/O and lm_head OIL8, FFN gate/up OIL4 with
  * per-block codebooks, FFN down ternary I2_S with per-token int8 activations,
- * RMSNorm, rotary embedding, attention over an FP32 KV cache, greedy argmax.
+ * RMSNorm, rotary embedding, attention over an FP32 or bf16 KV cache, greedy
+ * argmax.
  *
  * Replaces, for this weight format mix, the reference's inference path
  * DenseModel::forward (src/model.cpp:45-75) -> TransformerBlock::forward
@@ -45,6 +46,10 @@ typedef struct {
     int64_t cb_block;  /* OIL4 codebook block length (0 = one codebook per tensor) */
     int64_t max_batch; /* sequences decoded together, 1..16 */
     float eps, theta;  /* RMSNorm epsilon, RoPE base */
+    /* KV-cache element type: 0 = FP32 (KVCache's Tensor, src/kv_cache.cpp:61-62),
+     * 1 = bf16: K (after RoPE) and V rounded to nearest even when appended,
+     * attention reads them back exactly; half the cache bytes. */
+    int64_t kv_dtype;
 } mth_decoder_config;
 
 typedef struct {
@@ -91,6 +96,28 @@ int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_str
 
 /* Steps run since the last start (host-side count). */
 int64_t mth_decoder_steps_done(const mth_decoder* d);
+
+/* Per-layer intermediate values, for parity tests and debugging (no
+ * reference counterpart).  With taps non-null, every later step runs its
+ * launches directly (no graph) and copies, for layer l, into
+ * taps + l * mth_decoder_tap_floats(d), in this order, B = the started batch:
+ *   x_attn [B][hidden]  residual stream after the attention half
+ *   gu     [B][2*ffn]   gate outputs then up outputs, per token
+ *   act    [B][ffn]     silu(gate) * up in FP32, before quantisation
+ *   aq     [B][ffn]     its int8 quantisation (bytes: B*ffn/4 floats of storage)
+ *   a_inv  [B]          per-token inverse scale of aq
+ *   down   [B][hidden]  the ternary down projection (added to x_attn next)
+ * taps: device memory of layers * mth_decoder_tap_floats(d) floats; null
+ * turns the taps off.  Valid after mth_decoder_start (the batch sets the size). */
+int mth_decoder_set_taps(mth_decoder* d, float* taps);
+int64_t mth_decoder_tap_floats(const mth_decoder* d);
+
+/* Host copy (synchronous) of layer `layer`'s K and V caches, each
+ * [batch][kv_heads][max_seq][head_dim] of the cache's element type (FP32, or
+ * bf16 bits as uint16 with kv_dtype 1) for the started batch; either pointer
+ * may be null.  Positions not yet written hold zeros or older values.  For
+ * parity tests and debugging (no reference counterpart). */
+int mth_decoder_read_kv(const mth_decoder* d, int64_t layer, void* k, void* v, mth_stream_t stream);
 
 #ifdef __cplusplus
 }

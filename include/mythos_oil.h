@@ -6,7 +6,21 @@
  * hipMalloc or any HIP allocator), plain sizes and a HIP stream (hipStream_t
  * passed as void*; NULL = the default stream).  Calls are stream-ordered and
  * asynchronous: they validate, launch and return.  Outputs are overwritten,
- * never accumulated, and no entry point allocates memory.
+ * never accumulated.
+ *
+ * Workspace.  The batched GEMVs (mth_oil8_gemv, mth_oil4_gemv, mth_i2s_gemv
+ * with batch >= 2) and mth_argmax keep partial results in a device workspace
+ * the library owns, one per (device, stream).  The first call that needs more
+ * than the stream's workspace holds allocates a larger one (hipMalloc, at
+ * least double the old size) and retires the old block WITHOUT freeing it, so
+ * work queued earlier and HIP graphs captured earlier from that stream keep
+ * valid addresses until the process ends.  No other entry point allocates.
+ * Inside a stream capture a call never allocates: if the workspace is too
+ * small it fails with MTH_EUNSUPPORTED, so reserve the size beforehand with
+ * mth_workspace_reserve (or make one uncaptured call of the largest shape).
+ * Calls on one stream share its workspace; a captured graph uses the
+ * workspace of the stream it was captured on and must not be replayed
+ * concurrently with other work that uses that stream's workspace.
  *
  * Return value: MTH_OK (0) or a negative MTH_E* code; the thread-local message
  * of the last failure is returned by mth_last_error().  Validation covers
@@ -41,6 +55,12 @@ enum {
 const char* mth_last_error(void);
 /* ABI version: (major << 16) | minor. */
 int mth_version(void);
+
+/* Ensures the calling thread's current device holds at least `bytes` of
+ * workspace for `stream` (see "Workspace" above); call it before capturing
+ * batched GEMVs into a graph.  No reference counterpart: the reference's CPU
+ * kernels keep no device state. */
+int mth_workspace_reserve(int64_t bytes, mth_stream_t stream);
 
 /* ---------------------------------------------------------------- OIL8 -- */
 

@@ -10,9 +10,11 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "launch.h"
 #include "../../include/mythos_oil.h"
@@ -45,16 +47,27 @@ inline hipStream_t S(mth_stream_t s) { return (hipStream_t)s; }
 // generic kernels index with int64.  Reject sizes whose byte counts overflow.
 constexpr int64_t kMaxDim = (int64_t)1 << 40;
 
-// Device scratch (partial sums of the batched OIL4 GEMV's K slices, argmax
+// Device scratch (partial sums of the batched GEMVs' K slices, argmax
 // partials), one per (device, stream): calls on one stream are ordered and
-// may share it; another stream gets its own.  Grown on demand, never shrunk.
+// may share it; another stream gets its own.
+//
+// Growth allocates a new block (at least twice the old size) and RETIRES the
+// old one without freeing it: launches already queued, and any HIP graph
+// captured earlier from calls on that stream, keep using the old address, so
+// it stays valid until the process ends.  Doubling bounds the retired memory
+// by the final block's size.  Growth never happens inside a stream capture
+// (hipMalloc is not capturable): such a call fails with MTH_EUNSUPPORTED and
+// the caller reserves the size first (mth_workspace_reserve) or makes one
+// uncaptured call of that shape.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::vector<void*> g_ws_retired;  // superseded blocks: valid until the process ends
 
+// hipSuccess, or hipErrorStreamCaptureUnsupported when growing under capture
 hipError_t workspace(hipStream_t s, size_t need, void** out) {
     *out = nullptr;
     if (need == 0) return hipSuccess;
@@ -64,22 +77,29 @@ hipError_t workspace(hipStream_t s, size_t need, void** out) {
     std::lock_guard<std::mutex> g(g_ws_mu);
     Workspace& w = g_ws[{dev, s}];
     if (w.bytes < need) {
-        void* p = nullptr;
-        e = hipMalloc(&p, need);
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(s, &st);
         if (e != hipSuccess) return e;
-        if (w.base) {
-            (void)hipStreamSynchronize(s);  // earlier launches on s may still use it
-            (void)hipFree(w.base);
-        }
+        if (st != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+        const size_t bytes = std::max(need, 2 * w.bytes);
+        void* p = nullptr;
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return e;
+        if (w.base) g_ws_retired.push_back(w.base);
         w.base = p;
-        w.bytes = need;
+        w.bytes = bytes;
     }
     *out = w.base;
     return hipSuccess;
 }
 
-hipError_t bt_workspace(hipStream_t s, int64_t M, int64_t K, float** partial) {
-    return workspace(s, mth::oil4_bt_partial_bytes(M, K), (void**)partial);
+int workspace_fail(const char* what, hipError_t e, size_t need) {
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(MTH_EUNSUPPORTED,
+                    "%s: needs %zu bytes of workspace on this stream, more than it holds, and the stream is "
+                    "capturing; call mth_workspace_reserve (or this call uncaptured) before the capture",
+                    what, need);
+    return fail(MTH_EDEVICE, "%s: workspace allocation of %zu bytes failed: %s", what, need, hipGetErrorString(e));
 }
 
 #define REQUIRE(cond, ...) \
@@ -103,7 +123,15 @@ int api_ok() { return ok(); }
 extern "C" {
 
 const char* mth_last_error(void) { return g_err; }
-int mth_version(void) { return (1 << 16) | 0; }
+int mth_version(void) { return (1 << 16) | 1; }
+
+int mth_workspace_reserve(int64_t bytes, mth_stream_t stream) {
+    REQUIRE(bytes >= 0 && bytes < kMaxDim, "mth_workspace_reserve: bad size %lld", (long long)bytes);
+    void* p = nullptr;
+    const hipError_t e = workspace(S(stream), (size_t)bytes, &p);
+    if (e != hipSuccess) return workspace_fail("mth_workspace_reserve", e, (size_t)bytes);
+    return ok();
+}
 
 int mth_oil8_gemm(const uint8_t* indices, const float* codebook, const float* act, float* out,
                   int64_t M, int64_t N, int64_t K, mth_stream_t stream) {
@@ -121,9 +149,9 @@ int mth_oil8_gemv(const uint8_t* indices, const float* codebook, const float* x,
     const bool aligned = (((uintptr_t)indices | (uintptr_t)x) & 15u) == 0;
     if (aligned && mth::oil8_bt_supported(M, K, batch)) {
         void* partial = nullptr;
-        const hipError_t e = workspace(S(stream), mth::oil8_bt_partial_bytes(M, K), &partial);
-        if (e != hipSuccess)
-            return fail(MTH_EDEVICE, "mth_oil8_gemv: workspace allocation failed: %s", hipGetErrorString(e));
+        const size_t need = mth::oil8_bt_partial_bytes(M, K);
+        const hipError_t e = workspace(S(stream), need, &partial);
+        if (e != hipSuccess) return workspace_fail("mth_oil8_gemv", e, need);
         return check_launch(mth::launch_oil8_gemv_bt(indices, codebook, x, y, M, K, batch, (float*)partial, S(stream)),
                             "mth_oil8_gemv");
     }
@@ -149,11 +177,12 @@ int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_b
             (long long)K, (long long)cb_block);
     const bool aligned = (((uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)x) & 15u) == 0;
     if (aligned && mth::oil4_bt_supported(M, K, cb_block, batch)) {
-        float* partial = nullptr;
-        const hipError_t e = bt_workspace(S(stream), M, K, &partial);
-        if (e != hipSuccess)
-            return fail(MTH_EDEVICE, "mth_oil4_gemv: workspace allocation failed: %s", hipGetErrorString(e));
-        return check_launch(mth::launch_oil4_gemv_bt(packed, codebooks, cb_block, x, y, M, K, batch, partial, S(stream)),
+        void* partial = nullptr;
+        const size_t need = mth::oil4_bt_partial_bytes(M, K);
+        const hipError_t e = workspace(S(stream), need, &partial);
+        if (e != hipSuccess) return workspace_fail("mth_oil4_gemv", e, need);
+        return check_launch(mth::launch_oil4_gemv_bt(packed, codebooks, cb_block, x, y, M, K, batch, (float*)partial,
+                                                     S(stream)),
                             "mth_oil4_gemv");
     }
     return check_launch(mth::launch_oil4_gemv(packed, codebooks, cb_block, x, y, M, K, batch, S(stream)),
@@ -211,9 +240,9 @@ int mth_i2s_gemv(const uint8_t* packed, float w_scale, const int8_t* act, const 
     const bool aligned = (((uintptr_t)packed | (uintptr_t)act) & 15u) == 0;
     if (aligned && mth::i2s_bt_supported(M, K, batch)) {
         void* partial = nullptr;
-        const hipError_t e = workspace(S(stream), mth::i2s_bt_partial_bytes(M, K), &partial);
-        if (e != hipSuccess)
-            return fail(MTH_EDEVICE, "mth_i2s_gemv: workspace allocation failed: %s", hipGetErrorString(e));
+        const size_t need = mth::i2s_bt_partial_bytes(M, K);
+        const hipError_t e = workspace(S(stream), need, &partial);
+        if (e != hipSuccess) return workspace_fail("mth_i2s_gemv", e, need);
         return check_launch(mth::launch_i2s_gemv_bt(packed, w_scale, act, act_scale, y, M, K, batch, (float*)partial,
                                                     S(stream)),
                             "mth_i2s_gemv");
@@ -298,7 +327,7 @@ int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_sca
     REQUIRE(g && u && q && inv_scale, "mth_silu_mul_quant: null pointer");
     REQUIRE(rows > 0 && rows <= 65535 && gstride >= n && ustride >= n, "mth_silu_mul_quant: bad sizes");
     REQUIRE(mth::silu_mul_quant_supported(n), "mth_silu_mul_quant: n=%lld outside 1..12288", (long long)n);
-    return check_launch(mth::launch_silu_mul_quant(g, u, q, inv_scale, rows, n, gstride, ustride, S(stream)),
+    return check_launch(mth::launch_silu_mul_quant(g, u, q, inv_scale, nullptr, rows, n, gstride, ustride, S(stream)),
                         "mth_silu_mul_quant");
 }
 
@@ -372,7 +401,7 @@ int mth_argmax(const float* logits, int32_t* ids, int64_t rows, int64_t n, mth_s
     void* ws = nullptr;
     const size_t nc = (size_t)mth::argmax_chunks(n) * (size_t)rows;
     const hipError_t e = workspace(S(stream), nc * 8, &ws);
-    if (e != hipSuccess) return fail(MTH_EDEVICE, "mth_argmax: workspace allocation failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return workspace_fail("mth_argmax", e, nc * 8);
     return check_launch(mth::launch_argmax(logits, rows, n, ids, nullptr, nullptr, 0, 0, (float*)ws,
                                            (int*)((char*)ws + nc * 4), S(stream)),
                         "mth_argmax");

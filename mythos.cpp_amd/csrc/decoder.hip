@@ -33,7 +33,10 @@ struct mth_decoder {
 
     void* block = nullptr;  // one device allocation for every buffer below
     float *x = nullptr, *h = nullptr, *t = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
-    float *gu = nullptr, *a_inv = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr;
+    float *gu = nullptr, *a_inv = nullptr, *logits = nullptr;
+    char *kc = nullptr, *vc = nullptr;  // [layers][B][kv_heads][max_seq][head_dim], FP32 or bf16
+    size_t kv_elem = 4;
+    float* taps = nullptr;              // mth_decoder_set_taps
     float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr, *arg_v = nullptr;
     int8_t* aq = nullptr;
     int *hist = nullptr, *step = nullptr, *ids = nullptr, *arg_i = nullptr;
@@ -86,20 +89,33 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     do {                                 \
         if ((e = (call)) != hipSuccess) return e; \
     } while (0)
+    const int64_t tap_floats = mth_decoder_tap_floats(d);
+    auto tap_copy = [&](float* dst, const void* src, size_t bytes) {
+        return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
+    };
     TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, B, (int)H, (int)c.vocab, s));
     for (int64_t l = 0; l < c.layers; l++) {
         const mth_decoder_layer& L = d->layers[(size_t)l];
-        float* kc = d->kc + l * d->layer_kv;
-        float* vc = d->vc + l * d->layer_kv;
+        char* kc = d->kc + l * d->layer_kv * d->kv_elem;
+        char* vc = d->vc + l * d->layer_kv * d->kv_elem;
+        // taps of this layer (mth_decoder_set_taps): x_attn, gu, act, aq, a_inv, down
+        float* tp = d->taps ? d->taps + l * tap_floats : nullptr;
+        float* tp_gu = tp ? tp + B * H : nullptr;
+        float* tp_act = tp ? tp_gu + B * 2 * F : nullptr;
+        float* tp_aq = tp ? tp_act + B * F : nullptr;
+        float* tp_inv = tp ? tp_aq + B * F / 4 : nullptr;
+        float* tp_down = tp ? tp_inv + B : nullptr;
         // residual of the previous layer's FFN folded into this norm
         TRY(mth::launch_rms_norm(d->x, l == 0 ? nullptr : d->t, L.attn_norm, d->h, B, H, c.eps, s));
         TRY(oil8(d, L.wq, L.cbq, d->h, d->q, QD, H, s));
         TRY(oil8(d, L.wk, L.cbk, d->h, d->k, KD, H, s));
         TRY(oil8(d, L.wv, L.cbv, d->h, d->v, KD, H, s));
-        TRY(mth::launch_rope_attention(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, d->att, d->step, B,
-                                       (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
+        TRY(mth::launch_rope_attention(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
+                                       d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq,
+                                       s));
         TRY(oil8(d, L.wo, L.cbo, d->att, d->t, H, QD, s));
         TRY(mth::launch_rms_norm(d->x, d->t, L.ffn_norm, d->h, B, H, c.eps, s));
+        if (tp) TRY(tap_copy(tp, d->x, (size_t)(B * H) * 4));
         const int64_t nb = c.cb_block ? H / c.cb_block : 1;
         const bool fused = L.wup == L.wgate + F * (H / 2) && (c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
         // gate/up, then silu(gate)*up quantised to int8 per token (once, not
@@ -107,16 +123,28 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         // int8 activations
         if (fused) {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
-            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + F, d->aq, d->a_inv, B, F, 2 * F, 2 * F, s));
+            if (tp) TRY(tap_copy(tp_gu, d->gu, (size_t)(B * 2 * F) * 4));
+            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + F, d->aq, d->a_inv, tp_act, B, F, 2 * F, 2 * F, s));
         } else {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
-            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, B, F, F, F, s));
+            if (tp) {  // gate [B][F] and up [B][F] -> [B][gate, up]
+                TRY(hipMemcpy2DAsync(tp_gu, (size_t)(2 * F) * 4, d->gu, (size_t)F * 4, (size_t)F * 4, (size_t)B,
+                                     hipMemcpyDeviceToDevice, s));
+                TRY(hipMemcpy2DAsync(tp_gu + F, (size_t)(2 * F) * 4, d->gu + B * F, (size_t)F * 4, (size_t)F * 4,
+                                     (size_t)B, hipMemcpyDeviceToDevice, s));
+            }
+            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, tp_act, B, F, F, F, s));
         }
         if ((((uintptr_t)L.wdown | (uintptr_t)d->aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, B))
             TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->aq, d->a_inv, d->t, H, F, B, d->bt_partial, s));
         else
             TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, B, s));
+        if (tp) {
+            TRY(tap_copy(tp_aq, d->aq, (size_t)(B * F)));
+            TRY(tap_copy(tp_inv, d->a_inv, (size_t)B * 4));
+            TRY(tap_copy(tp_down, d->t, (size_t)(B * H) * 4));
+        }
     }
     TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
     TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
@@ -145,6 +173,8 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     if (!mth::silu_mul_quant_supported(c.ffn))
         return api_fail(MTH_EUNSUPPORTED, "mth_decoder_create: ffn=%lld above 12288", (long long)c.ffn);
     if (c.heads % c.kv_heads != 0) return api_fail(MTH_EINVAL, "mth_decoder_create: heads %% kv_heads != 0");
+    if (c.kv_dtype != 0 && c.kv_dtype != 1)
+        return api_fail(MTH_EINVAL, "mth_decoder_create: kv_dtype=%lld (0 = FP32, 1 = bf16)", (long long)c.kv_dtype);
     if (c.cb_block < 0 || (c.cb_block > 0 && c.hidden % c.cb_block != 0))
         return api_fail(MTH_EINVAL, "mth_decoder_create: cb_block=%lld does not divide hidden", (long long)c.cb_block);
     if (!mth::attention_supported((int)c.head_dim, (int)c.max_seq))
@@ -162,6 +192,7 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     const int64_t QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
     d->hist_stride = c.max_seq + 1;
     d->layer_kv = B * KD * c.max_seq;
+    d->kv_elem = c.kv_dtype == 1 ? 2 : 4;
     // workspace of the batched GEMVs: the largest of every projection's need
     const size_t partial = std::max({mth::oil4_bt_partial_bytes(2 * F, H), mth::oil8_bt_partial_bytes(QD, H),
                                      mth::oil8_bt_partial_bytes(KD, H), mth::oil8_bt_partial_bytes(H, QD),
@@ -178,8 +209,8 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->logits, (size_t)(B * c.vocab) * 4},
         {(void**)&d->arg_v, (size_t)(B * mth::argmax_chunks(c.vocab)) * 4},
         {(void**)&d->arg_i, (size_t)(B * mth::argmax_chunks(c.vocab)) * 4},
-        {(void**)&d->kc, (size_t)(c.layers * d->layer_kv) * 4},
-        {(void**)&d->vc, (size_t)(c.layers * d->layer_kv) * 4},
+        {(void**)&d->kc, (size_t)(c.layers * d->layer_kv) * d->kv_elem},
+        {(void**)&d->vc, (size_t)(c.layers * d->layer_kv) * d->kv_elem},
         {(void**)&d->rope_cos, (size_t)(c.max_seq * (c.head_dim / 2)) * 4},
         {(void**)&d->rope_sin, (size_t)(c.max_seq * (c.head_dim / 2)) * 4},
         {(void**)&d->bt_partial, partial},
@@ -284,7 +315,7 @@ int mth_decoder_step(mth_decoder* d, int64_t n, int use_graph, mth_stream_t stre
                         (long long)d->steps, (long long)d->c.max_seq);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = hipSuccess;
-    if (use_graph) {
+    if (use_graph && !d->taps) {
         if (d->exec && (d->graph_batch != d->batch || d->graph_prompt != d->prompt_len)) d->drop_graph();
         if (!d->exec) {
             e = hipStreamBeginCapture(d->cap_stream, hipStreamCaptureModeThreadLocal);
@@ -332,5 +363,36 @@ int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_str
 }
 
 int64_t mth_decoder_steps_done(const mth_decoder* d) { return d ? d->steps : 0; }
+
+int64_t mth_decoder_tap_floats(const mth_decoder* d) {
+    if (!d) return 0;
+    const int64_t B = d->batch, H = d->c.hidden, F = d->c.ffn;
+    return B * (2 * H + 3 * F + F / 4 + 1);
+}
+
+int mth_decoder_read_kv(const mth_decoder* d, int64_t layer, void* k, void* v, mth_stream_t stream) {
+    if (!d) return api_fail(MTH_EINVAL, "mth_decoder_read_kv: null decoder");
+    if (d->batch == 0) return api_fail(MTH_EINVAL, "mth_decoder_read_kv: no sequences started");
+    if (layer < 0 || layer >= d->c.layers)
+        return api_fail(MTH_EINVAL, "mth_decoder_read_kv: layer %lld outside 0..%lld", (long long)layer,
+                        (long long)d->c.layers - 1);
+    hipStream_t s = (hipStream_t)stream;
+    // rows of the started batch: the first batch * kv_heads * max_seq * head_dim elements of the layer
+    const size_t bytes = (size_t)(d->batch * d->c.kv_heads * d->c.max_seq * d->c.head_dim) * d->kv_elem;
+    const size_t off = (size_t)(layer * d->layer_kv) * d->kv_elem;
+    hipError_t e = hipSuccess;
+    if (k) e = hipMemcpyAsync(k, d->kc + off, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && v) e = hipMemcpyAsync(v, d->vc + off, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return api_fail(MTH_EDEVICE, "mth_decoder_read_kv: %s", hipGetErrorString(e));
+    return api_ok();
+}
+
+int mth_decoder_set_taps(mth_decoder* d, float* taps) {
+    if (!d) return api_fail(MTH_EINVAL, "mth_decoder_set_taps: null decoder");
+    if (taps && d->batch == 0) return api_fail(MTH_EINVAL, "mth_decoder_set_taps: no sequences started");
+    d->taps = taps;
+    return api_ok();
+}
 
 }  // extern "C"

@@ -217,6 +217,26 @@ __global__ __launch_bounds__(kT) void rope_kv_k(float* __restrict__ q, const flo
     }
 }
 
+// ---- KV-cache element types -----------------------------------------------------
+// FP32, or bf16 (round to nearest even on store, exact widening on load).
+__device__ __forceinline__ float kv_store_value(float v, float) { return v; }
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint16_t kv_store_value(float v, uint16_t) { return bf16_rne(v); }
+// the value an element reads back as after a store
+__device__ __forceinline__ float kv_rounded(float v, float) { return v; }
+__device__ __forceinline__ float kv_rounded(float v, uint16_t) { return __uint_as_float((uint32_t)bf16_rne(v) << 16); }
+__device__ __forceinline__ float4 kv_load4(const float* p) { return *(const float4*)p; }
+__device__ __forceinline__ float4 kv_load4(const uint16_t* p) {
+    const uint2 w = *(const uint2*)p;
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                       __uint_as_float(w.y & 0xffff0000u));
+}
+
 // ---- decode attention --------------------------------------------------------
 // Workgroup (head h, token b) over ctx = *step + ctx0 + 1 positions of kv
 // head kh = h % kv_heads, cache rows [b][kh][t][D].
@@ -232,10 +252,12 @@ __global__ __launch_bounds__(kT) void rope_kv_k(float* __restrict__ q, const flo
 // them to the cache row pos (KVCache::append) -- no workgroup reads that row
 // from memory in this launch.  Without ROPE, q is already rotated and all
 // ctx rows come from the cache.
-template <int D, bool ROPE>
+// KV: the cache element type (float, or uint16_t holding bf16 bits); with
+// bf16, the current position's k/v are rounded in LDS as the cache stores them.
+template <int D, bool ROPE, typename KV>
 __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, const float* __restrict__ kin,
                                                   const float* __restrict__ vin, const float* __restrict__ cos_t,
-                                                  const float* __restrict__ sin_t, float* kc, float* vc,
+                                                  const float* __restrict__ sin_t, KV* kc, KV* vc,
                                                   float* __restrict__ out, const int* __restrict__ step, int ctx0,
                                                   int heads, int kv_heads, int max_seq, float scale) {
     constexpr int G = D / 4;        // float4 column groups
@@ -261,26 +283,26 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
             qs[tid] = q1 * c - q2 * s;
             qs[tid + D / 2] = q1 * s + q2 * c;
             const float k1 = kh_in[tid], k2 = kh_in[tid + D / 2];
-            ks[tid] = k1 * c - k2 * s;
-            ks[tid + D / 2] = k1 * s + k2 * c;
-            vs[tid] = vh_in[tid];
-            vs[tid + D / 2] = vh_in[tid + D / 2];
+            ks[tid] = kv_rounded(k1 * c - k2 * s, KV{});
+            ks[tid + D / 2] = kv_rounded(k1 * s + k2 * c, KV{});
+            vs[tid] = kv_rounded(vh_in[tid], KV{});
+            vs[tid + D / 2] = kv_rounded(vh_in[tid + D / 2], KV{});
         }
         __syncthreads();
         if (h < kv_heads && tid < D) {
-            kc[(crow + pos) * D + tid] = ks[tid];
-            vc[(crow + pos) * D + tid] = vs[tid];
+            kc[(crow + pos) * D + tid] = kv_store_value(ks[tid], KV{});
+            vc[(crow + pos) * D + tid] = kv_store_value(vs[tid], KV{});
         }
     } else {
         if (tid < D) qs[tid] = qh[tid];
         __syncthreads();
     }
     const int nmem = ROPE ? pos : ctx;  // positions read from the cache
-    auto dot = [&](const float* kr) {
+    auto dot = [&](auto kr) {
         float s = 0.0f;
 #pragma unroll
         for (int d = 0; d < D; d += 4) {
-            const float4 k4 = *(const float4*)(kr + d);
+            const float4 k4 = kv_load4(kr + d);
             const float4 q4 = *(const float4*)(qs + d);
             s = s + q4.x * k4.x;
             s = s + q4.y * k4.y;
@@ -296,7 +318,7 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
         mx = fmaxf(mx, s);
     }
     if (ROPE && tid == (pos % kT)) {  // the current position, from LDS
-        const float s = dot(ks);
+        const float s = dot((const float*)ks);
         sc[pos] = s;
         mx = fmaxf(mx, s);
     }
@@ -320,16 +342,16 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
         a.z = fmaf(p, v.z, a.z);
         a.w = fmaf(p, v.w, a.w);
     };
-    const float* vcol = vc + crow * D + 4 * g;
+    const KV* vcol = vc + crow * D + 4 * g;
     int t = sl;
     for (; t + 3 * SL < nmem; t += 4 * SL) {
         float4 v4[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v4[j] = *(const float4*)(vcol + (int64_t)(t + j * SL) * D);
+        for (int j = 0; j < 4; ++j) v4[j] = kv_load4(vcol + (int64_t)(t + j * SL) * D);
 #pragma unroll
         for (int j = 0; j < 4; ++j) axpy(acc[j], sc[t + j * SL] * inv, v4[j]);
     }
-    for (; t < nmem; t += SL) axpy(acc[0], sc[t] * inv, *(const float4*)(vcol + (int64_t)t * D));
+    for (; t < nmem; t += SL) axpy(acc[0], sc[t] * inv, kv_load4(vcol + (int64_t)t * D));
     if (ROPE && sl == (pos % SL)) axpy(acc[1], sc[pos] * inv, *(const float4*)(vs + 4 * g));
     acc[0].x += acc[1].x; acc[0].y += acc[1].y; acc[0].z += acc[1].z; acc[0].w += acc[1].w;
     acc[2].x += acc[3].x; acc[2].y += acc[3].y; acc[2].z += acc[3].z; acc[2].w += acc[3].w;
@@ -356,9 +378,11 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
 // (src/int8_quant.cpp:8-31): max|a| (floor 1e-10), scale = 127/max,
 // q = (int8)round_half_away(a * scale), inv = max/127.  n <= kSQT * kSQ.
 constexpr int kSQT = 1024, kSQ = 12;
+// act (optional): the FP32 activations, [rows][n].
 __global__ __launch_bounds__(kSQT) void silu_mul_quant_k(const float* __restrict__ g, const float* __restrict__ u,
-                                                         int8_t* __restrict__ q, float* __restrict__ inv_scale, int n,
-                                                         int64_t gstride, int64_t ustride) {
+                                                         int8_t* __restrict__ q, float* __restrict__ inv_scale,
+                                                         float* __restrict__ act, int n, int64_t gstride,
+                                                         int64_t ustride) {
     __shared__ float red[kSQT / 64];
     const int r = blockIdx.x, tid = threadIdx.x;
     const float* gr = g + r * gstride;
@@ -389,6 +413,14 @@ __global__ __launch_bounds__(kSQT) void silu_mul_quant_k(const float* __restrict
     for (int j = 0; j < kSQ; ++j) {
         const int i = tid + j * kSQT;
         if (i < n) qr[i] = (int8_t)quant_i8(gv[j], sc);
+    }
+    if (act) {
+        float* ar = act + (int64_t)r * n;
+#pragma unroll
+        for (int j = 0; j < kSQ; ++j) {
+            const int i = tid + j * kSQT;
+            if (i < n) ar[i] = gv[j];
+        }
     }
     if (tid == 0) inv_scale[r] = __fdiv_rn(m, 127.0f);
 }
@@ -538,43 +570,46 @@ bool attention_supported(int head_dim, int max_seq) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) && max_seq > 0 && max_seq <= 16384;
 }
 
-template <bool ROPE>
+template <bool ROPE, typename KV>
 static hipError_t run_attention(const float* q, const float* k, const float* v, const float* cos_t,
-                                const float* sin_t, float* kc, float* vc, float* out, const int* step, int ctx0,
+                                const float* sin_t, KV* kc, KV* vc, float* out, const int* step, int ctx0,
                                 int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
     const dim3 grid((unsigned)heads, (unsigned)batch);
     if (head_dim == 64)
-        attention_k<64, ROPE><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads, kv_heads,
-                                                    max_seq, scale);
+        attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+                                                        kv_heads, max_seq, scale);
     else if (head_dim == 128)
-        attention_k<128, ROPE><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
-                                                     kv_heads, max_seq, scale);
+        attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+                                                         kv_heads, max_seq, scale);
     else
-        attention_k<256, ROPE><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
-                                                     kv_heads, max_seq, scale);
+        attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+                                                         kv_heads, max_seq, scale);
     return hipGetLastError();
 }
 
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
                             int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
-    return run_attention<false>(q, nullptr, nullptr, nullptr, nullptr, (float*)kc, (float*)vc, out, step, ctx0,
-                                batch, heads, kv_heads, head_dim, max_seq, s);
+    return run_attention<false, float>(q, nullptr, nullptr, nullptr, nullptr, (float*)kc, (float*)vc, out, step,
+                                       ctx0, batch, heads, kv_heads, head_dim, max_seq, s);
 }
 
 hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
-                                 const float* sin_t, float* kc, float* vc, float* out, const int* step,
+                                 const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out, const int* step,
                                  int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
-    return run_attention<true>(q, k, v, cos_t, sin_t, kc, vc, out, step, 0, batch, heads, kv_heads, head_dim,
-                               max_seq, s);
+    if (kv_bf16)
+        return run_attention<true, uint16_t>(q, k, v, cos_t, sin_t, (uint16_t*)kc, (uint16_t*)vc, out, step, 0,
+                                             batch, heads, kv_heads, head_dim, max_seq, s);
+    return run_attention<true, float>(q, k, v, cos_t, sin_t, (float*)kc, (float*)vc, out, step, 0, batch, heads,
+                                      kv_heads, head_dim, max_seq, s);
 }
 
 bool silu_mul_quant_supported(int64_t n) { return n > 0 && n <= (int64_t)kSQT * kSQ; }
 
-hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows,
-                                 int64_t n, int64_t gstride, int64_t ustride, hipStream_t s) {
-    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, q, inv_scale, (int)n, gstride, ustride);
+hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, float* act,
+                                 int64_t rows, int64_t n, int64_t gstride, int64_t ustride, hipStream_t s) {
+    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, q, inv_scale, act, (int)n, gstride, ustride);
     return hipGetLastError();
 }
 

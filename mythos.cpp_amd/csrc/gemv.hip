@@ -326,10 +326,10 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.a, cur.b, acc, 0, 0, 0);
         if (m + 1 < NMF) cur = nxt;
     }
-    // D[4g+i][n]: rows' hi (n = 0) + lo (n = 1) parts
+    // D[4g+i][n]: rows' hi (n = 0) + lo (n = 1) parts (oil4_hi_lo)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float s = acc[i] + __shfl_xor(acc[i], 1, MTH_WAVE);
+        const float s = oil4_hi_lo(acc[i], __shfl_xor(acc[i], 1, MTH_WAVE));
         if (n == 0) part[wave * 16 + 4 * g + i] = ldexpf(s, -sh);
     }
     __syncthreads();
@@ -445,10 +445,10 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
         }
     }
-    // D[4q+i][n]: rows' hi (n = 0) + lo (n = 1) parts
+    // D[4q+i][n]: rows' hi (n = 0) + lo (n = 1) parts (oil4_hi_lo)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float s = acc[i] + __shfl_xor(acc[i], 1, MTH_WAVE);
+        const float s = oil4_hi_lo(acc[i], __shfl_xor(acc[i], 1, MTH_WAVE));
         if (j == 0) part[wave * 16 + 4 * q + i] = ldexpf(s, -sh);
     }
     __syncthreads();

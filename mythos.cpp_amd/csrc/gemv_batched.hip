@@ -122,19 +122,20 @@ __global__ __launch_bounds__(256) void oil4_gemv_bt(const uint8_t* nib, const ui
         const CbPlanes pl = SHARED ? shared_planes : w.planes(p, stage, lane);
         uint4 xa, yb;
         w.exchange(p, lane, xa, yb);
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // hi and lo parts in separate accumulators (combined by oil4_hi_lo)
+        floatx4 acc_h = {0.0f, 0.0f, 0.0f, 0.0f}, acc_l = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const half8 a = lookup8(m < 4 ? u4get(xa, m) : u4get(yb, m - 4), pl);
             const half8 bh = *(const half8*)(bbuf + bt_slot(m, q, j));
             const half8 bl = *(const half8*)(bbuf + L::frag + bt_slot(m, q, j));
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc, 0, 0, 0);
+            acc_h = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_h, 0, 0, 0);
+            acc_l = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_l, 0, 0, 0);
         }
         // D[4q+i][n] of token n = j, in units of 2^sh(n)
         const int shn = shifts[(p & 1) * kBtTok + j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ysum[i] += ldexpf(acc[i], -shn);
+        for (int i = 0; i < 4; ++i) ysum[i] += ldexpf(oil4_hi_lo(acc_h[i], acc_l[i]), -shn);
     }
 
     // ---- output: rows row0w + 4q + i, token j ----
@@ -282,7 +283,8 @@ size_t oil4_bt_partial_bytes(int64_t M, int64_t K) {
 }
 
 bool oil8_bt_supported(int64_t M, int64_t K, int64_t batch) {
-    return batch >= 2 && K >= 64 && K % 64 == 0 && M < (1ll << 31) && M * K < (1ll << 40);
+    // the kernel takes K and its slice width as int
+    return batch >= 2 && K >= 64 && K % 64 == 0 && K < (1ll << 31) && M < (1ll << 31) && M * K < (1ll << 40);
 }
 
 size_t oil8_bt_partial_bytes(int64_t M, int64_t K) {

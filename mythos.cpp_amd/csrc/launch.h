@@ -98,14 +98,15 @@ bool attention_supported(int head_dim, int max_seq);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
                             int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s);
 // RoPE of the current token's q/k at pos = *step, KV append, then attention
-// over pos + 1 positions (one launch).
+// over pos + 1 positions (one launch).  Caches FP32, or bf16 bits (kv_bf16).
 hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
-                                 const float* sin_t, float* kc, float* vc, float* out, const int* step,
+                                 const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out, const int* step,
                                  int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s);
-// silu(g) * u then quantize_per_token: q [rows][n] int8, inv_scale [rows].
+// silu(g) * u then quantize_per_token: q [rows][n] int8, inv_scale [rows];
+// act (nullable) receives the FP32 activations [rows][n].
 bool silu_mul_quant_supported(int64_t n);
-hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows,
-                                 int64_t n, int64_t gstride, int64_t ustride, hipStream_t s);
+hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, float* act,
+                                 int64_t rows, int64_t n, int64_t gstride, int64_t ustride, hipStream_t s);
 // Greedy argmax in two launches; pv/pi: rows * argmax_chunks(n) partials.
 // With hist: writes the next input token; with step: advances it last.
 int argmax_chunks(int64_t n);

@@ -127,6 +127,16 @@ __device__ __forceinline__ float row16_max(float v) {
     return v;
 }
 
+// Sum of the hi-part and lo-part dot products of an FP16 hi/lo split of x
+// (x*2^s = hi + lo).  An infinite codebook entry w meets both parts: w*hi is
+// +-Inf, but w*lo is NaN where lo is exactly 0, which the reference's single
+// product w*x (src/kernel_oil4.cpp:50) never gives.  So an infinite hi sum is
+// the result: the reference's sum is then that infinity too (a NaN in its sum
+// needs Inf*0, a NaN entry or infinities of both signs, each of which makes
+// the hi sum NaN as well), except where x_k is so small relative to max|x|
+// that hi_k underflows to 0 (|x_k| < max|x| * 2^-39).
+__device__ __forceinline__ float oil4_hi_lo(float hi, float lo) { return __builtin_isinf(hi) ? hi : hi + lo; }
+
 // Power-of-two exponent s with max|x| * 2^s < 2^15 (0 for zero / non-finite).
 __device__ __forceinline__ int fp16_scale_shift(float mx) {
     int e = 0;

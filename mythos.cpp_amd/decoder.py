@@ -21,14 +21,18 @@ VP, I64, I32, F32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
 
 EXPORTS = ("mth_decoder_create", "mth_decoder_destroy", "mth_decoder_set_layer", "mth_decoder_set_globals",
            "mth_decoder_start", "mth_decoder_step", "mth_decoder_buffers", "mth_decoder_read",
-           "mth_decoder_steps_done")
+           "mth_decoder_steps_done", "mth_decoder_set_taps", "mth_decoder_tap_floats", "mth_decoder_read_kv")
 
 CONFIG_KEYS = ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ffn", "max_seq", "cb_block",
                "max_batch")
 
 
 class Config(C.Structure):
-    _fields_ = [(k, C.c_int64) for k in CONFIG_KEYS] + [("eps", C.c_float), ("theta", C.c_float)]
+    _fields_ = [(k, C.c_int64) for k in CONFIG_KEYS] + [("eps", C.c_float), ("theta", C.c_float),
+                                                         ("kv_dtype", C.c_int64)]
+
+
+KV_DTYPES = {"f32": 0, "bf16": 1}
 
 
 class Layer(C.Structure):
@@ -59,6 +63,12 @@ _lib.mth_decoder_read.argtypes = [VP, VP, VP, VP]
 _lib.mth_decoder_read.restype = I32
 _lib.mth_decoder_steps_done.argtypes = [VP]
 _lib.mth_decoder_steps_done.restype = I64
+_lib.mth_decoder_set_taps.argtypes = [VP, VP]
+_lib.mth_decoder_set_taps.restype = I32
+_lib.mth_decoder_tap_floats.argtypes = [VP]
+_lib.mth_decoder_tap_floats.restype = I64
+_lib.mth_decoder_read_kv.argtypes = [VP, I64, VP, VP, VP]
+_lib.mth_decoder_read_kv.restype = I32
 
 
 def _check(rc):
@@ -67,10 +77,12 @@ def _check(rc):
 
 
 class Decoder:
-    def __init__(self, cfg: dict, max_batch: int = 1, device="cuda"):
+    def __init__(self, cfg: dict, max_batch: int = 1, device="cuda", kv_dtype: str = "f32"):
         self.cfg = dict(cfg, max_batch=max_batch)
         self.device = device
-        c = Config(*[int(self.cfg[k]) for k in CONFIG_KEYS], float(cfg["eps"]), float(cfg["theta"]))
+        self.kv_dtype = kv_dtype
+        c = Config(*[int(self.cfg[k]) for k in CONFIG_KEYS], float(cfg["eps"]), float(cfg["theta"]),
+                   KV_DTYPES[kv_dtype])
         h = VP()
         _check(_lib.mth_decoder_create(C.byref(c), C.byref(h)))
         self._h = h
@@ -145,6 +157,55 @@ class Decoder:
         _check(_lib.mth_decoder_read(self._h, None, out.ctypes.data, mythos_oil._stream(stream)))
         n = min(stride, max(self.prompt_len, self.steps_done + 1))
         return out[:, :n]
+
+    def enable_taps(self):
+        """Turn on the per-layer taps (mth_decoder_set_taps) for the started
+        batch; later steps run without a graph."""
+        torch = mythos_oil._torch()
+        n = int(_lib.mth_decoder_tap_floats(self._h))
+        self._taps = torch.zeros(self.cfg["layers"] * n, dtype=torch.float32, device=self.device)
+        _check(_lib.mth_decoder_set_taps(self._h, self._taps.data_ptr()))
+
+    def disable_taps(self):
+        _check(_lib.mth_decoder_set_taps(self._h, None))
+        self._taps = None
+
+    def taps(self) -> list:
+        """Host copies of the last step's taps: one dict per layer with
+        x_attn [B][H], gate [B][F], up [B][F], act [B][F], aq [B][F] int8,
+        a_inv [B], down [B][H]."""
+        torch = mythos_oil._torch()
+        torch.cuda.synchronize()
+        B, H, F = self.batch, self.cfg["hidden"], self.cfg["ffn"]
+        n = int(_lib.mth_decoder_tap_floats(self._h))
+        t = self._taps.cpu().numpy().reshape(self.cfg["layers"], n)
+        out = []
+        for row in t:
+            o, d = 0, {}
+            for name, size in (("x_attn", B * H), ("gu", B * 2 * F), ("act", B * F), ("aq", B * F // 4),
+                               ("a_inv", B), ("down", B * H)):
+                d[name] = row[o:o + size]
+                o += size
+            gu = d.pop("gu").reshape(B, 2 * F)
+            d["gate"], d["up"] = gu[:, :F].copy(), gu[:, F:].copy()
+            d["x_attn"] = d["x_attn"].reshape(B, H)
+            d["act"] = d["act"].reshape(B, F)
+            d["aq"] = np.ascontiguousarray(d["aq"]).view(np.int8).reshape(B, F)
+            d["down"] = d["down"].reshape(B, H)
+            out.append(d)
+        return out
+
+    def read_kv(self, layer: int, stream=None):
+        """Layer `layer`'s K and V caches as FP32 host arrays
+        [batch][kv_heads][max_seq][head_dim] (bf16 caches widened exactly)."""
+        c = self.cfg
+        shape = (self.batch, c["kv_heads"], c["max_seq"], c["head_dim"])
+        dt = np.uint16 if self.kv_dtype == "bf16" else np.float32
+        k, v = np.empty(shape, dt), np.empty(shape, dt)
+        _check(_lib.mth_decoder_read_kv(self._h, layer, k.ctypes.data, v.ctypes.data, mythos_oil._stream(stream)))
+        if dt == np.uint16:
+            k, v = ((a.astype(np.uint32) << 16).view(np.float32) for a in (k, v))
+        return k, v
 
     def generate(self, prompts: np.ndarray, max_tokens: int, graph: bool = True) -> np.ndarray:
         """Generator::generate_tokens with greedy sampling and no EOS stop:

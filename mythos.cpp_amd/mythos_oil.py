@@ -19,7 +19,7 @@ HOST_LIB_PATH = os.path.join(_HERE, "libmythos_host.so")
 
 # Every extern "C" symbol declared in include/mythos_oil.h.
 EXPORTS = (
-    "mth_last_error", "mth_version",
+    "mth_last_error", "mth_version", "mth_workspace_reserve",
     "mth_oil8_gemm", "mth_oil8_gemv",
     "mth_oil4_gemm", "mth_oil4_gemv", "mth_oil4_gemm_prefill",
     "mth_quantize_per_token", "mth_dequantize_per_tensor",
@@ -85,6 +85,7 @@ _SIG = {
     "mth_rope_kv": [VP, VP, VP, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP],
     "mth_attention_decode": [VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP],
     "mth_argmax": [VP, VP, I64, I64, VP],
+    "mth_workspace_reserve": [I64, VP],
 }
 for _n, _a in _SIG.items():
     _f = getattr(_lib, _n)
@@ -104,6 +105,11 @@ def version() -> int:
 
 def last_error() -> str:
     return _lib.mth_last_error().decode()
+
+
+def workspace_reserve(nbytes: int, stream=None) -> None:
+    """Reserve the stream's device workspace before capturing batched calls."""
+    _check(_lib.mth_workspace_reserve(int(nbytes), _stream(stream)))
 
 
 def _check(rc: int) -> None:

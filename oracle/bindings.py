@@ -56,7 +56,8 @@ VP = C.c_void_p
 
 class DecoderConfig(C.Structure):
     _fields_ = [(n, C.c_int64) for n in ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ffn",
-                                         "max_seq", "cb_block")] + [("eps", C.c_float), ("theta", C.c_float)]
+                                         "max_seq", "cb_block")] + [("eps", C.c_float), ("theta", C.c_float),
+                                                                    ("kv_bf16", C.c_int64)]
 
 
 class DecoderLayer(C.Structure):
@@ -112,11 +113,16 @@ class Oracle:
             "orc_rope_apply": [VP, I64, I64, I64, VP, VP],
             "orc_attention_decode": [VP, VP, VP, VP, I64, I64, I64, I64, I64],
             "orc_decoder_step": [C.POINTER(DecoderConfig), C.POINTER(DecoderModel), VP, VP, I64, I32, VP, I32, I32],
+            "orc_decoder_attn_half": [C.POINTER(DecoderConfig), C.POINTER(DecoderModel), I64, VP, VP, I64, VP, I32,
+                                      I32],
+            "orc_i2s_gemv_rows": [VP, F32, VP, F32, VP, I64, I64, I32],
         }
         for name, args in sig.items():
             f = getattr(L, name)
             f.argtypes = args
             f.restype = None
+        L.orc_bf16_round.argtypes = [F32]
+        L.orc_bf16_round.restype = F32
         L.orc_fp16_to_float.argtypes = [C.c_uint16]
         L.orc_fp16_to_float.restype = F32
         L.orc_half_to_float_codebook.argtypes = [C.c_uint16]
@@ -237,6 +243,17 @@ class Oracle:
         self.lib.orc_i2s_gemm_vnni(_p(w, np.uint8), _p(a, np.int8), _p(o, np.float32), M, N, K)
         return o
 
+    def i2s_gemv_rows(self, packed, w_scale, q, inv, M, K, threads=1):
+        """i2s_gemv over M rows for int8 activations q [K] and act_scale inv."""
+        _need(packed, M * K // 4, "packed"); _need(q, K, "q")
+        y = np.empty(M, np.float32)
+        self.lib.orc_i2s_gemv_rows(_p(packed, np.uint8), w_scale, _p(q, np.int8), float(inv), _p(y, np.float32),
+                                   M, K, threads)
+        return y
+
+    def bf16_round(self, f: float) -> float:
+        return self.lib.orc_bf16_round(f)
+
     def i2s_gemv_f32(self, packed, w_scale, x, M, K, batch, threads=1):
         _need(packed, M * K // 4, "packed"); _need(x, batch * K, "x")
         y = np.empty((batch, M), np.float32)
@@ -314,7 +331,7 @@ class Oracle:
 class _OracleDecoder:
     def __init__(self, orc: "Oracle", cfg: dict, model: dict):
         self.orc, self.cfg = orc, cfg
-        self.c = DecoderConfig(*[cfg[k] for k in DECODER_CONFIG_KEYS])
+        self.c = DecoderConfig(*[cfg[k] for k in DECODER_CONFIG_KEYS], int(cfg.get("kv_bf16", 0)))
         keep = []
 
         def ptr(a, dtype):
@@ -344,10 +361,25 @@ class _OracleDecoder:
 
     def step(self, kc, vc, pos: int, token: int, down_mode: int = 0, threads: int = 8) -> np.ndarray:
         assert 0 <= pos < self.cfg["max_seq"]
+        assert kc.shape == vc.shape == (self.cfg["layers"], self.cfg["kv_heads"], self.cfg["max_seq"],
+                                        self.cfg["head_dim"])
         out = np.empty(self.cfg["vocab"], np.float32)
         self.orc.lib.orc_decoder_step(C.byref(self.c), C.byref(self.m), _p(kc, np.float32), _p(vc, np.float32),
                                       pos, token, _p(out, np.float32), down_mode, threads)
         return out
+
+    def attn_half(self, kc, vc, layer: int, pos: int, x, append: bool = True, threads: int = 8) -> np.ndarray:
+        """x + O(attention(rmsnorm(x))) of `layer` for one token at pos over
+        kc/vc [layers][kv_heads][max_seq][head_dim]; with append, the
+        position's K/V are computed and written into the cache first."""
+        assert 0 <= pos < self.cfg["max_seq"] and 0 <= layer < self.cfg["layers"]
+        assert kc.shape == vc.shape == (self.cfg["layers"], self.cfg["kv_heads"], self.cfg["max_seq"],
+                                        self.cfg["head_dim"])
+        y = np.array(x, np.float32, copy=True).ravel()
+        assert y.size == self.cfg["hidden"]
+        self.orc.lib.orc_decoder_attn_half(C.byref(self.c), C.byref(self.m), layer, _p(kc[layer], np.float32),
+                                           _p(vc[layer], np.float32), pos, _p(y, np.float32), int(append), threads)
+        return y
 
 
 class Reference:

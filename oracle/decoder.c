@@ -172,19 +172,68 @@ static void ternary_dense(const uint8_t* packed, float w_scale, const float* a, 
     }
 }
 
-void orc_decoder_step(const orc_decoder_config* c, const orc_decoder_model* m, float* kcache, float* vcache,
-                      int64_t pos, int32_t token, float* logits, int down_mode, int nthreads) {
-    const int64_t H = c->hidden, F = c->ffn, D = c->head_dim;
+/* Round to the nearest bf16 (ties to even), back to float. */
+float orc_bf16_round(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return f;  /* NaN */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void orc_i2s_gemv_rows(const uint8_t* packed, float w_scale, const int8_t* q, float inv, float* y, int64_t M,
+                       int64_t K, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int64_t m = 0; m < M; m++) orc_i2s_gemv(packed + m * (K / 4), w_scale, q, inv, y + m, K);
+}
+
+void orc_decoder_attn_half(const orc_decoder_config* c, const orc_decoder_model* m, int64_t l, float* kc,
+                           float* vc, int64_t pos, float* x, int append, int nthreads) {
+    const int64_t H = c->hidden, D = c->head_dim;
     const int64_t QD = c->heads * D, KD = c->kv_heads * D;
-    float* buf = (float*)malloc(sizeof(float) * (size_t)(3 * H + 4 * QD + 3 * F));
-    float* x = buf;            /* residual stream */
-    float* h = x + H;          /* normed input */
+    const orc_decoder_layer* L = &m->layers[l];
+    float* buf = (float*)malloc(sizeof(float) * (size_t)(2 * H + 4 * QD));
+    float* h = buf;            /* normed input */
     float* t = h + H;          /* projection output */
     float* q = t + H;
     float* k = q + QD;
     float* v = k + QD;
     float* att = v + QD;
-    float* g = att + QD;
+    if (nthreads < 1) nthreads = 1;
+    orc_rms_norm(x, L->attn_norm, c->eps, h, 1, H);
+    orc_oil8_gemv(L->wq, L->cbq, h, q, QD, H, 1, nthreads);
+    orc_rope_apply(q, c->heads, D, pos, m->rope_cos, m->rope_sin);
+    if (append) {
+        orc_oil8_gemv(L->wk, L->cbk, h, k, KD, H, 1, nthreads);
+        orc_oil8_gemv(L->wv, L->cbv, h, v, KD, H, 1, nthreads);
+        orc_rope_apply(k, c->kv_heads, D, pos, m->rope_cos, m->rope_sin);
+        if (c->kv_bf16)        /* a bf16 cache stores the rounded values */
+            for (int64_t i = 0; i < KD; i++) {
+                k[i] = orc_bf16_round(k[i]);
+                v[i] = orc_bf16_round(v[i]);
+            }
+        for (int64_t kh = 0; kh < c->kv_heads; kh++) {    /* KVCache::append, src/kv_cache.cpp:122-133 */
+            memcpy(kc + (kh * c->max_seq + pos) * D, k + kh * D, sizeof(float) * (size_t)D);
+            memcpy(vc + (kh * c->max_seq + pos) * D, v + kh * D, sizeof(float) * (size_t)D);
+        }
+    }
+    orc_attention_decode(q, kc, vc, att, c->heads, c->kv_heads, D, pos + 1, c->max_seq);
+    orc_oil8_gemv(L->wo, L->cbo, att, t, H, QD, 1, nthreads);
+    orc_add(t, x, x, H);
+    free(buf);
+}
+
+void orc_decoder_step(const orc_decoder_config* c, const orc_decoder_model* m, float* kcache, float* vcache,
+                      int64_t pos, int32_t token, float* logits, int down_mode, int nthreads) {
+    const int64_t H = c->hidden, F = c->ffn, D = c->head_dim;
+    float* buf = (float*)malloc(sizeof(float) * (size_t)(3 * H + 3 * F));
+    float* x = buf;            /* residual stream */
+    float* h = x + H;          /* normed input */
+    float* t = h + H;          /* projection output */
+    float* g = t + H;
     float* u = g + F;
     float* a = u + F;
     if (nthreads < 1) nthreads = 1;
@@ -195,19 +244,7 @@ void orc_decoder_step(const orc_decoder_config* c, const orc_decoder_model* m, f
         const orc_decoder_layer* L = &m->layers[l];
         float* kc = kcache + l * c->kv_heads * c->max_seq * D;
         float* vc = vcache + l * c->kv_heads * c->max_seq * D;
-        orc_rms_norm(x, L->attn_norm, c->eps, h, 1, H);
-        orc_oil8_gemv(L->wq, L->cbq, h, q, QD, H, 1, nthreads);
-        orc_oil8_gemv(L->wk, L->cbk, h, k, KD, H, 1, nthreads);
-        orc_oil8_gemv(L->wv, L->cbv, h, v, KD, H, 1, nthreads);
-        orc_rope_apply(q, c->heads, D, pos, m->rope_cos, m->rope_sin);
-        orc_rope_apply(k, c->kv_heads, D, pos, m->rope_cos, m->rope_sin);
-        for (int64_t kh = 0; kh < c->kv_heads; kh++) {
-            memcpy(kc + (kh * c->max_seq + pos) * D, k + kh * D, sizeof(float) * (size_t)D);
-            memcpy(vc + (kh * c->max_seq + pos) * D, v + kh * D, sizeof(float) * (size_t)D);
-        }
-        orc_attention_decode(q, kc, vc, att, c->heads, c->kv_heads, D, pos + 1, c->max_seq);
-        orc_oil8_gemv(L->wo, L->cbo, att, t, H, QD, 1, nthreads);
-        orc_add(t, x, x, H);
+        orc_decoder_attn_half(c, m, l, kc, vc, pos, x, 1, nthreads);
         orc_rms_norm(x, L->ffn_norm, c->eps, h, 1, H);
         orc_oil4_gemv_blocked(L->wgate, L->cbgate, c->cb_block, h, g, F, H, 1, nthreads);
         orc_oil4_gemv_blocked(L->wup, L->cbup, c->cb_block, h, u, F, H, 1, nthreads);

@@ -108,6 +108,7 @@ int32_t orc_argmax(const float* logits, int64_t n);                    /* src/sa
 typedef struct {
     int64_t vocab, hidden, layers, heads, kv_heads, head_dim, ffn, max_seq, cb_block;
     float eps, theta;
+    int64_t kv_bf16;      /* 1: K/V rounded to bf16 (nearest even) when appended */
 } orc_decoder_config;
 
 typedef struct {          /* one block; weights in [out][in] rows */
@@ -137,6 +138,22 @@ typedef struct {
 void orc_decoder_step(const orc_decoder_config* c, const orc_decoder_model* m, float* kcache,
                       float* vcache, int64_t pos, int32_t token, float* logits, int down_mode,
                       int nthreads);
+
+/* The attention half of layer l for one token: x <- x + O(attention(rmsnorm(x)))
+ * (src/transformer.cpp:396-403) over the layer's cache kc/vc
+ * [kv_heads][max_seq][head_dim].  append = 1 computes the position's K/V and
+ * writes them into the cache first; append = 0 takes the cache as it is
+ * (position pos already filled, e.g. with another implementation's values). */
+void orc_decoder_attn_half(const orc_decoder_config* c, const orc_decoder_model* m, int64_t l, float* kc,
+                           float* vc, int64_t pos, float* x, int append, int nthreads);
+
+/* i2s_gemv (src/kernel_i2s.cpp:32-40) over M rows for given int8 activations
+ * q [K] and act_scale inv: y[m]. */
+void orc_i2s_gemv_rows(const uint8_t* packed, float w_scale, const int8_t* q, float inv, float* y, int64_t M,
+                       int64_t K, int nthreads);
+
+/* float -> bf16 -> float, round to nearest even (NaN kept a NaN). */
+float orc_bf16_round(float f);
 
 /* ---- OIL4 prefill GEMM reference: C[m][n] = bf16(sum_k A[m][k] * W[n][k]) ---- */
 void orc_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cb16,

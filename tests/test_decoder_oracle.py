@@ -186,3 +186,78 @@ def test_decoder_with_attention_against_float64(oracle, gold, tiny):
         got = dec.step(kc, vc, pos, tok, down_mode=1, threads=1).astype(np.float64)
         err = np.linalg.norm(got - ref[pos]) / np.linalg.norm(ref[pos])
         assert err < 1e-5, (pos, err)
+
+
+def test_bf16_round_pins(oracle):
+    """orc_bf16_round: round to the nearest bf16, ties to even, checked
+    against an integer restatement and hand-picked ties and specials."""
+    g = np.random.default_rng(3)
+    x = np.concatenate([g.normal(0, 1, 4000), g.normal(0, 1e30, 50), [0.0, -0.0, np.inf, -np.inf, 3.0e38]])
+    x = x.astype(np.float32)
+    got = np.array([oracle.bf16_round(float(v)) for v in x], np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    want = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # ties: 1 + 2^-8 sits halfway between 1 and 1 + 2^-7 -> the even one (1);
+    # 1 + 3*2^-8 halfway between 1 + 2^-7 and 1 + 2^-6 -> 1 + 2^-6
+    assert oracle.bf16_round(1.0 + 2.0 ** -8) == 1.0
+    assert oracle.bf16_round(1.0 + 3 * 2.0 ** -8) == 1.0 + 2.0 ** -6
+    assert np.isnan(oracle.bf16_round(float("nan")))
+
+
+def test_attn_half_position0_closed_form(oracle, tiny):
+    """At position 0 the softmax has one entry, so attention returns V: the
+    attention half is x + Wo (Wv rmsnorm(x)), checked in float64 with the
+    dequantised weights.  It appends the rotated K and the V to the cache."""
+    cfg, model = tiny
+    dec = oracle.decoder(cfg, model)
+    kc, vc = dec.new_cache()
+    g = np.random.default_rng(4)
+    x = g.normal(0, 1, cfg["hidden"]).astype(np.float32)
+    ly = model["layers"][1]
+    y = dec.attn_half(kc, vc, 1, 0, x, threads=1).astype(np.float64)
+    xd = x.astype(np.float64)
+    h = xd / np.sqrt(np.mean(xd * xd) + cfg["eps"]) * ly["attn_norm"]
+    v = synth.dequant_oil8(ly["wv"], ly["cbv"]).astype(np.float64) @ h
+    heads, kvh, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    att = np.concatenate([v[(hh % kvh) * D:(hh % kvh + 1) * D] for hh in range(heads)])
+    want = xd + synth.dequant_oil8(ly["wo"], ly["cbo"]).astype(np.float64) @ att
+    assert np.linalg.norm(y - want) / np.linalg.norm(want) < 1e-6
+    assert np.allclose(vc[1, :, 0].ravel(), v, rtol=1e-5, atol=1e-6)
+    assert not kc[0].any() and not kc[1, :, 1:].any()      # only layer 1, position 0 written
+
+
+def test_kv_bf16_cache_holds_rounded_values(oracle, tiny):
+    """kv_bf16: every cached K/V value is a bf16 value (low 16 bits zero) and
+    equals the FP32 cache's value rounded; the logits move by that rounding."""
+    cfg, model = tiny
+    d32 = oracle.decoder(cfg, model)
+    d16 = oracle.decoder(dict(cfg, kv_bf16=1), model)
+    k32, v32 = d32.new_cache()
+    k16, v16 = d16.new_cache()
+    ids = synth.decoder_prompts(cfg, 1, 4, config=61)[0]
+    for pos, tok in enumerate(ids):
+        a = d32.step(k32, v32, pos, int(tok), threads=1).astype(np.float64)
+        b = d16.step(k16, v16, pos, int(tok), threads=1).astype(np.float64)
+        assert np.linalg.norm(a - b) / np.linalg.norm(a) < 2e-2
+    assert not (k16.view(np.uint32) & 0xFFFF).any() and not (v16.view(np.uint32) & 0xFFFF).any()
+    # position 0 of layer 0 sees the same input on both sides
+    r = np.array([oracle.bf16_round(float(t)) for t in k32[0, :, 0].ravel()], np.float32)
+    assert np.array_equal(r, k16[0, :, 0].ravel())
+
+
+def test_i2s_gemv_rows_composition(oracle):
+    """i2s_gemv_rows on quantize_per_token(x) is the fused i2s_gemv_f32, and
+    its integer dot product matches an int64 closed form."""
+    g = np.random.default_rng(8)
+    M, K = 37, 256
+    packed = g.integers(0, 256, M * K // 4, dtype=np.uint8)
+    x = g.normal(0, 1, K).astype(np.float32)
+    q, _, inv = oracle.quantize_per_token(x, 1, K)
+    y = oracle.i2s_gemv_rows(packed, 0.5, q.ravel(), float(inv[0]), M, K)
+    assert np.array_equal(y, oracle.i2s_gemv_f32(packed, 0.5, x, M, K, 1).ravel())
+    codes = np.stack([(packed.reshape(M, K // 4) >> (2 * j)) & 3 for j in range(4)], -1).reshape(M, K)
+    t = np.where(codes == 0, -1, np.where(codes == 1, 0, 1)).astype(np.int64)
+    dot = t @ q.ravel().astype(np.int64)
+    want = (dot.astype(np.float32) * np.float32(0.5)) * np.float32(inv[0])
+    assert np.array_equal(y, want)

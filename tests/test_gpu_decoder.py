@@ -8,7 +8,17 @@ activations can round one element differently, so the bar is norm-wise
 relative 1e-4).  Free-running greedy decoding is checked token by token: every
 generated token must be the oracle's argmax for the GPU's own prefix unless the
 oracle's top two logits are within the same tolerance (a near tie).
+
+At the full config-5 size the stack is checked layer by layer through the
+decoder's taps (mth_decoder_set_taps), each stage re-anchored on the GPU's own
+input to it: the attention half and the gate/up projections to FP32 accuracy
+(1e-5), SwiGLU to a few ulps, and the int8 stage exactly: the oracle's
+quantize_per_token of the GPU's FP32 activations must give the GPU's int8
+values and scale bit for bit, and the oracle's I2_S GEMV of those the GPU's
+down projection bit for bit.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -18,7 +28,12 @@ pytestmark = pytest.mark.gpu
 
 SMALL = dict(vocab=1000, hidden=256, layers=2, heads=2, kv_heads=2, head_dim=128, ffn=512, max_seq=24,
              cb_block=128, eps=1e-5, theta=10000.0)
+# hidden 512 / ffn 1024: every projection runs its batched MFMA kernel for
+# batches >= 2 (OIL4 needs K >= 512), gate and up as one launch over 2*ffn rows
+MID = dict(vocab=1000, hidden=512, layers=2, heads=4, kv_heads=4, head_dim=128, ffn=1024, max_seq=20,
+           cb_block=128, eps=1e-5, theta=10000.0)
 TOL = 1e-4
+THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 @pytest.fixture(scope="module")
@@ -33,22 +48,26 @@ def rel(a, b):
     return np.linalg.norm(a - b) / np.linalg.norm(b)
 
 
-def make(cfg, model, batch):
+def make(cfg, model, batch, kv="f32"):
     import decoder
-    d = decoder.Decoder(cfg, max_batch=batch)
+    d = decoder.Decoder(cfg, max_batch=batch, kv_dtype=kv)
     d.load(model)
     return d
 
 
-@pytest.mark.parametrize("graph", [False, True])
-def test_teacher_forced_logits(graph, small, oracle):
+def oracle_cfg(cfg, kv="f32", **kw):
+    return dict(cfg, kv_bf16=int(kv == "bf16"), **kw)
+
+
+@pytest.mark.parametrize("graph,kv", [(False, "f32"), (True, "f32"), (True, "bf16")])
+def test_teacher_forced_logits(graph, kv, small, oracle):
     cfg, model = small
-    print(f"decoder teacher-forced graph={graph}", flush=True)
+    print(f"decoder teacher-forced graph={graph} kv={kv}", flush=True)
     ids = synth.decoder_prompts(cfg, 1, 20, config=61)[0]
     ids[4] = -3                                        # out of range: embedding row 0
-    dec = make(cfg, model, 1)
+    dec = make(cfg, model, 1, kv)
     dec.start(ids)
-    orc = oracle.decoder(cfg, model)
+    orc = oracle.decoder(oracle_cfg(cfg, kv), model)
     kc, vc = orc.new_cache()
     for pos, tok in enumerate(ids):
         dec.step(1, graph=graph)
@@ -120,6 +139,105 @@ def test_step_limits(small):
     assert toks.shape == (2, cfg["max_seq"] + 1)
 
 
+def check_layers(dec, orc, oracle, cfg, model, caches, prompts, pos):
+    """One teacher-forced step of every sequence checked layer by layer
+    through the decoder's taps (module docstring), then the logits from the
+    GPU's own final residual stream.  The K/V the step appended are compared
+    with the oracle's (FP32: 1e-5; bf16: equal but for rare one-ulp rounding
+    flips of values that sit on a rounding boundary), and the oracle's
+    attention then reads the GPU's cache, so that such a flip cannot blur the
+    1e-5 bar of the attention half."""
+    H, F, B = cfg["hidden"], cfg["ffn"], prompts.shape[0]
+    D, kvh = cfg["head_dim"], cfg["kv_heads"]
+    bf16 = dec.kv_dtype == "bf16"
+    taps = dec.taps()
+    logits = dec.logits()
+    kv = [dec.read_kv(l) for l in range(cfg["layers"])]
+    for b in range(B):
+        tok = int(prompts[b, pos])
+        x = model["emb"][tok if 0 <= tok < cfg["vocab"] else 0].astype(np.float32)
+        kc, vc = caches[b]
+        for l, (t, ly) in enumerate(zip(taps, model["layers"])):
+            where = f"step {pos} seq {b} layer {l}"
+            kg, vg = kv[l][0][b, :, :pos + 1], kv[l][1][b, :, :pos + 1]
+            # the oracle's own K/V of this position, on the GPU's earlier ones
+            kc[l, :, :pos], vc[l, :, :pos] = kg[:, :pos], vg[:, :pos]
+            orc.attn_half(kc, vc, l, pos, x, append=True, threads=THREADS)
+            for name, want, got in (("K", kc[l, :, pos], kg[:, pos]), ("V", vc[l, :, pos], vg[:, pos])):
+                if bf16:  # a value close to a rounding boundary (or a cancellation near 0) may round apart
+                    d = np.abs(got.astype(np.float64) - want)
+                    ok = d <= 2.0 ** -7 * np.abs(want) + 1e-5 * np.abs(want).max()
+                    assert ok.all() and (d > 0).mean() < 0.01, (where, name, int((~ok).sum()), int((d > 0).sum()))
+                else:
+                    assert rel(got, want) < 1e-5, (where, name, rel(got, want))
+            # attention over the GPU's cache, this position included
+            kc[l, :, :pos + 1], vc[l, :, :pos + 1] = kg, vg
+            x_attn = orc.attn_half(kc, vc, l, pos, x, append=False, threads=THREADS)
+            d_ref, d_got = x_attn - x, t["x_attn"][b] - x
+            assert rel(d_got, d_ref) < 1e-5, (where, "attention half", rel(d_got, d_ref))
+            h = oracle.rms_norm(t["x_attn"][b], ly["ffn_norm"], cfg["eps"], 1, H)
+            gate = oracle.oil4_gemv_blocked(ly["wgate"], ly["cbgate"], h, F, H, 1, cfg["cb_block"], THREADS)
+            up = oracle.oil4_gemv_blocked(ly["wup"], ly["cbup"], h, F, H, 1, cfg["cb_block"], THREADS)
+            assert rel(t["gate"][b], gate) < 1e-5 and rel(t["up"][b], up) < 1e-5, (where, "gate/up")
+            act = oracle.silu_mul(t["gate"][b], t["up"][b])
+            assert rel(t["act"][b], act) < 1e-6, (where, "swiglu", rel(t["act"][b], act))
+            q, _, inv = oracle.quantize_per_token(t["act"][b], 1, F)
+            assert np.array_equal(q.ravel(), t["aq"][b]), (where, "int8 activations",
+                                                            int((q.ravel() != t["aq"][b]).sum()))
+            assert np.float32(inv[0]) == t["a_inv"][b], (where, "act scale")
+            down = oracle.i2s_gemv_rows(ly["wdown"], float(ly["down_scale"]), t["aq"][b], t["a_inv"][b], H, F,
+                                        THREADS)
+            assert np.array_equal(down, t["down"][b]), (where, "down projection")
+            x = (t["x_attn"][b] + t["down"][b]).astype(np.float32)
+        h = oracle.rms_norm(x, model["final_norm"], cfg["eps"], 1, H)
+        want = oracle.oil8_gemv(model["lm_idx"], model["lm_cb"], h, cfg["vocab"], H, 1, threads=THREADS)
+        assert rel(logits[b], want) < 1e-5, (pos, b, "logits", rel(logits[b], want))
+
+
+@pytest.fixture(scope="module")
+def mid():
+    cfg = synth.decoder_config(**MID)
+    return cfg, synth.decoder_model(cfg, config=65, random_gamma=True)
+
+
+@pytest.mark.parametrize("batch,kv", [(2, "f32"), (5, "bf16"), (16, "f32"), (16, "bf16")])
+def test_mid_batched_kernels_per_layer(batch, kv, mid, oracle):
+    """Batches of 2..16 at hidden 512: the batched OIL8 / OIL4 (fused gate+up
+    over 2*ffn rows) / I2_S kernels and their K-slice reductions, every layer
+    of every sequence against the oracle through the taps, six teacher-forced
+    steps (the KV cache grows to six positions)."""
+    cfg, model = mid
+    print(f"decoder mid batch={batch} kv={kv}", flush=True)
+    steps = 6
+    prompts = synth.decoder_prompts(cfg, batch, steps, config=66)
+    dec = make(cfg, model, batch, kv)
+    dec.start(prompts)
+    dec.enable_taps()
+    orc = oracle.decoder(oracle_cfg(cfg, kv), model)
+    caches = [orc.new_cache() for _ in range(batch)]
+    for pos in range(steps):
+        dec.step(1)
+        check_layers(dec, orc, oracle, cfg, model, caches, prompts, pos)
+    dec.close()
+
+
+def test_mid_graph_batch_matches_taps_run(mid):
+    """The graph-replayed batch-16 step gives the same logits, bit for bit,
+    as the eager step with taps on (the taps only add copies)."""
+    cfg, model = mid
+    prompts = synth.decoder_prompts(cfg, 16, 4, config=69)
+    a, b = make(cfg, model, 16), make(cfg, model, 16)
+    a.start(prompts)
+    b.start(prompts)
+    b.enable_taps()
+    for _ in range(4):
+        a.step(1, graph=True)
+        b.step(1)
+        assert np.array_equal(a.logits(), b.logits())
+    a.close()
+    b.close()
+
+
 @pytest.fixture(scope="module")
 def config5():
     cfg = synth.decoder_config()
@@ -127,46 +245,47 @@ def config5():
     return cfg, synth.decoder_model(cfg)
 
 
-def run_teacher_forced(cfg, model, oracle, prompt, steps):
-    dec = make(cfg, model, 1)
-    dec.start(prompt)
-    orc = oracle.decoder(cfg, model)
-    kc, vc = orc.new_cache()
-    errs = []
-    for pos in range(steps):
-        print(f"decoder config 5: step {pos}", flush=True)
-        dec.step(1)
-        got = dec.logits()[0]
-        want = orc.step(kc, vc, pos, int(prompt[pos]), threads=16)
-        errs.append(rel(got, want))
-    dec.close()
-    return errs
-
-
-def test_config5_full_size_exact_path(config5, oracle):
+def test_config5_b16_exact_path(config5, oracle):
     """The BASELINE config-5 stack (32 layers, hidden 4096, ffn 11008, vocab
-    32000) with every ternary down weight 0: the FFN output is exactly 0 on
-    both sides, so no int8 rounding boundary is involved, and the attention
-    half of every block at full size (norms, OIL8 Q/K/V/O, RoPE, attention,
-    residuals) and the OIL8 lm_head over 32000 rows must agree to FP32
-    tolerance.  The FFN half is held to the same bar at small width
-    (test_teacher_forced_logits) and its kernels at full size in
-    test_gpu_gemv.py / test_gpu_dense.py."""
+    32000) at batch 16 with every ternary down weight 0: the FFN output is
+    exactly 0 on both sides, so no int8 rounding boundary is involved; the
+    attention half of every block (norms, OIL8 Q/K/V/O on the batched MFMA
+    kernel, RoPE, attention, residuals) and the OIL8 lm_head over 32000 rows
+    must agree with the oracle to FP32 tolerance, for every sequence, over
+    two teacher-forced steps."""
     cfg, model = config5
+    B, steps = 16, 2
     zero = dict(model, layers=[dict(ly, wdown=np.full_like(ly["wdown"], 0x55)) for ly in model["layers"]])
-    prompt = synth.decoder_prompts(cfg, 1, 3)[0]
-    errs = run_teacher_forced(cfg, zero, oracle, prompt, 3)
-    assert max(errs) < TOL, errs
+    prompts = synth.decoder_prompts(cfg, B, steps, config=67)
+    dec = make(cfg, zero, B)
+    dec.start(prompts)
+    orc = oracle.decoder(dict(cfg, max_seq=steps), zero)
+    caches = [orc.new_cache() for _ in range(B)]
+    for pos in range(steps):
+        print(f"decoder config 5 b=16 exact path: step {pos}", flush=True)
+        dec.step(1)
+        got = dec.logits()
+        errs = [rel(got[b], orc.step(*caches[b], pos, int(prompts[b, pos]), threads=THREADS)) for b in range(B)]
+        assert max(errs) < TOL, (pos, errs)
+    dec.close()
 
 
-def test_config5_full_size_int8_ffn(config5, oracle):
-    """The same stack with its ternary down projections.  Per token the FFN
-    activations are quantised to int8 (11008 values per layer); the device's
-    FP32 activations differ from the oracle's in the last bits, which moves a
-    few values across a rounding boundary in each of the 32 layers, each such
-    step a discrete change of about 1e-3 of the residual.  Through 32 layers
-    the logits stay within a few percent (measured 2.2e-2 at step 0)."""
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_config5_b16_per_layer(kv, config5, oracle):
+    """Config 5 at batch 16 with its ternary down projections, two
+    teacher-forced steps, every layer of every sequence checked through the
+    taps (module docstring).  The int8 stage is compared bit for bit, so a
+    wiring error in the 11008-wide FFN cannot hide in a loose logits bar."""
     cfg, model = config5
-    prompt = synth.decoder_prompts(cfg, 1, 2)[0]
-    errs = run_teacher_forced(cfg, model, oracle, prompt, 2)
-    assert max(errs) < 0.05, errs
+    B, steps = 16, 2
+    prompts = synth.decoder_prompts(cfg, B, steps, config=68)
+    dec = make(cfg, model, B, kv)
+    dec.start(prompts)
+    dec.enable_taps()
+    orc = oracle.decoder(oracle_cfg(cfg, kv, max_seq=steps), model)
+    caches = [orc.new_cache() for _ in range(B)]
+    for pos in range(steps):
+        print(f"decoder config 5 b=16 per-layer kv={kv}: step {pos}", flush=True)
+        dec.step(1)
+        check_layers(dec, orc, oracle, cfg, model, caches, prompts, pos)
+    dec.close()
