@@ -101,6 +101,21 @@ int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_b
                   const float* x, float* y, int64_t M, int64_t K, int64_t batch,
                   mth_stream_t stream);
 
+/* mth_oil4_gemv for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference (its CPU kernels need no scratch).  Same
+ * arguments, results and kernels as mth_oil4_gemv; the batched path's K-slice
+ * partial sums (16 tokens x M rows x K/1024 slices of FP32 for K >= 2048)
+ * live in a fixed 8 MiB device array per GPU instead of the workspace, and
+ * the call never allocates.  Shapes whose partial sums exceed 8 MiB (e.g.
+ * K = 4096 with M > 32768) fail with MTH_EINVAL.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (several streams,
+ * threads or concurrently replayed graphs) race; stream-ordered calls do not.
+ * Nothing in the array needs clearing: every call writes what it reads. */
+int mth_oil4_gemv_noalloc(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_block,
+                          const float* x, float* y, int64_t M, int64_t K, int64_t batch,
+                          mth_stream_t stream);
+
 /* Prefill GEMM (no reference counterpart beyond oil4_gemm's per-token
  * definition): C[m*N + n] = bf16( sum_k A[m*K + k] * W[n][k] ), A bf16
  * [M][K] row-major, W OIL4 [N][K] with per-block codebooks as in

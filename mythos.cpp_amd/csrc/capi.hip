@@ -107,6 +107,35 @@ int workspace_fail(const char* what, hipError_t e, size_t need) {
         if (!(cond)) return fail(MTH_EINVAL, __VA_ARGS__); \
     } while (0)
 
+// Scratch of mth_oil4_gemv_noalloc: the K-slice partial sums of the batched
+// OIL4 GEMV, in a fixed device array instead of the allocated workspace.  The
+// array's name is a host-side stand-in; the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the calling thread's current device's scratch.
+hipError_t scratch_address(void** out) {
+    *out = nullptr;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
 }  // namespace
 
 namespace mth {
@@ -187,6 +216,35 @@ int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_b
     }
     return check_launch(mth::launch_oil4_gemv(packed, codebooks, cb_block, x, y, M, K, batch, S(stream)),
                         "mth_oil4_gemv");
+}
+
+int mth_oil4_gemv_noalloc(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_block, const float* x,
+                          float* y, int64_t M, int64_t K, int64_t batch, mth_stream_t stream) {
+    REQUIRE(packed && codebooks && x && y, "mth_oil4_gemv_noalloc: null pointer");
+    REQUIRE(M > 0 && K > 0 && batch > 0 && M < kMaxDim && K < kMaxDim && batch <= 65536,
+            "mth_oil4_gemv_noalloc: bad sizes M=%lld K=%lld batch=%lld", (long long)M, (long long)K,
+            (long long)batch);
+    REQUIRE(K % 2 == 0, "mth_oil4_gemv_noalloc: K=%lld must be even (two nibbles per byte)", (long long)K);
+    REQUIRE(cb_block >= 0, "mth_oil4_gemv_noalloc: cb_block=%lld < 0", (long long)cb_block);
+    REQUIRE(cb_block == 0 || K % cb_block == 0, "mth_oil4_gemv_noalloc: K=%lld not a multiple of cb_block=%lld",
+            (long long)K, (long long)cb_block);
+    const bool aligned = (((uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)x) & 15u) == 0;
+    if (aligned && mth::oil4_bt_supported(M, K, cb_block, batch)) {
+        const size_t need = mth::oil4_bt_partial_bytes(M, K);
+        REQUIRE(need <= kNoAllocScratchBytes,
+                "mth_oil4_gemv_noalloc: M=%lld K=%lld batch=%lld needs %zu bytes of scratch, more than the %zu "
+                "this entry point holds; use mth_oil4_gemv",
+                (long long)M, (long long)K, (long long)batch, need, kNoAllocScratchBytes);
+        void* partial = nullptr;
+        const hipError_t e = scratch_address(&partial);
+        if (e != hipSuccess)
+            return fail(MTH_EDEVICE, "mth_oil4_gemv_noalloc: scratch address: %s", hipGetErrorString(e));
+        return check_launch(mth::launch_oil4_gemv_bt(packed, codebooks, cb_block, x, y, M, K, batch, (float*)partial,
+                                                     S(stream)),
+                            "mth_oil4_gemv_noalloc");
+    }
+    return check_launch(mth::launch_oil4_gemv(packed, codebooks, cb_block, x, y, M, K, batch, S(stream)),
+                        "mth_oil4_gemv_noalloc");
 }
 
 int mth_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* packed, const uint16_t* codebooks,

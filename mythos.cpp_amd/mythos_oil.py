@@ -21,7 +21,7 @@ HOST_LIB_PATH = os.path.join(_HERE, "libmythos_host.so")
 EXPORTS = (
     "mth_last_error", "mth_version", "mth_workspace_reserve",
     "mth_oil8_gemm", "mth_oil8_gemv",
-    "mth_oil4_gemm", "mth_oil4_gemv", "mth_oil4_gemm_prefill",
+    "mth_oil4_gemm", "mth_oil4_gemv", "mth_oil4_gemv_noalloc", "mth_oil4_gemm_prefill",
     "mth_quantize_per_token", "mth_dequantize_per_tensor",
     "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
     "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
@@ -63,6 +63,7 @@ _SIG = {
     "mth_oil8_gemv": [VP, VP, VP, VP, I64, I64, I64, VP],
     "mth_oil4_gemm": [VP, VP, VP, VP, I64, I64, I64, VP],
     "mth_oil4_gemv": [VP, VP, I64, VP, VP, I64, I64, I64, VP],
+    "mth_oil4_gemv_noalloc": [VP, VP, I64, VP, VP, I64, I64, I64, VP],
     "mth_oil4_gemm_prefill": [VP, VP, VP, I64, VP, I64, I64, I64, VP],
     "mth_quantize_per_token": [VP, VP, VP, VP, I64, I64, VP],
     "mth_dequantize_per_tensor": [VP, VP, I64, F32, VP],
@@ -179,6 +180,16 @@ def oil4_gemv(packed, codebooks, cb_block, x, y, M, K, batch=1, stream=None):
     _check(_lib.mth_oil4_gemv(_ptr(packed, t.uint8, M * K // 2, "packed"), _ptr(codebooks, t.int16, ncb, "codebooks"),
                               cb_block, _ptr(x, t.float32, batch * K, "x"), _ptr(y, t.float32, batch * M, "y"),
                               M, K, batch, _stream(stream)))
+
+
+def oil4_gemv_noalloc(packed, codebooks, cb_block, x, y, M, K, batch=1, stream=None):
+    """oil4_gemv whose scratch is a fixed per-GPU device array (no allocation)."""
+    t = _torch()
+    ncb = M * (K // cb_block) * 16 if cb_block else 16
+    _check(_lib.mth_oil4_gemv_noalloc(_ptr(packed, t.uint8, M * K // 2, "packed"),
+                                      _ptr(codebooks, t.int16, ncb, "codebooks"), cb_block,
+                                      _ptr(x, t.float32, batch * K, "x"), _ptr(y, t.float32, batch * M, "y"),
+                                      M, K, batch, _stream(stream)))
 
 
 def oil4_gemm_prefill(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K, stream=None):
