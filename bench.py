@@ -35,6 +35,7 @@ sys.path.insert(0, os.path.join(ROOT, "mythos.cpp_amd"))
 METRIC = "HBM GB/s (% peak) for OIL8/OIL4/I2_S GEMV 4096^2 b=1; 32-layer decode tok/s"
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0
+I8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 1 << 30
 
 
@@ -142,6 +143,23 @@ def bench_prefill(mth, dev, M, N, K, steps, warmup, block=128):
                         max(8, steps // 100), max(2, warmup // 100))
     flop = 2.0 * M * N * K
     return dict(sec=sec, steps=n, flop=flop, copies=n_cp)
+
+
+def bench_ternary_gemm(mth, dev, M, N, K, steps, warmup):
+    """Ternary prefill GEMM (i2s_gemm_vnni, int8 MFMA): M weight rows x N
+    tokens x K; weights rotated over 4 copies (the 5.6 MB of activations and
+    11 MB of weights fit the 256 MB MALL either way: this is compute-bound)."""
+    import torch
+    import synth
+    w = synth.stream(6).ternary(M, K)
+    a = np.random.default_rng(6).integers(-127, 128, (N, K), dtype=np.int8)
+    a_d = dev_copy(a, dev)
+    o = torch.empty(M * N, dtype=torch.float32, device=dev)
+    n_cp = 4
+    ws = [dev_copy(w, dev) for _ in range(n_cp)]
+    sec, n = time_graph(lambda i: mth.i2s_gemm_vnni(ws[i], a_d, o, M, N, K), n_cp, max(8, steps // 100),
+                        max(2, warmup // 100))
+    return dict(sec=sec, steps=n, ops=2.0 * M * N * K, copies=n_cp)
 
 
 def bench_decode(dev, batches=(1, 16)):
@@ -252,7 +270,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,i2s,prefill,decode (default all)")
+    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,i2s,prefill,ternary_gemm,decode (default all)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -301,6 +319,13 @@ def main():
         extra["oil4_prefill_gemm_512x14336x4096"] = dict(us=r["sec"] * 1e6, TFLOPs=tf, frac=tf / F16_PEAK_TFLOPS,
                                                          steps=r["steps"])
         log(f"prefill: {r['sec']*1e6:.1f} us/launch, {tf:.0f} TFLOP/s ({tf/F16_PEAK_TFLOPS:.1%})")
+
+    if want("ternary_gemm"):
+        r = bench_ternary_gemm(mth, dev, 4096, 512, 11008, args.steps, args.warmup)
+        tops = r["ops"] / r["sec"] / 1e12
+        extra["i2s_gemm_vnni_4096x512x11008"] = dict(us=r["sec"] * 1e6, TOPs=tops, frac=tops / I8_PEAK_TOPS,
+                                                     steps=r["steps"])
+        log(f"ternary gemm: {r['sec']*1e6:.1f} us/launch, {tops:.0f} TOP/s ({tops/I8_PEAK_TOPS:.1%} of int8 MFMA)")
 
     if want("decode"):
         extra.update(bench_decode(dev))

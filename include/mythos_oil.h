@@ -9,7 +9,9 @@
  * never accumulated.
  *
  * Workspace.  The batched GEMVs (mth_oil8_gemv, mth_oil4_gemv, mth_i2s_gemv
- * with batch >= 2) and mth_argmax keep partial results in a device workspace
+ * with batch >= 2), mth_argmax, mth_oil4_gemm_prefill (an FP16 copy of A,
+ * M*K*2 bytes, for K % 256 == 0) and mth_i2s_gemm_vnni (permuted activations,
+ * for its MFMA shapes) keep intermediate data in a device workspace
  * the library owns, one per (device, stream).  The first call that needs more
  * than the stream's workspace holds allocates a larger one (hipMalloc, at
  * least double the old size) and retires the old block WITHOUT freeing it, so
@@ -161,7 +163,10 @@ int mth_i2s_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int6
                  mth_stream_t stream);
 
 /* oil::kernel::i2s_gemm_vnni (include/oil/kernel.h:63-65, body at
- * src/kernel_i2s.cpp:201-235): int8 activations, exact integer dot as FP32. */
+ * src/kernel_i2s.cpp:201-235): int8 activations, exact integer dot as FP32.
+ * M >= 64, N >= 64, K % 256 == 0 with 16-byte aligned w / act run on int8
+ * MFMA (bit-exact) and use N*K + 4*N bytes of workspace; other shapes run one
+ * wave per output. */
 int mth_i2s_gemm_vnni(const uint8_t* w, const int8_t* act, float* out, int64_t M, int64_t N, int64_t K,
                       mth_stream_t stream);
 

@@ -256,7 +256,16 @@ int mth_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* packed, const u
     REQUIRE(K % 2 == 0, "mth_oil4_gemm_prefill: K=%lld must be even", (long long)K);
     REQUIRE(cb_block > 0 && K % cb_block == 0, "mth_oil4_gemm_prefill: K=%lld not a multiple of cb_block=%lld",
             (long long)K, (long long)cb_block);
-    const bool aligned = (((uintptr_t)a_bf16 | (uintptr_t)packed | (uintptr_t)codebooks) & 15u) == 0;
+    const bool aligned = (((uintptr_t)a_bf16 | (uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)c_bf16) & 15u) == 0;
+    const size_t need = aligned ? mth::oil4_prefill_workspace_bytes(M, N, K, cb_block) : 0;
+    if (need) {
+        void* a16 = nullptr;
+        const hipError_t e = workspace(S(stream), need, &a16);
+        if (e != hipSuccess) return workspace_fail("mth_oil4_gemm_prefill", e, need);
+        return check_launch(mth::launch_oil4_gemm_prefill_a16(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K,
+                                                             (uint16_t*)a16, S(stream)),
+                            "mth_oil4_gemm_prefill");
+    }
     if (!aligned || !mth::oil4_gemm_prefill_supported(M, N, K, cb_block))
         return fail(MTH_EUNSUPPORTED,
                     "mth_oil4_gemm_prefill: M=%lld N=%lld K=%lld cb_block=%lld not supported "
@@ -330,7 +339,14 @@ int mth_i2s_gemm_vnni(const uint8_t* w, const int8_t* act, float* out, int64_t M
                       mth_stream_t stream) {
     REQUIRE(w && act && out, "mth_i2s_gemm_vnni: null pointer");
     REQUIRE(M > 0 && N > 0 && K > 0 && M * N < kMaxDim && K < (1ll << 24), "mth_i2s_gemm_vnni: bad sizes");
-    return check_launch(mth::launch_i2s_gemm_vnni(w, act, out, M, N, K, S(stream)), "mth_i2s_gemm_vnni");
+    const bool aligned = (((uintptr_t)w | (uintptr_t)act) & 15u) == 0;
+    const size_t need = aligned ? mth::i2s_gemm_workspace_bytes(M, N, K) : 0;
+    void* ws = nullptr;
+    if (need) {
+        const hipError_t e = workspace(S(stream), need, &ws);
+        if (e != hipSuccess) return workspace_fail("mth_i2s_gemm_vnni", e, need);
+    }
+    return check_launch(mth::launch_i2s_gemm_vnni(w, act, out, M, N, K, ws, S(stream)), "mth_i2s_gemm_vnni");
 }
 
 int mth_tl1_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int64_t N, int64_t K,

@@ -77,15 +77,15 @@ __device__ __forceinline__ float transposed_sum(float (&v)[R], int lane) {
 // ===================================================================
 // OIL8
 // ===================================================================
-// The codebook and x are fetched, and the table staged, before the weight
-// stream is released: a load issued after other waves' weight loads waits
-// behind them in the CU's in-order memory pipeline (~1.5-3 us at this size),
-// while the stream itself only starts ~0.5 us later this way.  The single
-// unreplicated 1 KiB table costs ~1.9x a conflict-free gather (measured on
-// gfx950: 3.6 vs 1.9 cycles per wave64 ds_read_b32) but needs one store per
-// thread to fill, where a replicated table's fill would sit on this critical
-// path.  idx and x are not __restrict__, so the compiler keeps their loads in
-// program order around the barrier.
+// Issue order: x and the thread's codebook entry first (a load issued behind
+// other waves' weight loads waits for them: the CU returns loads in order),
+// then the R rows' index bytes, and only then the table store and the
+// barrier, so the weight stream is in flight while the table is staged
+// (measured ~1 us earlier than staging first).  The single unreplicated 1 KiB
+// table costs ~1.9x a conflict-free gather (gfx950: 3.6 vs 1.9 cycles per
+// wave64 ds_read_b32) but needs one store per thread to fill; a 64-copy
+// conflict-free table measured no faster (its fill costs what the gathers
+// save).
 template <int R>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void oil8_gemv_k(const uint8_t* idx, const float* __restrict__ cb, const float* x, float* __restrict__ y, int M,
@@ -101,11 +101,14 @@ void oil8_gemv_k(const uint8_t* idx, const float* __restrict__ cb, const float* 
     float4 xq[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) xq[q] = ldf4(x + kl + 4 * q);
-    tab[tid] = cb[tid];
-    __syncthreads();
+    const float cbv = cb[tid];
+    __builtin_amdgcn_sched_barrier(0);
     uint4 w[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) w[r] = ld_stream(idx + (int64_t)min(m0 + r, M - 1) * K + kl);
+    __builtin_amdgcn_sched_barrier(0);
+    tab[tid] = cbv;
+    __syncthreads();
 
     for (int t = 0; t < batch; ++t) {
         float xr[16];

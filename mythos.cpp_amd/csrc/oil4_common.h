@@ -57,17 +57,35 @@ __device__ __forceinline__ CbPlanes cb_planes(const uint4& a, const uint4& b) {
     return p;
 }
 
+// (a & m) | (b & ~m) in one v_bfi_b32: the compiler otherwise spends an AND
+// and an OR on the pick selectors below (VOP3 takes no literal on gfx9, so it
+// cannot fold both constants into one v_and_or_b32).
+__device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
+    return r;
+}
+
+// Pick-selector base: byte j holds j.  Kept in a VGPR (loop-invariant) so
+// that bit_select reads only one scalar operand.
+__device__ __forceinline__ uint32_t pick_base() {
+    uint32_t c = 0x03020100u;
+    asm("" : "+v"(c));
+    return c;
+}
+
 // Weights 0..7 of d (weight v = low nibble of byte v/2 for even v, high for
 // odd v) -> FP16 pairs {0,2}, {4,6}, {1,3}, {5,7}.  The low 3 bits of each
 // nibble select within entries 0-7 and 8-15, a second v_perm picks by bit 3,
-// a third interleaves lo and hi bytes into FP16 pairs.
+// a third interleaves lo and hi bytes into FP16 pairs (23 VALU per 8 weights).
 __device__ __forceinline__ half8 lookup8(uint32_t d, const CbPlanes& p) {
     const uint32_t sE = d & 0x07070707u;
     const uint32_t dO = d >> 4;
     const uint32_t sO = dO & 0x07070707u;
     // byte j of the pick selector: j (entries 0-7) or 4 + j (entries 8-15)
-    const uint32_t pE = ((d >> 1) & 0x04040404u) | 0x03020100u;
-    const uint32_t pO = ((dO >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t base = pick_base();
+    const uint32_t pE = bit_select(0x04040404u, d >> 1, base);
+    const uint32_t pO = bit_select(0x04040404u, d >> 5, base);
     const uint32_t loE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sE),
                                                __builtin_amdgcn_perm(p.l[1], p.l[0], sE), pE);
     const uint32_t hiE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sE),
@@ -88,8 +106,9 @@ __device__ __forceinline__ half8 lookup8_natural(uint32_t d, const CbPlanes& p) 
     const uint32_t sE = d & 0x07070707u;
     const uint32_t dO = d >> 4;
     const uint32_t sO = dO & 0x07070707u;
-    const uint32_t pE = ((d >> 1) & 0x04040404u) | 0x03020100u;
-    const uint32_t pO = ((dO >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t base = pick_base();
+    const uint32_t pE = bit_select(0x04040404u, d >> 1, base);
+    const uint32_t pO = bit_select(0x04040404u, d >> 5, base);
     const uint32_t loE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.l[3], p.l[2], sE),
                                                __builtin_amdgcn_perm(p.l[1], p.l[0], sE), pE);
     const uint32_t hiE = __builtin_amdgcn_perm(__builtin_amdgcn_perm(p.h[3], p.h[2], sE),
@@ -184,9 +203,10 @@ struct Oil4TileLoads {
         }
     }
 
-    // Byte planes of the codebook block behind this lane's columns of phase p
-    // (stage: the wave's 2 KB codebook stage).
-    __device__ __forceinline__ CbPlanes planes(int p, uint8_t* stage, int lane) {
+    // The 16 FP16 entries (entries 2i, 2i+1 in dword i of a, then b) of the
+    // codebook block behind this lane's columns of phase p (stage: the wave's
+    // 2 KB codebook stage).
+    __device__ __forceinline__ void block(int p, uint8_t* stage, int lane, uint4& a, uint4& b) {
         const int j = lane & 15, q = lane >> 4;
         if (p % 2 == 0) {
             *(uint4*)(stage + oil4_stage_off(lane >> 3, lane & 7)) = c0[p / 2];
@@ -194,10 +214,16 @@ struct Oil4TileLoads {
             wave_lds_order();
         }
         const int bi = 2 * (p & 1) + (q >> 1);  // block of this lane's columns
-        const CbPlanes pl = cb_planes(*(const uint4*)(stage + oil4_stage_off(j, 2 * bi)),
-                                      *(const uint4*)(stage + oil4_stage_off(j, 2 * bi + 1)));
+        a = *(const uint4*)(stage + oil4_stage_off(j, 2 * bi));
+        b = *(const uint4*)(stage + oil4_stage_off(j, 2 * bi + 1));
         wave_lds_order();
-        return pl;
+    }
+
+    // Byte planes of that block (lookup8).
+    __device__ __forceinline__ CbPlanes planes(int p, uint8_t* stage, int lane) {
+        uint4 a, b;
+        block(p, stage, lane, a, b);
+        return cb_planes(a, b);
     }
 
     // Rows 0-7 / 8-15 -> lane (j, q): a = piece 2q, b = piece 2q+1 of row j.

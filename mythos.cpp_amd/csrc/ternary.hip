@@ -210,6 +210,138 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
     }
 }
 
+// ---------------------------------------------------------------------------
+// I2_S GEMV, batch 1 (i2s_gemv_rows): R rows per wave, 4R per workgroup.
+// ---------------------------------------------------------------------------
+// A 4 MB GEMV is latency-bound, so everything is requested up front: the
+// activations first, then every weight segment of the workgroup's rows (NSEG
+// 128-bit loads per row and lane), and only then the absmax reduction and the
+// quantisation run while the weights stream in.  Lane l owns 16-byte segments
+// l + 64 s of every row (64 weights each) and its 64 activations per segment
+// (byte-transposed from LDS, as in i2s_gemv_fast); the R row sums are reduced
+// across the wave by a transposed butterfly.  K % 64 == 0, K <= 4096 NSEG,
+// K <= 1024 XQ (FUSED).  Dynamic LDS: K bytes.
+template <int R>
+__device__ __forceinline__ int transposed_sum_i(int (&v)[R], int lane) {
+#pragma unroll
+    for (int n = R, mask = 32; n > 1; n >>= 1, mask >>= 1) {
+        const bool hi = (lane & mask) != 0;
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const int send = hi ? v[j] : v[j + n / 2];
+            const int keep = hi ? v[j + n / 2] : v[j];
+            v[j] = keep + __shfl_xor(send, mask, MTH_WAVE);
+        }
+    }
+    int s = v[0];
+#pragma unroll
+    for (int mask = 32 / R; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask, MTH_WAVE);
+    return s;
+}
+
+template <int R, int NSEG, int XQ, bool FUSED>
+__global__ __launch_bounds__(kWG) void i2s_gemv_rows(const uint8_t* packed, float w_scale,
+                                                     const float* __restrict__ x, const int8_t* act,
+                                                     const float* __restrict__ act_scale, float* __restrict__ y,
+                                                     int M, int K) {
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    int8_t* q = (int8_t*)lds_raw;
+    __shared__ float red[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int bpr = K >> 2, nseg = bpr >> 4;
+    const int row0 = (blockIdx.x * kWaves + wave) * R;
+
+    float4 xr[XQ];
+    if (FUSED) {
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int k = (tid + j * kWG) * 4;
+            xr[j] = ldf4(x + (k < K ? k : 0));
+        }
+    }
+    uint4 w[R][NSEG];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int s = 0; s < NSEG; ++s)
+            w[r][s] = ld_stream(packed + (int64_t)min(row0 + r, M - 1) * bpr + (int64_t)min(lane + 64 * s, nseg - 1) * 16);
+
+    float inv;
+    if (FUSED) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int k = (tid + j * kWG) * 4;
+            if (k >= K) xr[j] = make_float4(0, 0, 0, 0);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(xr[j].x), fabsf(xr[j].y)), fmaxf(fabsf(xr[j].z), fabsf(xr[j].w))));
+        }
+        m = wave_max(m);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        if (mx < 1e-10f) mx = 1e-10f;
+        const float sc = __fdiv_rn(127.0f, mx);
+        inv = __fdiv_rn(mx, 127.0f);
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int k = (tid + j * kWG) * 4;
+            if (k < K) {
+                const uint32_t b0 = (uint32_t)quant_i8(xr[j].x, sc) & 0xffu, b1 = (uint32_t)quant_i8(xr[j].y, sc) & 0xffu;
+                const uint32_t b2 = (uint32_t)quant_i8(xr[j].z, sc) & 0xffu, b3 = (uint32_t)quant_i8(xr[j].w, sc) & 0xffu;
+                *(uint32_t*)(q + k) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+    } else {
+        inv = act_scale[0];
+        for (int k = tid * 16; k < K; k += kWG * 16) *(uint4*)(q + k) = ld16(act + k);
+    }
+    __syncthreads();
+
+    uint32_t A[NSEG][4][4];
+    int asum = 0;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        const int seg = lane + 64 * s;
+        if (seg < nseg) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint4 n = *(const uint4*)(q + seg * 64 + 16 * d);
+                const uint32_t N[4] = {n.x, n.y, n.z, n.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    A[s][d][j] = ((N[0] >> (8 * j)) & 0xffu) | (((N[1] >> (8 * j)) & 0xffu) << 8) |
+                                 (((N[2] >> (8 * j)) & 0xffu) << 16) | (((N[3] >> (8 * j)) & 0xffu) << 24);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asum = dot4(N[j], 0x01010101u, asum);
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) A[s][d][j] = 0;
+        }
+    }
+    int acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int a = 0;
+#pragma unroll
+        for (int s = 0; s < NSEG; ++s) {
+            const bool sv = lane + 64 * s < nseg;
+            const uint32_t pad = 0x55555555u;  // t = 0 codes for segments past the row
+            a = tdot16(sv ? w[r][s].x : pad, A[s][0], a);
+            a = tdot16(sv ? w[r][s].y : pad, A[s][1], a);
+            a = tdot16(sv ? w[r][s].z : pad, A[s][2], a);
+            a = tdot16(sv ? w[r][s].w : pad, A[s][3], a);
+        }
+        acc[r] = a - asum;
+    }
+    const int tot = transposed_sum_i<R>(acc, lane);
+    constexpr int Lr = MTH_WAVE / R;
+    const int row = row0 + lane / Lr;
+    if ((lane % Lr) == 0 && row < M) y[row] = __fmul_rn(__fmul_rn((float)tot, w_scale), inv);
+}
+
 // Generic I2_S GEMV: one wave per (row, token); any K % 4 == 0.
 template <bool FUSED>
 __global__ __launch_bounds__(kWG) void i2s_gemv_generic(
@@ -472,6 +604,153 @@ inline int ib_slices(int64_t M, int64_t K) {
     return S;
 }
 
+// ---------------------------------------------------------------------------
+// Ternary GEMM on int8 MFMA: i2s_gemm_vnni for many tokens (prefill)
+// ---------------------------------------------------------------------------
+//   out[m*N + n] = (float) sum_k t(m, k) * a[n][k]      (src/kernel_i2s.cpp:201-235)
+// exact in int32.  v_mfma_i32_16x16x64_i8, A = weights (u-codes u = t + 1 in
+// {0, 1, 2}), B = activations, D - sum_k a[n][k] = sum t a.  The MFMA's k
+// order is permuted alike on both operands: in a 16-column group whose codes
+// are the dword q (column 4b + f in field f of byte b), plane f of the u-codes,
+// (ucode(q) >> 2f) & 0x03030303, holds column 4b + f at byte b -- two VALU
+// per four weights.  The activations are permuted to the same order once per
+// call (i2s_act_perm: a 4x4 byte transpose of every 16-byte group), which also
+// writes each token's sum over k.
+//   * workgroup tile 64 weight rows x 128 tokens, K steps of 256, one per CU
+//     at config size (4096 x 512); XCD-aware: the workgroups of a token tile
+//     share two XCDs, whose L2 then holds those tokens' activations;
+//   * weights: 4 KB of codes per step, staged 3 steps ahead in registers,
+//     decoded once per workgroup into a double-buffered LDS tile (XOR-swizzled
+//     16-byte slots, conflict-free fragment reads);
+//   * activations: every wave reads the B fragments of its 32 tokens straight
+//     from L2 into registers, one step ahead;
+//   * wave w: all 64 rows x tokens 32w..32w+31 (4 x 2 accumulator tiles).
+constexpr int TGM = 64, TGN = 128, TGK = 256;
+
+// 16-byte groups of a [N][K] int8 -> permuted order; sums[n] = sum_k a[n][k].
+// One workgroup per token.
+__global__ __launch_bounds__(kWG) void i2s_act_perm(const int8_t* __restrict__ a, int8_t* __restrict__ ap,
+                                                    int* __restrict__ sums, int K) {
+    __shared__ int red[kWaves];
+    const int64_t row = blockIdx.x;
+    const int8_t* src = a + row * K;
+    int8_t* dst = ap + row * K;
+    int sum = 0;
+    for (int g = threadIdx.x; g < K / 16; g += kWG) {
+        const uint4 v = ld16(src + 16 * g);
+        uint4 o;
+        o.x = byte_t4x4(v.x, v.y, v.z, v.w, 0);
+        o.y = byte_t4x4(v.x, v.y, v.z, v.w, 1);
+        o.z = byte_t4x4(v.x, v.y, v.z, v.w, 2);
+        o.w = byte_t4x4(v.x, v.y, v.z, v.w, 3);
+        *(uint4*)(dst + 16 * g) = o;
+        sum = dot4(v.x, 0x01010101u, dot4(v.y, 0x01010101u, dot4(v.z, 0x01010101u, dot4(v.w, 0x01010101u, sum))));
+    }
+    sum = group_sum_i<64>(sum);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) sums[row] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// LDS byte offset of 16-byte slot q (0..15) of weight row r in a step tile
+__device__ __forceinline__ int tg_off(int r, int q) { return r * TGK + 16 * (q ^ (r & 7)); }
+
+__global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int8_t* ap, const int* __restrict__ sums,
+                                                     float* __restrict__ out, int M, int N, int K) {
+    __shared__ __align__(16) uint8_t wt[2][TGM * TGK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tm = (M + TGM - 1) / TGM, tn = (N + TGN - 1) / TGN;
+    int mt, nt;
+    {
+        const int id = blockIdx.x, total = tm * tn;
+        if (total % 8 == 0 && 8 % tn == 0) {  // 8 / tn XCDs per token tile
+            const int grp = 8 / tn, xcd = id % 8;
+            nt = xcd / grp;
+            mt = (id / 8) * grp + xcd % grp;
+        } else {
+            mt = id / tn;
+            nt = id % tn;
+        }
+    }
+    const int m0 = mt * TGM, n0 = nt * TGN;
+    const int bpr = K / 4, steps = K / TGK;
+
+    // ---- weight codes: thread -> row tid/4, code bytes 16 (tid%4) .. +15 of the step
+    const int wr = tid >> 2, wc = tid & 3;
+    const uint8_t* wsrc = w + (int64_t)min(m0 + wr, M - 1) * bpr + 16 * wc;
+    uint4 wv[4];
+    auto decode = [&](const uint4& v, uint8_t* tile) {
+        const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {  // code dword g: columns 64 wc + 16 g .. +15
+            const uint32_t u = ucode(q[g]);
+            *(uint4*)(tile + tg_off(wr, 4 * wc + g)) =
+                make_uint4(u & 0x03030303u, (u >> 2) & 0x03030303u, (u >> 4) & 0x03030303u, (u >> 6) & 0x03030303u);
+        }
+    };
+    // ---- activations: lane (n = lane%16, g = lane/16), tokens n0 + 32 wave + 16 j + n
+    const int8_t* bsrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bsrc[j] = ap + (int64_t)min(n0 + 32 * wave + 16 * j + (lane & 15), N - 1) * K + 16 * (lane >> 4);
+    i32x4 bv[2][2][4];  // [buffer][j][k chunk c]
+    auto load_b = [&](int step, int b) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) bv[b][j][c] = *(const i32x4*)(bsrc[j] + step * TGK + 64 * c);
+    };
+
+    i32x4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+#pragma unroll
+    for (int u = 0; u < 4; ++u) wv[u] = ld_stream(wsrc + (int64_t)min(u, steps - 1) * (TGK / 4));
+    load_b(0, 0);
+    decode(wv[0], wt[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < steps; s0 += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int step = s0 + u;
+            if (step >= steps) break;
+            load_b(min(step + 1, steps - 1), (u + 1) & 1);
+            decode(wv[(u + 1) & 3], wt[(u + 1) & 1]);                                  // W(step + 1)
+            wv[u & 3] = ld_stream(wsrc + (int64_t)min(step + 4, steps - 1) * (TGK / 4));  // slot of W(step)
+            const uint8_t* cur = wt[u & 1];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                i32x4 af[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    af[i] = *(const i32x4*)(cur + tg_off(16 * i + (lane & 15), 4 * c + (lane >> 4)));
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bv[u & 1][j][c], acc[i][j], 0, 0, 0);
+            }
+            __syncthreads();
+        }
+    }
+    // D: lane l holds rows 16 i + 4 (l/16) + r, token 16 j + l%16 (of the wave's 32)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + 32 * wave + 16 * j + (lane & 15);
+        if (n >= N) continue;
+        const int as = sums[n];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 16 * i + 4 * (lane >> 4) + r;
+                if (m < M) out[(int64_t)m * N + n] = (float)(acc[i][j][r] - as);
+            }
+    }
+}
+
 template <int LPR, int NSEG>
 hipError_t run_i2s_fast(const uint8_t* packed, float w_scale, const float* x, const int8_t* act,
                         const float* act_scale, float* y, int64_t M, int64_t K, int64_t batch, hipStream_t s) {
@@ -514,6 +793,13 @@ hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x,
     const int64_t nseg = K / 64;
     const bool fast = K % 64 == 0 && nseg <= 256 && M < (1ll << 31) && aligned16(packed) &&
                       (x ? aligned16(x) : aligned16(act));
+    if (fast && batch == 1 && x && K <= 4096) {
+        // batch 1, f32 activations: all loads up front, 16 rows per workgroup
+        const int grid = ceil_div(M, 4 * kWaves);
+        const size_t lds = (size_t)K;
+        i2s_gemv_rows<4, 1, 4, true><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M, (int)K);
+        return hipGetLastError();
+    }
     if (fast) {
         if (nseg <= 16) return run_i2s_fast<16, 1>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
         if (nseg <= 32) return run_i2s_fast<16, 2>(packed, w_scale, x, act, act_scale, y, M, K, batch, s);
@@ -561,8 +847,22 @@ hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o, int64_t M
     return hipGetLastError();
 }
 
+size_t i2s_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    const bool mfma = M >= 64 && N >= 64 && K % TGK == 0 && K < (1ll << 24) && M < (1ll << 31) && N < (1ll << 31) &&
+                      ((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN) < (1ll << 31);
+    return mfma ? (size_t)(((N * K + 255) / 256) * 256 + N * 4) : 0;
+}
+
 hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o, int64_t M, int64_t N, int64_t K,
-                                hipStream_t s) {
+                                void* ws, hipStream_t s) {
+    if (ws) {  // i2s_gemm_workspace_bytes(M, N, K) bytes: permuted activations, then token sums
+        int8_t* ap = (int8_t*)ws;
+        int* sums = (int*)((char*)ws + ((N * K + 255) / 256) * 256);
+        i2s_act_perm<<<(unsigned)N, kWG, 0, s>>>(a, ap, sums, (int)K);
+        const unsigned grid = (unsigned)(((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN));
+        i2s_gemm_mfma<<<grid, kWG, 0, s>>>(w, ap, sums, o, (int)M, (int)N, (int)K);
+        return hipGetLastError();
+    }
     i2s_gemm_vnni_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);
     return hipGetLastError();
 }

@@ -10,7 +10,7 @@ chosen by shape (the launcher's dispatch rules):
   valu     batch 1, cb_block 64               (oil4_gemv_valu, FP32 FMA)
   generic  K = 1000, cb_block 100             (oil4_generic)
   bt       batch 4, cb_block 128              (oil4_gemv_bt, split-K MFMA)
-  prefill  bf16 A, cb_block 128 / 32          (oil4_prefill_mfma / oil4_gemm_prefill_k)
+  prefill  bf16 A: oil4_prefill_ws (N % 96 == 0), oil4_prefill_mfma, oil4_gemm_prefill_k
 
 A flush of subnormals to zero would turn the all-subnormal case's outputs into
 0 (relative error 1); the bar is 1e-5 of sum|w*x| per element.  NaN outputs
@@ -36,7 +36,10 @@ GEMV_PATHS = [  # name, M, K, batch, cb_block
     ("generic", 40, 1000, 1, 100),
     ("bt", 200, 2048, 4, 128),
 ]
-PREFILL_PATHS = [("prefill_mfma", 128, 96, 512, 128), ("prefill_k", 64, 80, 256, 32)]
+# producer/consumer FP16-A kernel (N a multiple of 96), the LDS-staged kernel
+# (N fits no tile of the former), the first kernel (codebook block 32)
+PREFILL_PATHS = [("prefill_ws", 128, 96, 512, 128), ("prefill_mfma", 72, 100, 512, 128),
+                 ("prefill_k", 64, 80, 256, 32)]
 
 
 def codebooks(kind, rows, nblk, seed):
