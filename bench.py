@@ -270,7 +270,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,i2s,prefill,ternary_gemm,decode (default all)")
+    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,prefill,ternary_gemm,decode (default all)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -307,6 +307,12 @@ def main():
         extra["oil8_gemv_4096x4096_b1"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
                                                bytes=r["bytes"], copies=r["copies"])
         log(f"oil8 b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
+    if want("oil8b16"):
+        r, _ = bench_oil8_gemv(mth, dev, 4096, 4096, 16, args.steps, args.warmup)
+        gbs = r["bytes"] / r["sec"] / 1e9
+        extra["oil8_gemv_4096x4096_b16"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
+                                                bytes=r["bytes"], copies=r["copies"])
+        log(f"oil8 b=16: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
     if want("i2s"):
         r, _ = bench_i2s_gemv(mth, dev, 4096, 4096, 1, args.steps, args.warmup)
         gbs = r["bytes"] / r["sec"] / 1e9

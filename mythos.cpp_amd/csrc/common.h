@@ -54,6 +54,63 @@ __device__ __forceinline__ uint32_t u4get(const uint4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
+// ---- row segments: one launch over up to three matrices with the same K --
+// Segment s covers workgroups [g0[s], g0[s+1]) and rows [off[s], off[s] +
+// rows[s]) of the concatenated row space (g0, off: INT_MAX past the last).
+struct Oil8SegArgs {
+    const uint8_t* idx[3];
+    const float* cb[3];
+    float* y[3];
+    int rows[3];
+    int g0[3];
+    int off[3];
+    int mtot;
+};
+// Host-side description of one segment.
+struct Oil8Seg {
+    const uint8_t* idx;
+    const float* cb;
+    float* y;
+    int64_t rows;
+};
+constexpr int kOil8MaxSegs = 3;
+
+// Segment table for workgroups of `per_group` rows (nseg <= 3, rows < 2^31).
+inline Oil8SegArgs make_seg_args(const Oil8Seg* seg, int nseg, int per_group) {
+    Oil8SegArgs a{};
+    int g = 0, r = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            a.idx[i] = seg[i].idx;
+            a.cb[i] = seg[i].cb;
+            a.y[i] = seg[i].y;
+            a.rows[i] = (int)seg[i].rows;
+            a.g0[i] = g;
+            a.off[i] = r;
+            g += (int)((seg[i].rows + per_group - 1) / per_group);
+            r += (int)seg[i].rows;
+        } else {
+            a.idx[i] = seg[0].idx;
+            a.cb[i] = seg[0].cb;
+            a.y[i] = seg[0].y;
+            a.rows[i] = 1;
+            a.g0[i] = 0x7fffffff;
+            a.off[i] = 0x7fffffff;
+        }
+    }
+    a.mtot = r;
+    return a;
+}
+// Workgroups of a segment table (blockIdx.x range).
+inline int seg_groups(const Oil8Seg* seg, int nseg, int per_group) {
+    int g = 0;
+    for (int i = 0; i < nseg; ++i) g += (int)((seg[i].rows + per_group - 1) / per_group);
+    return g;
+}
+
+__device__ __forceinline__ int seg_of_group(const Oil8SegArgs& a, int g) { return (g >= a.g0[1]) + (g >= a.g0[2]); }
+__device__ __forceinline__ int seg_of_row(const Oil8SegArgs& a, int r) { return (r >= a.off[1]) + (r >= a.off[2]); }
+
 // ---- int8 helpers ---------------------------------------------------------
 // sum_{i<4} (int8)a.byte[i] * (int8)b.byte[i] + c   (v_dot4_i32_i8)
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

@@ -1,7 +1,7 @@
 // decoder.hip — the mixed-format decoder stack (include/mythos_decoder.h).
 //
 // One decode step for B sequences is a fixed sequence of launches on one
-// stream (per layer: RMSNorm, Q/K/V OIL8 GEMVs, RoPE + KV append + attention
+// stream (per layer: RMSNorm, one OIL8 launch for Q, K and V, RoPE + KV append + attention
 // in one kernel, O GEMV, residual add fused into the FFN RMSNorm, gate/up
 // OIL4 GEMV (one launch over 2*ffn rows when gate and up are adjacent),
 // SwiGLU fused with the per-token int8 quantisation, ternary down GEMV on the
@@ -81,6 +81,24 @@ hipError_t oil8(const mth_decoder* d, const uint8_t* w, const float* cb, const f
     return mth::launch_oil8_gemv(w, cb, x, y, M, K, d->batch, s);
 }
 
+// Q, K and V projections of the normed input: one launch over the three
+// matrices (each with its own codebook) where the kernels take them.
+hipError_t qkv(const mth_decoder* d, const mth_decoder_layer& L, hipStream_t s) {
+    const mth_decoder_config& c = d->c;
+    const int64_t H = c.hidden, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    const mth::Oil8Seg seg[3] = {{L.wq, L.cbq, d->q, QD}, {L.wk, L.cbk, d->k, KD}, {L.wv, L.cbv, d->v, KD}};
+    if (d->batch >= 2) {
+        if (mth::oil8_bt_segs_fusable(seg, 3, H, d->batch))
+            return mth::launch_oil8_gemv_bt_segs(seg, 3, d->h, H, d->batch, d->bt_partial, s);
+    } else if (mth::oil8_segs_fusable(seg, 3, H)) {
+        return mth::launch_oil8_gemv_segs(seg, 3, d->h, H, d->batch, s);
+    }
+    hipError_t e = oil8(d, L.wq, L.cbq, d->h, d->q, QD, H, s);
+    if (e == hipSuccess) e = oil8(d, L.wk, L.cbk, d->h, d->k, KD, H, s);
+    if (e == hipSuccess) e = oil8(d, L.wv, L.cbv, d->h, d->v, KD, H, s);
+    return e;
+}
+
 hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     const mth_decoder_config& c = d->c;
     const int64_t B = d->batch, H = c.hidden, F = c.ffn, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
@@ -107,9 +125,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         float* tp_down = tp ? tp_inv + B : nullptr;
         // residual of the previous layer's FFN folded into this norm
         TRY(mth::launch_rms_norm(d->x, l == 0 ? nullptr : d->t, L.attn_norm, d->h, B, H, c.eps, s));
-        TRY(oil8(d, L.wq, L.cbq, d->h, d->q, QD, H, s));
-        TRY(oil8(d, L.wk, L.cbk, d->h, d->k, KD, H, s));
-        TRY(oil8(d, L.wv, L.cbv, d->h, d->v, KD, H, s));
+        TRY(qkv(d, L, s));
         TRY(mth::launch_rope_attention(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
                                        d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq,
                                        s));
@@ -194,8 +210,8 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     d->layer_kv = B * KD * c.max_seq;
     d->kv_elem = c.kv_dtype == 1 ? 2 : 4;
     // workspace of the batched GEMVs: the largest of every projection's need
-    const size_t partial = std::max({mth::oil4_bt_partial_bytes(2 * F, H), mth::oil8_bt_partial_bytes(QD, H),
-                                     mth::oil8_bt_partial_bytes(KD, H), mth::oil8_bt_partial_bytes(H, QD),
+    const size_t partial = std::max({mth::oil4_bt_partial_bytes(2 * F, H), mth::oil8_bt_partial_bytes(QD + 2 * KD, H),
+                                     mth::oil8_bt_partial_bytes(H, QD),
                                      mth::oil8_bt_partial_bytes(c.vocab, H), mth::i2s_bt_partial_bytes(H, F)});
     struct Slot {
         void** p;

@@ -88,15 +88,19 @@ __device__ __forceinline__ float transposed_sum(float (&v)[R], int lane) {
 // save).
 template <int R>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4, 4)))
-void oil8_gemv_k(const uint8_t* idx, const float* __restrict__ cb, const float* x, float* __restrict__ y, int M,
-                 int K, int batch) {
+void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch) {
     __shared__ float tab[256];
     __shared__ float part[kWaves][R];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kq = wave * 1024 + lane * 16;  // first column of this lane
     const bool act = kq < K;
     const int kl = act ? kq : K - 16;        // clamped: every load below is unconditional
-    const int m0 = blockIdx.x * R;
+    const int sgi = seg_of_group(sg, blockIdx.x);
+    const uint8_t* idx = sg.idx[sgi];
+    const float* __restrict__ cb = sg.cb[sgi];
+    float* __restrict__ y = sg.y[sgi];
+    const int M = sg.rows[sgi];
+    const int m0 = (blockIdx.x - sg.g0[sgi]) * R;
 
     float4 xq[4];
 #pragma unroll
@@ -657,11 +661,29 @@ hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x,
                             int64_t M, int64_t K, int64_t batch, hipStream_t s) {
     const bool fast = (K % 16 == 0) && K <= 4096 && M < (1ll << 31) && aligned16(idx) && aligned16(x);
     if (fast) {
-        constexpr int R = 4;
-        oil8_gemv_k<R><<<ceil_div(M, R), kWG, 0, s>>>(idx, cb, x, y, (int)M, (int)K, (int)batch);
+        const Oil8Seg seg{idx, cb, y, M};
+        return launch_oil8_gemv_segs(&seg, 1, x, K, batch, s);
     } else {
         oil8_generic<<<ceil_div(M, kWaves), kWG, 0, s>>>(idx, cb, x, y, M, K, 1, batch, M);
     }
+    return hipGetLastError();
+}
+
+bool oil8_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K) {
+    if (nseg < 1 || nseg > kOil8MaxSegs || K % 16 != 0 || K > 4096) return false;
+    int64_t total = 0;
+    for (int i = 0; i < nseg; ++i) {
+        if (seg[i].rows < 1 || !aligned16(seg[i].idx)) return false;
+        total += seg[i].rows;
+    }
+    return total < (1ll << 31);
+}
+
+hipError_t launch_oil8_gemv_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
+                                 hipStream_t s) {
+    constexpr int R = 4;
+    const Oil8SegArgs a = make_seg_args(seg, nseg, R);
+    oil8_gemv_k<R><<<seg_groups(seg, nseg, R), kWG, 0, s>>>(a, x, (int)K, (int)batch);
     return hipGetLastError();
 }
 

@@ -176,84 +176,262 @@ __global__ __launch_bounds__(256) void oil4_bt_reduce(const float* __restrict__ 
 inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 // ===================================================================
-// OIL8, batch 2..16, on FP32 MFMA (v_mfma_f32_16x16x4_f32)
+// OIL8, batch 2..16, on FP16 MFMA (three products per weight block)
 // ===================================================================
 //   y[t][m] = sum_k cb[idx[m][k]] * x[t][k]
-// Workgroup = 4 waves x 16 rows and one K slice of ks columns (a multiple of
-// 64); grid = (ceil(M / 64), K / ks).  Per 64-column chunk, lane l (row
-// r = l % 16, k group g = l / 16) loads the 16 index bytes of its row at
-// chunk columns 16g .. 16g + 15 (one 128-bit load), gathers their FP32
-// codebook values from LDS and feeds them to 16 MFMAs: in MFMA j the lane's
-// A element is W[r][16g + j] and its B element x[t = r][16g + j], i.e. the k
-// order inside the chunk is permuted alike on both operands.  Products and
-// sums are FP32.  The chunk's x for 16 tokens ([16][64] floats, rows padded
-// to 68 floats against bank conflicts) is staged in LDS once per workgroup
-// (double buffered) and read by all four waves.  Slices are added by
-// oil4_bt_reduce (same [slice][16][M] partial layout).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr int kO8Pad = 68;
+// The codebook is scaled by 2^sw (max|cb| 2^sw < 2^15) and each entry split
+// into FP16 hi + lo parts, c 2^sw = ch + cl; each token's activations of the
+// K slice alike with its own 2^sx, x 2^sx = xh + xl.  Every residual is
+// below 2^-22 of the value, every FP16 product is exact in FP32, and
+//   D = Ah Bh + Ah Bl + Al Bh          (v_mfma_f32_16x16x32_f16, FP32 sums)
+// leaves out only Al Bl (2^-22 of the product), so D 2^-(sw+sx) is the FP32
+// dot product to FP32 accuracy.  Three FP16 MFMAs cost a sixth of the
+// sixteen FP32 MFMAs (v_mfma_f32_16x16x4_f32) the same 512 products take.
+//
+// Tiling.  Workgroup = 4 waves x NT tiles of 16 rows, one K slice of
+// 128 PH columns.  Per 128-column phase a wave loads each tile in two
+// 128-byte-per-row instructions (rows 0-7, rows 8-15, 8 lanes per row) and
+// a DPP row rotation hands lane (j = l % 16, q = l / 16) the 32 index bytes
+// of row j at columns 32q .. 32q + 31; MFMA m takes bytes 8m .. 8m + 7 as
+// its A column group q (k order 32q + 8m + e on both operands).  The
+// 256-entry table of (hi, lo) pairs sits in LDS (one ds_read_b32 gather per
+// weight gives both parts); the slice's activations for 16 tokens are
+// converted once into hi / lo B fragments in LDS (8 KB per phase) and read
+// by all waves, so the main loop has no barrier.  All weight loads of the
+// slice are issued before the conversion.  Slices (grid.y) write partial
+// sums that oil8_seg_reduce adds in slice order (deterministic).
+//
+// Non-finite values.  Inf cannot be split (Inf - Inf is NaN), so a
+// workgroup whose codebook or activations hold a non-finite value computes
+// its outputs with FP32 FMAs over the reference's products in column order
+// instead (a uniform branch; same outputs up to the summation order).
+constexpr int kH3Tok = 16;
+constexpr int kH3Hdr = 1280;   // table (1 KB), token shifts, wave maxima
+constexpr int kH3Phase = 8192; // B of one 128-column phase: hi 4 KB, then lo 4 KB
 
-__global__ __launch_bounds__(256) void oil8_gemv_bt(const uint8_t* idx, const float* __restrict__ cb, const float* x,
-                                                    float* __restrict__ y, float* __restrict__ partial, int M, int K,
-                                                    int batch, int ks) {
-    __shared__ float tab[256];
-    __shared__ __align__(16) float xs[2][kBtTok * kO8Pad];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.x * kBtRows + wave * 16;
-    const int k0 = blockIdx.y * ks;
-    const int nch = ks / 64;
-    const uint8_t* wrow = idx + (int64_t)min(m0 + r, M - 1) * K + k0 + 16 * g;  // clamped rows
-    const int xt = tid >> 4, xc = (tid & 15) * 4;  // staging: token xt, 4 columns at xc
-    const bool xv = xt < batch;
-    const float* xrow = x + (int64_t)(xv ? xt : 0) * K + k0 + xc;
-    float4 xn = xv ? ldf4(xrow) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    tab[tid] = cb[tid];
-    uint4 wn = ld_stream(wrow);
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < nch; ++c) {
-        float* xb = xs[c & 1];
-        *(float4*)(xb + xt * kO8Pad + xc) = xn;
-        __syncthreads();  // the buffer written two chunks ago has been read by all
-        const uint4 w = wn;
-        if (c + 1 < nch) {
-            wn = ld_stream(wrow + (c + 1) * 64);
-            if (xv) xn = ldf4(xrow + (c + 1) * 64);
-        }
-        const float* xp = xb + r * kO8Pad + 16 * g;
-        float4 xb4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) xb4[q] = *(const float4*)(xp + 4 * q);
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float xq[4] = {xb4[q].x, xb4[q].y, xb4[q].z, xb4[q].w};
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(tab[(wd[q] >> (8 * b)) & 0xffu], xq[b], acc, 0, 0, 0);
-        }
-    }
-    // D: lane l holds rows 4g + i, token r
-    const int t = r;
-    if (t >= batch) return;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * g + i;
-        if (m >= M) continue;
-        if (gridDim.y == 1)
-            y[(int64_t)t * M + m] = acc[i];
-        else
-            partial[((int64_t)blockIdx.y * kBtTok + t) * M + m] = acc[i];
-    }
+// B slot (MFMA m, column group q, token n): 16 bytes, tokens XOR-permuted
+// per (m, q) so that the 16 threads storing one token and the 16 lanes
+// reading one (m, q) both hit distinct banks.
+__device__ __forceinline__ int h3_slot(int m, int q, int n) {
+    const int mq = m * 4 + q;
+    return (mq * kH3Tok + (n ^ mq)) * 16;
 }
 
-// K slices for the OIL8 batched GEMV: enough workgroups to cover the CUs,
-// at most 16, each a multiple of 64 columns.
-inline int o8_slices(int64_t M, int64_t K) {
-    const int64_t groups = (M + kBtRows - 1) / kBtRows;
-    int S = 1;
-    while (S < 16 && groups * S < 256 && K % (64 * S * 2) == 0) S *= 2;
-    return S;
+// lane (j, q) <- row j, pieces 2q (a) and 2q + 1 (b) of a 16-row tile loaded
+// as wx (rows 0-7) and wy (rows 8-15), lane (j, q) holding piece 2q + j/8
+// of row j % 8 (see Oil4TileLoads::exchange)
+__device__ __forceinline__ void h3_exchange(const uint4& wx, const uint4& wy, int lane, uint4& a, uint4& b) {
+    const bool keep = (lane & 15) < 8;
+    const uint32_t ry0 = dpp_ror8(wy.x), ry1 = dpp_ror8(wy.y), ry2 = dpp_ror8(wy.z), ry3 = dpp_ror8(wy.w);
+    const uint32_t rx0 = dpp_ror8(wx.x), rx1 = dpp_ror8(wx.y), rx2 = dpp_ror8(wx.z), rx3 = dpp_ror8(wx.w);
+    a = make_uint4(keep ? wx.x : ry0, keep ? wx.y : ry1, keep ? wx.z : ry2, keep ? wx.w : ry3);
+    b = make_uint4(keep ? rx0 : wy.x, keep ? rx1 : wy.y, keep ? rx2 : wy.z, keep ? rx3 : wy.w);
+}
+
+__device__ __forceinline__ uint32_t h3_pair(float c) {
+    const _Float16 h = (_Float16)c;
+    const _Float16 l = (_Float16)(c - (float)h);
+    return (uint32_t)__builtin_bit_cast(uint16_t, h) | ((uint32_t)__builtin_bit_cast(uint16_t, l) << 16);
+}
+
+template <int NT, int PH>
+__global__ __launch_bounds__(256) void oil8_gemv_h3(Oil8SegArgs sg, const float* x, float* __restrict__ partial,
+                                                    int K, int batch) {
+    constexpr int KS = 128 * PH;
+    __shared__ __align__(16) uint8_t lds[kH3Hdr + PH * kH3Phase];
+    uint32_t* tab = (uint32_t*)lds;
+    int* shifts = (int*)(lds + 1024);
+    float* wmax = (float*)(lds + 1024 + 4 * kH3Tok);
+    uint8_t* bsm = lds + kH3Hdr;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
+    const int sgi = seg_of_group(sg, blockIdx.x);
+    const uint8_t* idx = sg.idx[sgi];
+    const int M = sg.rows[sgi];
+    const int row0w = (blockIdx.x - sg.g0[sgi]) * (64 * NT) + wave * 16 * NT;
+    const int k0 = blockIdx.y * KS;
+
+    // ---- activations of the slice (thread -> token tt, columns 8u .. 8u+7
+    // of every phase), the thread's codebook entry, then every weight load
+    const int tt = tid >> 4, u = tid & 15;
+    const bool tok = tt < batch;
+    const float* xr = x + (int64_t)(tok ? tt : 0) * K + k0 + 8 * u;
+    float4 xa[PH], xb[PH];
+#pragma unroll
+    for (int p = 0; p < PH; ++p) {
+        xa[p] = ldf4(xr + 128 * p);
+        xb[p] = ldf4(xr + 128 * p + 4);
+    }
+    const float cbv = sg.cb[sgi][tid];
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wx[NT][PH], wy[NT][PH];
+    {
+        const uint8_t* px[NT];
+        const uint8_t* py[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            px[t] = idx + (int64_t)min(row0w + 16 * t + jj8, M - 1) * K + k0 + 16 * (2 * q + hi8);
+            py[t] = idx + (int64_t)min(row0w + 16 * t + 8 + jj8, M - 1) * K + k0 + 16 * (2 * q + hi8);
+        }
+#pragma unroll
+        for (int p = 0; p < PH; ++p)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                wx[t][p] = ld_stream(px[t] + 128 * p);
+                wy[t][p] = ld_stream(py[t] + 128 * p);
+            }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- scales: token max over the slice (its 16 threads form one DPP
+    // row), codebook max over the workgroup; any non-finite value -> FMA path
+    float xm = 0.0f;
+    bool fin = __builtin_isfinite(cbv);
+    if (tok) {
+#pragma unroll
+        for (int p = 0; p < PH; ++p) {
+            const float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                xm = fmaxf(xm, fabsf(v[e]));
+                fin = fin && __builtin_isfinite(v[e]);
+            }
+        }
+    }
+    const int sx = fp16_scale_shift(row16_max(xm));
+    const float cm = wave_max(fabsf(cbv));
+    if (lane == 0) wmax[wave] = cm;
+    if (u == 0) shifts[tt] = sx;
+    const bool special = __syncthreads_or(!fin) != 0;
+
+    floatx4 acc[NT];
+    int unscale = 0;
+    if (!special) {
+        const int sw = fp16_scale_shift(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+        tab[tid] = h3_pair(ldexpf(cbv, sw));
+#pragma unroll
+        for (int p = 0; p < PH; ++p) {
+            const float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+            half8 vh, vl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xs = tok ? ldexpf(v[e], sx) : 0.0f;
+                const _Float16 h = (_Float16)xs;
+                vh[e] = h;
+                vl[e] = (_Float16)(xs - (float)h);
+            }
+            uint8_t* bp = bsm + p * kH3Phase + h3_slot(u & 3, u >> 2, tt);
+            *(half8*)bp = vh;
+            *(half8*)(bp + 4096) = vl;
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int p = 0; p < PH; ++p) {
+            uint4 a[NT], b[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) h3_exchange(wx[t][p], wy[t][p], lane, a[t], b[t]);
+            const uint8_t* bp = bsm + p * kH3Phase;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const half8 bh = *(const half8*)(bp + h3_slot(m, q, j));
+                const half8 bl = *(const half8*)(bp + 4096 + h3_slot(m, q, j));
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint32_t w0 = m == 0 ? a[t].x : m == 1 ? a[t].z : m == 2 ? b[t].x : b[t].z;
+                    const uint32_t w1 = m == 0 ? a[t].y : m == 1 ? a[t].w : m == 2 ? b[t].y : b[t].w;
+                    uint32_t gv[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        gv[e] = tab[(w0 >> (8 * e)) & 0xffu];
+                        gv[4 + e] = tab[(w1 >> (8 * e)) & 0xffu];
+                    }
+                    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+                    u32x4v ah, al;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        ah[d] = __builtin_amdgcn_perm(gv[2 * d + 1], gv[2 * d], 0x05040100u);
+                        al[d] = __builtin_amdgcn_perm(gv[2 * d + 1], gv[2 * d], 0x07060302u);
+                    }
+                    const half8 Ah = __builtin_bit_cast(half8, ah), Al = __builtin_bit_cast(half8, al);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, bh, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, bl, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, bh, acc[t], 0, 0, 0);
+                }
+            }
+        }
+        unscale = sw + shifts[j];
+    } else {
+        // FP32 FMAs over the slice's columns in order (rows 4q + i, token j)
+        const float* cb = sg.cb[sgi];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = row0w + 16 * t + 4 * q + i;
+                float sum = 0.0f;
+                if (j < batch && row < M) {
+                    const uint8_t* wr = idx + (int64_t)row * K + k0;
+                    const float* xx = x + (int64_t)j * K + k0;
+                    for (int k = 0; k < KS; ++k) sum = fmaf(cb[wr[k]], xx[k], sum);
+                }
+                acc[t][i] = sum;
+            }
+    }
+
+    // ---- D[4q + i][j]: rows row0w + 16t + 4q + i, token j
+    if (j >= batch) return;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0w + 16 * t + 4 * q + i;
+            if (row >= M) continue;
+            const float v = ldexpf(acc[t][i], -unscale);
+            if (gridDim.y == 1)
+                sg.y[sgi][(int64_t)j * M + row] = v;
+            else
+                partial[((int64_t)blockIdx.y * kH3Tok + j) * sg.mtot + sg.off[sgi] + row] = v;
+        }
+}
+
+// y of segment s, token t, row r = sum over slices z = 0, 1, ... of
+// partial[z][t][off[s] + r] (slice order: deterministic).
+__global__ __launch_bounds__(256) void oil8_seg_reduce(const float* __restrict__ partial, Oil8SegArgs sg, int batch,
+                                                       int nslice) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)batch * sg.mtot) return;
+    const int t = (int)(i / sg.mtot), r = (int)(i - (int64_t)t * sg.mtot);
+    const int s = seg_of_row(sg, r);
+    const float* p = partial + (int64_t)t * sg.mtot + r;
+    const int64_t zs = (int64_t)kH3Tok * sg.mtot;
+    float sum = p[0];
+    for (int z0 = 1; z0 < nslice; z0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = z0 + e < nslice ? p[(z0 + e) * zs] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (z0 + e < nslice) sum += v[e];
+    }
+    sg.y[s][(int64_t)t * sg.rows[s] + (r - sg.off[s])] = sum;
+}
+
+// phases of 128 columns per K slice
+inline int h3_phases(int64_t K) { return K % 512 == 0 ? 4 : (K % 256 == 0 ? 2 : 1); }
+
+// tiles per wave: two once the grid has enough workgroups without them
+inline int h3_tiles(int groups64, int64_t slices) { return (int64_t)groups64 * slices >= 2048 ? 2 : 1; }
+
+template <int NT, int PH>
+void run_h3(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int b, float* partial, hipStream_t s) {
+    const Oil8SegArgs a = make_seg_args(seg, nseg, 64 * NT);
+    const int S = (int)(K / (128 * PH));
+    const dim3 grid((unsigned)seg_groups(seg, nseg, 64 * NT), (unsigned)S);
+    oil8_gemv_h3<NT, PH><<<grid, 256, 0, s>>>(a, x, partial, (int)K, b);
+    if (S > 1) oil8_seg_reduce<<<ceil_div_i((int64_t)b * a.mtot, 256), 256, 0, s>>>(partial, a, b, S);
 }
 
 // phases of 256 columns per K slice: 4 (K a multiple of 1024, K >= 2048) or 2
@@ -283,29 +461,58 @@ size_t oil4_bt_partial_bytes(int64_t M, int64_t K) {
 }
 
 bool oil8_bt_supported(int64_t M, int64_t K, int64_t batch) {
-    // the kernel takes K and its slice width as int
-    return batch >= 2 && K >= 64 && K % 64 == 0 && K < (1ll << 31) && M < (1ll << 31) && M * K < (1ll << 40);
+    // the kernel takes K, rows and the concatenated row index as int
+    return batch >= 2 && K >= 128 && K % 128 == 0 && K < (1ll << 31) && M < (1ll << 31) && M * K < (1ll << 40);
 }
 
 size_t oil8_bt_partial_bytes(int64_t M, int64_t K) {
-    const int S = o8_slices(M, K);
-    return S > 1 ? (size_t)(S * kBtTok * M * 4) : 0;
+    const int64_t S = K / (128 * h3_phases(K));
+    return S > 1 ? (size_t)(S * kH3Tok * M * 4) : 0;
 }
 
-hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
-                               int64_t batch, float* partial, hipStream_t s) {
-    const int S = o8_slices(M, K);
-    const dim3 grid(ceil_div_i(M, kBtRows), (unsigned)S);
-    for (int64_t t0 = 0; t0 < batch; t0 += kBtTok) {
-        const int b = (int)(batch - t0 < kBtTok ? batch - t0 : kBtTok);
-        oil8_gemv_bt<<<grid, 256, 0, s>>>(idx, cb, x + t0 * K, y + t0 * M, partial, (int)M, (int)K, b,
-                                          (int)(K / S));
-        if (S > 1)
-            oil4_bt_reduce<<<ceil_div_i((int64_t)b * M, 256), 256, 0, s>>>(partial, y + t0 * M, (int)M, b, S);
+bool oil8_bt_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K, int64_t batch) {
+    if (nseg < 1 || nseg > kOil8MaxSegs) return false;
+    int64_t total = 0;
+    for (int i = 0; i < nseg; ++i) {
+        if (seg[i].rows < 1 || ((uintptr_t)seg[i].idx & 15u) != 0) return false;
+        total += seg[i].rows;
+    }
+    return oil8_bt_supported(total, K, batch);
+}
+
+hipError_t launch_oil8_gemv_bt_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
+                                    float* partial, hipStream_t s) {
+    const int ph = h3_phases(K);
+    const int64_t S = K / (128 * ph);
+    const int nt = h3_tiles(seg_groups(seg, nseg, 64), S);
+    // groups of 16 tokens, one launch each (the weights are read per group)
+    for (int64_t t0 = 0; t0 < batch; t0 += kH3Tok) {
+        const int b = (int)(batch - t0 < kH3Tok ? batch - t0 : kH3Tok);
+        Oil8Seg g[kOil8MaxSegs];
+        for (int i = 0; i < nseg; ++i) {
+            g[i] = seg[i];
+            g[i].y = seg[i].y + t0 * seg[i].rows;
+        }
+        const float* xg = x + t0 * K;
+        if (nt == 2) {
+            if (ph == 4) run_h3<2, 4>(g, nseg, xg, K, b, partial, s);
+            else if (ph == 2) run_h3<2, 2>(g, nseg, xg, K, b, partial, s);
+            else run_h3<2, 1>(g, nseg, xg, K, b, partial, s);
+        } else {
+            if (ph == 4) run_h3<1, 4>(g, nseg, xg, K, b, partial, s);
+            else if (ph == 2) run_h3<1, 2>(g, nseg, xg, K, b, partial, s);
+            else run_h3<1, 1>(g, nseg, xg, K, b, partial, s);
+        }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
+                               int64_t batch, float* partial, hipStream_t s) {
+    const Oil8Seg seg{idx, cb, y, M};
+    return launch_oil8_gemv_bt_segs(&seg, 1, x, K, batch, partial, s);
 }
 
 hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y,

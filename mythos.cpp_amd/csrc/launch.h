@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.h"
+
 namespace mth {
 
 // ---- errors of the C ABI (capi.hip): set the calling thread's message ----
@@ -18,6 +20,15 @@ int api_ok();
 // y[t*M + m] = sum_k cb[idx[m*K + k]] * x[t*K + k]          (t < batch)
 hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x, float* y,
                             int64_t M, int64_t K, int64_t batch, hipStream_t s);
+// Up to three OIL8 matrices with the same K and input, each with its own
+// codebook and output (the Q, K and V projections), in one launch:
+// seg[i].y[t*rows + m] = sum_k seg[i].cb[seg[i].idx[m*K + k]] * x[t*K + k].
+// (Oil8Seg: common.h)
+// Segments fused into one launch: K % 16 == 0, K <= 4096, 16-byte aligned
+// weights and x (each workgroup stays inside one segment).
+bool oil8_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K);
+hipError_t launch_oil8_gemv_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
+                                 hipStream_t s);
 // Reference per-(m,n) indexing (src/kernel_oil8.cpp:20-24):
 // out[r] = sum_k cb[idx[r*K + k]] * act[(r % N)*K + k],  r < M*N
 hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float* act, float* out,
@@ -36,12 +47,17 @@ bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch);
 size_t oil4_bt_partial_bytes(int64_t M, int64_t K);
 hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y,
                                int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
-// OIL8 for batches of 2 and more (gemv_batched.hip, FP32 MFMA); same
-// workspace contract as the OIL4 batched kernel.
+// OIL8 for batches of 2 and more (gemv_batched.hip, FP16 MFMA with
+// three products per block); same workspace contract as the OIL4 batched
+// kernel.  The segmented form takes up to kOil8MaxSegs matrices; its
+// workspace is oil8_bt_partial_bytes(total rows, K).
 bool oil8_bt_supported(int64_t M, int64_t K, int64_t batch);
 size_t oil8_bt_partial_bytes(int64_t M, int64_t K);
 hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
                                int64_t batch, float* partial, hipStream_t s);
+bool oil8_bt_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K, int64_t batch);
+hipError_t launch_oil8_gemv_bt_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
+                                    float* partial, hipStream_t s);
 // Reference per-(m,n) indexing with one codebook (src/kernel_oil4.cpp:41-52).
 hipError_t launch_oil4_gemm_mn(const uint8_t* nib, const uint16_t* cb, const float* act, float* out,
                                int64_t M, int64_t N, int64_t K, hipStream_t s);

@@ -159,7 +159,7 @@ __device__ __forceinline__ float oil4_hi_lo(float hi, float lo) { return __built
 // Power-of-two exponent s with max|x| * 2^s < 2^15 (0 for zero / non-finite).
 __device__ __forceinline__ int fp16_scale_shift(float mx) {
     int e = 0;
-    if (mx > 0.0f && mx <= 3.0e38f) {
+    if (mx > 0.0f && mx <= 3.40282347e38f) {
         (void)frexpf(mx, &e);
         return 15 - e;
     }

@@ -125,6 +125,31 @@ def test_batch_matches_single_sequences(small):
             assert rel(dec3.logits()[b], dec1.logits()[0]) < TOL, (b, s)
 
 
+# grouped-query attention: Q, K and V segments of 256, 128 and 128 rows in
+# the fused projection launch
+GQA = dict(SMALL, heads=4, kv_heads=2, head_dim=64)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_gqa_teacher_forced(batch, oracle):
+    cfg = synth.decoder_config(**GQA)
+    model = synth.decoder_model(cfg, config=66, random_gamma=True)
+    P = 8
+    prompts = synth.decoder_prompts(cfg, batch, P, config=67)
+    print(f"decoder gqa batch={batch}", flush=True)
+    dec = make(cfg, model, batch)
+    dec.start(prompts)
+    orc = oracle.decoder(oracle_cfg(cfg), model)
+    caches = [orc.new_cache() for _ in range(batch)]
+    for pos in range(P):
+        dec.step(1)
+        lg = dec.logits()
+        for b in range(batch):
+            want = orc.step(*caches[b], pos, int(prompts[b][pos]))
+            assert rel(lg[b], want) < TOL, (b, pos, rel(lg[b], want))
+    dec.close()
+
+
 def test_step_limits(small):
     import mythos_oil
     cfg, model = small

@@ -87,6 +87,86 @@ def test_oil8_integer_codebook_bit_exact(oracle, mth, dev):
     assert np.array_equal(y.cpu().numpy(), ref.ravel())
 
 
+def run_oil8(mth, dev, idx, cb, x, M, K, batch):
+    import torch
+    y = empty(batch * M, torch.float32, dev)
+    mth.oil8_gemv(to_dev(idx, dev), to_dev(cb, dev), to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    return y.cpu().numpy().reshape(batch, M)
+
+
+def test_oil8_batched_integer_codebook_bit_exact(oracle, mth, dev):
+    """Batched kernel (FP16 hi/lo products): integer codebook and x keep every
+    product and partial sum an exact integer, so the sum is the reference's
+    bits whatever the order; a dropped or mis-scaled product term shows."""
+    M, K, B = 640, 4096, 16
+    g = np.random.default_rng(6)
+    idx = g.integers(0, 256, (M, K), dtype=np.uint8)
+    cb = (np.arange(256) - 128).astype(np.float32) * 3
+    x = g.integers(-3, 4, (B, K)).astype(np.float32)
+    print(f"oil8_gemv integer M={M} K={K} batch={B}", flush=True)
+    got = run_oil8(mth, dev, idx, cb, x, M, K, B)
+    assert np.array_equal(got, oracle.oil8_gemv(idx, cb, x, M, K, B))
+
+
+def test_oil8_batched_codebook_range(oracle, mth, dev):
+    """Codebook magnitudes over 2^-60 .. 2^40 and per-token activation
+    scales from 2^-40 to 2^40 (every product and sum a normal FP32 number):
+    the power-of-two scales put every hi / lo part in FP16 range, so the FP32
+    bar holds for every token."""
+    M, K, B = 256, 2048, 9
+    g = np.random.default_rng(7)
+    idx = g.integers(0, 256, (M, K), dtype=np.uint8)
+    cb = (g.normal(0, 1, 256) * np.exp2(g.integers(-60, 40, 256))).astype(np.float32)
+    x = (g.normal(0, 1, (B, K)) * np.exp2(np.linspace(-40, 40, B))[:, None]).astype(np.float32)
+    print(f"oil8_gemv range M={M} K={K} batch={B}", flush=True)
+    got = run_oil8(mth, dev, idx, cb, x, M, K, B)
+    ref = oracle.oil8_gemv(idx, cb, x, M, K, B, threads=8)
+    absw = (np.abs(cb[idx]).astype(np.float64) @ np.abs(x.astype(np.float64)).T).T
+    for t in range(B):
+        fp32_close(got[t], ref[t], absw[t], 1e-5, f"oil8 range token {t}")
+
+
+@pytest.mark.parametrize("where", ["codebook_inf", "codebook_nan", "x_inf", "x_nan"])
+def test_oil8_batched_non_finite(where, oracle, mth, dev):
+    """A non-finite codebook entry or activation cannot take the hi / lo
+    split (Inf - Inf is NaN): those workgroups sum the reference's FP32
+    products directly.  Non-finite outputs must match the oracle's class
+    (NaN, +Inf, -Inf); finite ones the FP32 bar."""
+    M, K, B = 300, 1024, 4
+    g = np.random.default_rng(8)
+    idx = g.integers(0, 256, (M, K), dtype=np.uint8)
+    cb = g.normal(0, 0.02, 256).astype(np.float32)
+    x = g.normal(0, 1, (B, K)).astype(np.float32)
+    if where == "codebook_inf":
+        cb[17] = np.inf
+        cb[200] = -np.inf
+        idx[idx == 17] = 18                          # rows 0..99 only see +Inf, rows 100..199 only -Inf
+        idx[idx == 200] = 201
+        idx[:100, 5] = 17
+        idx[100:200, 9] = 200
+    elif where == "codebook_nan":
+        cb[3] = np.nan
+        idx[idx == 3] = 4
+        idx[150:, 100] = 3
+    elif where == "x_inf":
+        x[1, 77] = np.inf
+    else:
+        x[2, 500] = np.nan
+    print(f"oil8_gemv non-finite {where}", flush=True)
+    got = run_oil8(mth, dev, idx, cb, x, M, K, B)
+    with np.errstate(all="ignore"):
+        ref = oracle.oil8_gemv(idx, cb, x, M, K, B, threads=8)
+    fin = np.isfinite(ref)
+    assert (~fin).any()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    with np.errstate(all="ignore"):
+        absw = (np.abs(cb[idx]).astype(np.float64) @ np.abs(x.astype(np.float64)).T).T
+    fp32_close(got[fin], ref[fin], absw[fin], 1e-5, f"oil8 finite outputs ({where})")
+
+
 # ------------------------------------------------------------------ OIL4 --
 @pytest.mark.parametrize("M,K,batch,block", [
     (11008, 4096, 1, 128),   # config 2, b=1
