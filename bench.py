@@ -162,12 +162,16 @@ def bench_ternary_gemm(mth, dev, M, N, K, steps, warmup):
     return dict(sec=sec, steps=n, ops=2.0 * M * N * K, copies=n_cp)
 
 
-def bench_decode(dev, batches=(1, 16)):
+def bench_decode(dev, batches=(1, 16), kv_dtype="bf16"):
     """Config 5: the 32-layer mixed-format decoder, greedy, 64-token random
-    prompts, 128 generated tokens per sequence.  The prompt is fed through the
-    same decode step (64 steps, the last one yielding the first token); the
-    remaining 127 tokens take 127 steps, timed with HIP events on the launch
-    stream.  Each step is one replay of the captured step graph."""
+    prompts, 128 generated tokens per sequence, bf16 KV cache.  The prompt is
+    fed through the same decode step (64 steps, the last one yielding the
+    first token); the remaining 127 tokens take 127 steps, timed with HIP
+    events on the launch stream.  Each step is one replay of the captured step
+    graph.  Roofline bytes per step: every weight byte once plus the KV cache
+    rows the attention reads (positions 0 .. pos-1 of every layer, sequence
+    and kv head, K and V) and the row it appends, averaged over the timed
+    steps."""
     import torch
     import decoder
     import synth
@@ -175,7 +179,7 @@ def bench_decode(dev, batches=(1, 16)):
     t0 = time.time()
     model = synth.decoder_model(cfg, config=5)
     log(f"decode: weights generated in {time.time() - t0:.1f} s")
-    dec = decoder.Decoder(cfg, max_batch=max(batches))
+    dec = decoder.Decoder(cfg, max_batch=max(batches), kv_dtype=kv_dtype)
     dec.load(model)
     H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["layers"]
     layer_bytes = sum(model["layers"][0][k].nbytes for k in ("attn_norm", "ffn_norm", "wq", "cbq", "wk", "cbk", "wv",
@@ -201,13 +205,19 @@ def bench_decode(dev, batches=(1, 16)):
         t_prompt, t_dec = e[0].elapsed_time(e[1]) / 1e3, e[1].elapsed_time(e[2]) / 1e3
         toks = dec.tokens()
         step_ms = t_dec / (G - 1) * 1e3
+        # timed steps run at positions P .. P+G-2: step at pos reads pos cache rows and appends one
+        row = 2 * L * B * cfg["kv_heads"] * cfg["head_dim"] * (2 if kv_dtype == "bf16" else 4)
+        kv_bytes = row * (sum(range(P, P + G - 1)) + (G - 1)) / (G - 1)
         gbs = weight_bytes / (t_dec / (G - 1)) / 1e9
+        tot = (weight_bytes + kv_bytes) / (t_dec / (G - 1)) / 1e9
         out[f"decode_config5_b{B}"] = dict(
             tok_per_s=B * (G - 1) / t_dec, ms_per_step=step_ms, prompt_ms=t_prompt * 1e3,
             end_to_end_tok_per_s=B * G / (t_prompt + t_dec), weight_bytes_per_step=weight_bytes,
-            weight_GBps=gbs, frac=gbs / HBM_PEAK_GBS, generated=int(toks.shape[1] - P),
-            first_tokens=[int(t) for t in toks[0, P:P + 8]])
-        log(f"decode b={B}: {B * (G - 1) / t_dec:.1f} tok/s, {step_ms:.3f} ms/step, weights {gbs:.0f} GB/s")
+            kv_bytes_per_step=kv_bytes, kv_dtype=kv_dtype, weight_GBps=gbs, GBps=tot, frac=tot / HBM_PEAK_GBS,
+            weight_frac=gbs / HBM_PEAK_GBS, launches_per_step=dec.launches_per_step,
+            generated=int(toks.shape[1] - P), first_tokens=[int(t) for t in toks[0, P:P + 8]])
+        log(f"decode b={B}: {B * (G - 1) / t_dec:.1f} tok/s, {step_ms:.3f} ms/step, weights+KV {tot:.0f} GB/s "
+            f"({tot / HBM_PEAK_GBS:.1%}), {dec.launches_per_step} launches/step")
     dec.close()
     return out
 

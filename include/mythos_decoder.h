@@ -97,6 +97,11 @@ int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_str
 /* Steps run since the last start (host-side count). */
 int64_t mth_decoder_steps_done(const mth_decoder* d);
 
+/* Kernel launches of one step: the nodes of the captured step graph (every
+ * node is a kernel), 0 before the first graph step of the started batch.
+ * For measurement (no reference counterpart). */
+int64_t mth_decoder_launches(const mth_decoder* d);
+
 /* Per-layer intermediate values, for parity tests and debugging (no
  * reference counterpart).  With taps non-null, every later step runs its
  * launches directly (no graph) and copies, for layer l, into

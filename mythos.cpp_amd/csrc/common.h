@@ -111,6 +111,58 @@ inline int seg_groups(const Oil8Seg* seg, int nseg, int per_group) {
 __device__ __forceinline__ int seg_of_group(const Oil8SegArgs& a, int g) { return (g >= a.g0[1]) + (g >= a.g0[2]); }
 __device__ __forceinline__ int seg_of_row(const Oil8SegArgs& a, int r) { return (r >= a.off[1]) + (r >= a.off[2]); }
 
+// ---- a batched GEMV's output as its K-slice partial sums ------------------
+// value(t, m) = epi(sum over z < n of p[z*zs + t*ts + m]) with the slices
+// added in the order 0, 1, ... (the order of the GEMVs' own reduction
+// kernels) and epi(v) = (v * scale) * tscale[t] where tscale is set (the
+// I2_S epilogue), else v.  n == 1: the finished output.  A consumer that
+// reads it in place of a reduced array saves the reduction launch.
+struct Slices {
+    const float* p;
+    int64_t ts, zs;
+    int n;
+    float scale;
+    const float* tscale;
+};
+constexpr int kMaxSlices = 16;
+inline Slices plain_slices(const float* y, int64_t ts) { return Slices{y, ts, 0, 1, 1.0f, nullptr}; }
+
+__device__ __forceinline__ float slice_value(const Slices& s, int t, int64_t m) {
+    const float* q = s.p + (int64_t)t * s.ts + m;
+    float v[kMaxSlices];
+#pragma unroll
+    for (int z = 0; z < kMaxSlices; ++z) v[z] = z < s.n ? q[z * s.zs] : 0.0f;  // every load before the first add
+    float sum = v[0];
+#pragma unroll
+    for (int z = 1; z < kMaxSlices; ++z)
+        if (z < s.n) sum += v[z];
+    if (s.tscale) sum = __fmul_rn(__fmul_rn(sum, s.scale), s.tscale[t]);
+    return sum;
+}
+// Four consecutive m (m % 4 == 0; 16-byte aligned rows).
+__device__ __forceinline__ float4 slice_value4(const Slices& s, int t, int64_t m) {
+    const float* q = s.p + (int64_t)t * s.ts + m;
+    float4 v[kMaxSlices];
+#pragma unroll
+    for (int z = 0; z < kMaxSlices; ++z)
+        v[z] = z < s.n ? *(const float4*)(q + z * s.zs) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 sum = v[0];
+#pragma unroll
+    for (int z = 1; z < kMaxSlices; ++z)
+        if (z < s.n) {
+            sum.x += v[z].x;
+            sum.y += v[z].y;
+            sum.z += v[z].z;
+            sum.w += v[z].w;
+        }
+    if (s.tscale) {
+        const float ts = s.tscale[t];
+        sum = make_float4(__fmul_rn(__fmul_rn(sum.x, s.scale), ts), __fmul_rn(__fmul_rn(sum.y, s.scale), ts),
+                          __fmul_rn(__fmul_rn(sum.z, s.scale), ts), __fmul_rn(__fmul_rn(sum.w, s.scale), ts));
+    }
+    return sum;
+}
+
 // ---- int8 helpers ---------------------------------------------------------
 // sum_{i<4} (int8)a.byte[i] * (int8)b.byte[i] + c   (v_dot4_i32_i8)
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

@@ -47,6 +47,7 @@ struct mth_decoder {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int64_t graph_batch = 0, graph_prompt = 0;
+    size_t graph_nodes = 0;
 
     void drop_graph() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -107,11 +108,23 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     do {                                 \
         if ((e = (call)) != hipSuccess) return e; \
     } while (0)
+    using mth::Slices;
+    using mth::plain_slices;
+    // Batches of 2..16 leave the Q/K/V, O and down projections' outputs as
+    // their split-K partial sums (one token group, in the workspace) and the
+    // consumer (the attention, the next norm) adds them: no reduction
+    // launches.
+    // Each partial buffer is read by the launch right after its producer and
+    // only then overwritten.  Taps copy whole outputs, so they take the
+    // reduced path (same sums in the same order).
+    const bool fold = B >= 2 && B <= 16 && !d->taps;
+    const Slices none{nullptr, 0, 0, 0, 1.0f, nullptr};
     const int64_t tap_floats = mth_decoder_tap_floats(d);
     auto tap_copy = [&](float* dst, const void* src, size_t bytes) {
         return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
     };
     TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, B, (int)H, (int)c.vocab, s));
+    Slices resid = none;  // the previous layer's FFN output, added by the next norm
     for (int64_t l = 0; l < c.layers; l++) {
         const mth_decoder_layer& L = d->layers[(size_t)l];
         char* kc = d->kc + l * d->layer_kv * d->kv_elem;
@@ -124,13 +137,30 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         float* tp_inv = tp ? tp_aq + B * F / 4 : nullptr;
         float* tp_down = tp ? tp_inv + B : nullptr;
         // residual of the previous layer's FFN folded into this norm
-        TRY(mth::launch_rms_norm(d->x, l == 0 ? nullptr : d->t, L.attn_norm, d->h, B, H, c.eps, s));
-        TRY(qkv(d, L, s));
-        TRY(mth::launch_rope_attention(d->q, d->k, d->v, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
-                                       d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq,
-                                       s));
-        TRY(oil8(d, L.wo, L.cbo, d->att, d->t, H, QD, s));
-        TRY(mth::launch_rms_norm(d->x, d->t, L.ffn_norm, d->h, B, H, c.eps, s));
+        TRY(mth::launch_rms_norm_slices(d->x, resid, L.attn_norm, d->h, B, H, c.eps, s));
+        // Q, K, V, then RoPE + KV append + attention
+        Slices sq = plain_slices(d->q, QD), sk = plain_slices(d->k, KD), sv = plain_slices(d->v, KD);
+        const mth::Oil8Seg qkv_seg[3] = {{L.wq, L.cbq, d->q, QD}, {L.wk, L.cbk, d->k, KD}, {L.wv, L.cbv, d->v, KD}};
+        if (fold && mth::oil8_bt_segs_fusable(qkv_seg, 3, H, B) && mth::oil8_bt_slices(H) <= mth::kMaxSlices) {
+            Slices o[3];
+            TRY(mth::launch_oil8_gemv_bt_segs_slices(qkv_seg, 3, d->h, H, B, d->bt_partial, o, s));
+            sq = o[0], sk = o[1], sv = o[2];
+        } else {
+            TRY(qkv(d, L, s));
+        }
+        TRY(mth::launch_rope_attention_slices(sq, sk, sv, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
+                                              d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim,
+                                              (int)c.max_seq, s));
+        // O projection; its output is added to the residual by the FFN norm
+        Slices so = plain_slices(d->t, H);
+        const mth::Oil8Seg o_seg{L.wo, L.cbo, d->t, H};
+        if (fold && mth::oil8_bt_segs_fusable(&o_seg, 1, QD, B) && mth::oil8_bt_slices(QD) <= mth::kMaxSlices &&
+            ((uintptr_t)d->att & 15u) == 0) {
+            TRY(mth::launch_oil8_gemv_bt_segs_slices(&o_seg, 1, d->att, QD, B, d->bt_partial, &so, s));
+        } else {
+            TRY(oil8(d, L.wo, L.cbo, d->att, d->t, H, QD, s));
+        }
+        TRY(mth::launch_rms_norm_slices(d->x, so, L.ffn_norm, d->h, B, H, c.eps, s));
         if (tp) TRY(tap_copy(tp, d->x, (size_t)(B * H) * 4));
         const int64_t nb = c.cb_block ? H / c.cb_block : 1;
         const bool fused = L.wup == L.wgate + F * (H / 2) && (c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
@@ -138,9 +168,12 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         // per workgroup of the down projection), then the ternary GEMV on the
         // int8 activations
         if (fused) {
+            const Slices sg = plain_slices(d->gu, 2 * F), su = plain_slices(d->gu + F, 2 * F);
+            // (reduced here: the SwiGLU has one workgroup per token, too few
+            // to read the gate/up slices as fast as the reduction kernel)
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
             if (tp) TRY(tap_copy(tp_gu, d->gu, (size_t)(B * 2 * F) * 4));
-            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + F, d->aq, d->a_inv, tp_act, B, F, 2 * F, 2 * F, s));
+            TRY(mth::launch_silu_mul_quant_slices(sg, su, d->aq, d->a_inv, tp_act, B, F, s));
         } else {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
@@ -152,17 +185,23 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
             }
             TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, tp_act, B, F, F, F, s));
         }
-        if ((((uintptr_t)L.wdown | (uintptr_t)d->aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, B))
-            TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->aq, d->a_inv, d->t, H, F, B, d->bt_partial, s));
-        else
+        resid = plain_slices(d->t, H);
+        if ((((uintptr_t)L.wdown | (uintptr_t)d->aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, B)) {
+            if (fold)
+                TRY(mth::launch_i2s_gemv_bt_slices(L.wdown, L.down_scale, d->aq, d->a_inv, d->t, H, F, B,
+                                                   d->bt_partial, &resid, s));
+            else
+                TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->aq, d->a_inv, d->t, H, F, B, d->bt_partial, s));
+        } else {
             TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, B, s));
+        }
         if (tp) {
             TRY(tap_copy(tp_aq, d->aq, (size_t)(B * F)));
             TRY(tap_copy(tp_inv, d->a_inv, (size_t)B * 4));
             TRY(tap_copy(tp_down, d->t, (size_t)(B * H) * 4));
         }
     }
-    TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
+    TRY(mth::launch_rms_norm_slices(d->x, resid, d->g.final_norm, d->h, B, H, c.eps, s));
     TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
     TRY(mth::launch_argmax(d->logits, B, c.vocab, d->ids, d->hist, d->step, (int)d->hist_stride, (int)d->prompt_len,
                            d->arg_v, d->arg_i, s));
@@ -340,6 +379,7 @@ int mth_decoder_step(mth_decoder* d, int64_t n, int use_graph, mth_stream_t stre
                 e = hipStreamEndCapture(d->cap_stream, &d->graph);
                 if (le != hipSuccess) e = le;
             }
+            if (e == hipSuccess) e = hipGraphGetNodes(d->graph, nullptr, &d->graph_nodes);
             if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
             if (e != hipSuccess) {
                 d->drop_graph();
@@ -379,6 +419,8 @@ int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_str
 }
 
 int64_t mth_decoder_steps_done(const mth_decoder* d) { return d ? d->steps : 0; }
+
+int64_t mth_decoder_launches(const mth_decoder* d) { return d && d->exec ? (int64_t)d->graph_nodes : 0; }
 
 int64_t mth_decoder_tap_floats(const mth_decoder* d) {
     if (!d) return 0;

@@ -74,17 +74,18 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // x and y may be the same array (in-place normalisation): each thread reads
 // its own elements before it writes them.
 constexpr int kRN = 1024;  // threads of the float4 RMSNorm (one float4 each at dim 4096)
-__global__ __launch_bounds__(kRN) void rms_norm_k(float* x, const float* __restrict__ t,
-                                                  const float* __restrict__ gamma, float* y, int dim, float eps) {
+// t: the residual as Slices (common.h; t.n == 0: none), so the split-K
+// partial sums of the GEMV that produced it are added here.
+__global__ __launch_bounds__(kRN) void rms_norm_k(float* x, Slices t, const float* __restrict__ gamma, float* y,
+                                                  int dim, float eps) {
     __shared__ double red[kRN / 64];
     float* xr = x + (int64_t)blockIdx.x * dim;
-    const float* tr = t ? t + (int64_t)blockIdx.x * dim : nullptr;
     float* yr = y + (int64_t)blockIdx.x * dim;
     double ss = 0.0;
     for (int i = threadIdx.x * 4; i < dim; i += kRN * 4) {
         float4 v = ldf4(xr + i);
-        if (tr) {
-            const float4 a = ldf4(tr + i);
+        if (t.n) {
+            const float4 a = slice_value4(t, blockIdx.x, i);
             v = make_float4((a.x + v.x), (a.y + v.y), (a.z + v.z), (a.w + v.w));
             *(float4*)(xr + i) = v;
         }
@@ -110,18 +111,16 @@ __global__ __launch_bounds__(kRN) void rms_norm_k(float* x, const float* __restr
 }
 
 // Generic-width variant (dim % 4 != 0 or unaligned rows).
-__global__ __launch_bounds__(kT) void rms_norm_any_k(float* x, const float* __restrict__ t,
-                                                     const float* __restrict__ gamma, float* y, int64_t dim,
-                                                     float eps) {
+__global__ __launch_bounds__(kT) void rms_norm_any_k(float* x, Slices t, const float* __restrict__ gamma, float* y,
+                                                     int64_t dim, float eps) {
     __shared__ double red[4];
     float* xr = x + (int64_t)blockIdx.x * dim;
-    const float* tr = t ? t + (int64_t)blockIdx.x * dim : nullptr;
     float* yr = y + (int64_t)blockIdx.x * dim;
     double ss = 0.0;
     for (int64_t i = threadIdx.x; i < dim; i += kT) {
         float v = xr[i];
-        if (tr) {
-            v = (tr[i] + v);
+        if (t.n) {
+            v = (slice_value(t, blockIdx.x, i) + v);
             xr[i] = v;
         }
         ss += (double)v * v;
@@ -231,37 +230,49 @@ __device__ __forceinline__ uint16_t kv_store_value(float v, uint16_t) { return b
 __device__ __forceinline__ float kv_rounded(float v, float) { return v; }
 __device__ __forceinline__ float kv_rounded(float v, uint16_t) { return __uint_as_float((uint32_t)bf16_rne(v) << 16); }
 __device__ __forceinline__ float4 kv_load4(const float* p) { return *(const float4*)p; }
-__device__ __forceinline__ float4 kv_load4(const uint16_t* p) {
-    const uint2 w = *(const uint2*)p;
+__device__ __forceinline__ float4 kv_widen(const uint2& w) {
     return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
                        __uint_as_float(w.y & 0xffff0000u));
 }
+__device__ __forceinline__ float4 kv_widen(const float4& v) { return v; }
+__device__ __forceinline__ float4 kv_load4(const uint16_t* p) { return kv_widen(*(const uint2*)p); }
+// four elements as loaded (bf16 stays packed until used)
+template <typename KV> struct KvRaw4 { typedef float4 type; };
+template <> struct KvRaw4<uint16_t> { typedef uint2 type; };
+__device__ __forceinline__ float4 kv_raw4(const float* p) { return *(const float4*)p; }
+__device__ __forceinline__ uint2 kv_raw4(const uint16_t* p) { return *(const uint2*)p; }
 
 // ---- decode attention --------------------------------------------------------
 // Workgroup (head h, token b) over ctx = *step + ctx0 + 1 positions of kv
 // head kh = h % kv_heads, cache rows [b][kh][t][D].
-// Scores: one position per thread (t = tid, tid + 256, ...), the dot product
-// over d in order with separate multiply and add (the reference's scalar
-// loop, src/transformer.cpp:200-232), K rows as float4 loads, q broadcast
-// from LDS: every thread has its whole row in flight at once.  Softmax in
-// LDS.  P*V: thread = (float4 column group, position slice); slices are
-// summed through LDS in a fixed order.
-// ROPE: the current token's q/k/v (pre-rotation, [B][heads*D] and
-// [B][kv_heads*D]) are rotated here (RotaryEmbedding::apply), the current
-// position's k/v come from LDS, and the workgroup with h < kv_heads writes
-// them to the cache row pos (KVCache::append) -- no workgroup reads that row
-// from memory in this launch.  Without ROPE, q is already rotated and all
-// ctx rows come from the cache.
+// Latency, not bandwidth, bounds this kernel at decode sizes, so the cache
+// rows are loaded as early as their order of use allows (the CU returns
+// loads in issue order): first each thread's K row of the first 256
+// positions, then the V rows it accumulates in P*V (up to VP of them,
+// positions sl + SL j, kept packed), so the scores wait only for K and the
+// V rows arrive during the softmax.  Scores: one position per thread, the
+// dot product over d in four interleaved FP32 partial sums (d mod 4) added
+// pairwise, q broadcast from LDS.  Softmax in LDS.  P*V: thread = (float4
+// column group g, position slice sl), four accumulators; slices are summed
+// through LDS in a fixed order.
+// ROPE: the current token's q/k/v (pre-rotation, the Q/K/V projection
+// outputs read as Slices, common.h: [B][heads*D] and [B][kv_heads*D] or
+// their split-K partial sums) are rotated here (RotaryEmbedding::apply), the
+// current position's k/v come from LDS, and the workgroup with h < kv_heads
+// writes them to the cache row pos (KVCache::append) -- no workgroup reads
+// that row from memory in this launch.  Without ROPE, q is already rotated
+// and all ctx rows come from the cache.
 // KV: the cache element type (float, or uint16_t holding bf16 bits); with
 // bf16, the current position's k/v are rounded in LDS as the cache stores them.
 template <int D, bool ROPE, typename KV>
-__global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, const float* __restrict__ kin,
-                                                  const float* __restrict__ vin, const float* __restrict__ cos_t,
+__global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices vin, const float* __restrict__ cos_t,
                                                   const float* __restrict__ sin_t, KV* kc, KV* vc,
                                                   float* __restrict__ out, const int* __restrict__ step, int ctx0,
                                                   int heads, int kv_heads, int max_seq, float scale) {
+    typedef typename KvRaw4<KV>::type Raw;
     constexpr int G = D / 4;        // float4 column groups
     constexpr int SL = kT / G;      // position slices in P*V
+    constexpr int VP = (sizeof(KV) == 2 ? 16 : 8) * 128 / D;  // V rows per thread held in registers
     extern __shared__ float sc[];   // [max_seq] scores, then probabilities
     __shared__ __align__(16) float qs[D], ks[D], vs[D];
     __shared__ float4 part[SL][G];
@@ -271,54 +282,85 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
     const int ctx = pos + 1;
     const int kh = h % kv_heads;
     const int64_t crow = ((int64_t)b * kv_heads + kh) * max_seq;  // cache row of position 0
-    const float* qh = q + ((int64_t)b * heads + h) * D;
+    const int nmem = ROPE ? pos : ctx;  // positions read from the cache
+    const int g = tid % G, sl = tid / G;
+
     if (ROPE) {
         const float* cr = cos_t + (int64_t)pos * (D / 2);
         const float* sr = sin_t + (int64_t)pos * (D / 2);
-        const float* kh_in = kin + ((int64_t)b * kv_heads + kh) * D;
-        const float* vh_in = vin + ((int64_t)b * kv_heads + kh) * D;
         if (tid < D / 2) {
             const float c = cr[tid], s = sr[tid];
-            const float q1 = qh[tid], q2 = qh[tid + D / 2];
+            const float q1 = slice_value(q, b, h * D + tid), q2 = slice_value(q, b, h * D + tid + D / 2);
             qs[tid] = q1 * c - q2 * s;
             qs[tid + D / 2] = q1 * s + q2 * c;
-            const float k1 = kh_in[tid], k2 = kh_in[tid + D / 2];
+            const float k1 = slice_value(kin, b, kh * D + tid), k2 = slice_value(kin, b, kh * D + tid + D / 2);
             ks[tid] = kv_rounded(k1 * c - k2 * s, KV{});
             ks[tid + D / 2] = kv_rounded(k1 * s + k2 * c, KV{});
-            vs[tid] = kv_rounded(vh_in[tid], KV{});
-            vs[tid + D / 2] = kv_rounded(vh_in[tid + D / 2], KV{});
-        }
-        __syncthreads();
-        if (h < kv_heads && tid < D) {
-            kc[(crow + pos) * D + tid] = kv_store_value(ks[tid], KV{});
-            vc[(crow + pos) * D + tid] = kv_store_value(vs[tid], KV{});
+            vs[tid] = kv_rounded(slice_value(vin, b, kh * D + tid), KV{});
+            vs[tid + D / 2] = kv_rounded(slice_value(vin, b, kh * D + tid + D / 2), KV{});
         }
     } else {
-        if (tid < D) qs[tid] = qh[tid];
-        __syncthreads();
+        if (tid < D) qs[tid] = slice_value(q, b, h * D + tid);
     }
-    const int nmem = ROPE ? pos : ctx;  // positions read from the cache
-    auto dot = [&](auto kr) {
-        float s = 0.0f;
+    // cache rows: this thread's K row of the first tile, then its V rows
+    Raw kr0[D / 4];
+    const bool has0 = tid < nmem;
+    {
+        const KV* kr = kc + (crow + (has0 ? tid : 0)) * D;
 #pragma unroll
-        for (int d = 0; d < D; d += 4) {
-            const float4 k4 = kv_load4(kr + d);
-            const float4 q4 = *(const float4*)(qs + d);
-            s = s + q4.x * k4.x;
-            s = s + q4.y * k4.y;
-            s = s + q4.z * k4.z;
-            s = s + q4.w * k4.w;
+        for (int d = 0; d < D / 4; ++d) kr0[d] = kv_raw4(kr + 4 * d);
+    }
+    const KV* vcol = vc + crow * D + 4 * g;
+    Raw vpre[VP];
+#pragma unroll
+    for (int j = 0; j < VP; ++j) {
+        const int t = sl + SL * j;
+        vpre[j] = kv_raw4(vcol + (int64_t)(t < nmem ? t : 0) * D);
+    }
+    __syncthreads();  // qs, ks, vs
+    if (ROPE && h < kv_heads && tid < D) {
+        kc[(crow + pos) * D + tid] = kv_store_value(ks[tid], KV{});
+        vc[(crow + pos) * D + tid] = kv_store_value(vs[tid], KV{});
+    }
+    auto dot_raw = [&](const Raw* kr) {
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D / 4; ++d) {
+            const float4 k4 = kv_widen(kr[d]);
+            const float4 q4 = *(const float4*)(qs + 4 * d);
+            s0 = s0 + q4.x * k4.x;
+            s1 = s1 + q4.y * k4.y;
+            s2 = s2 + q4.z * k4.z;
+            s3 = s3 + q4.w * k4.w;
         }
-        return s * scale;
+        return ((s0 + s1) + (s2 + s3)) * scale;
     };
     float mx = -INFINITY;
-    for (int t = tid; t < nmem; t += kT) {
-        const float s = dot(kc + (crow + t) * D);
+    if (has0) {
+        const float s = dot_raw(kr0);
+        sc[tid] = s;
+        mx = s;
+    }
+    for (int t = tid + kT; t < nmem; t += kT) {
+        Raw kr[D / 4];
+#pragma unroll
+        for (int d = 0; d < D / 4; ++d) kr[d] = kv_raw4(kc + (crow + t) * D + 4 * d);
+        const float s = dot_raw(kr);
         sc[t] = s;
         mx = fmaxf(mx, s);
     }
     if (ROPE && tid == (pos % kT)) {  // the current position, from LDS
-        const float s = dot((const float*)ks);
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; d += 4) {
+            const float4 k4 = *(const float4*)(ks + d);
+            const float4 q4 = *(const float4*)(qs + d);
+            s0 = s0 + q4.x * k4.x;
+            s1 = s1 + q4.y * k4.y;
+            s2 = s2 + q4.z * k4.z;
+            s3 = s3 + q4.w * k4.w;
+        }
+        const float s = ((s0 + s1) + (s2 + s3)) * scale;
         sc[pos] = s;
         mx = fmaxf(mx, s);
     }
@@ -331,8 +373,6 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
     }
     sum = block_sum(sum, redf);   // its barriers also publish sc[]
     const float inv = 1.0f / sum;
-    const int g = tid % G, sl = tid / G;
-    // four independent accumulators keep four rows of V in flight per thread
     float4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -342,8 +382,12 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
         a.z = fmaf(p, v.z, a.z);
         a.w = fmaf(p, v.w, a.w);
     };
-    const KV* vcol = vc + crow * D + 4 * g;
-    int t = sl;
+#pragma unroll
+    for (int j = 0; j < VP; ++j) {
+        const int t = sl + SL * j;
+        if (t < nmem) axpy(acc[j & 3], sc[t] * inv, kv_widen(vpre[j]));
+    }
+    int t = sl + SL * VP;
     for (; t + 3 * SL < nmem; t += 4 * SL) {
         float4 v4[4];
 #pragma unroll
@@ -379,20 +423,30 @@ __global__ __launch_bounds__(kT) void attention_k(const float* __restrict__ q, c
 // q = (int8)round_half_away(a * scale), inv = max/127.  n <= kSQT * kSQ.
 constexpr int kSQT = 1024, kSQ = 12;
 // act (optional): the FP32 activations, [rows][n].
-__global__ __launch_bounds__(kSQT) void silu_mul_quant_k(const float* __restrict__ g, const float* __restrict__ u,
-                                                         int8_t* __restrict__ q, float* __restrict__ inv_scale,
-                                                         float* __restrict__ act, int n, int64_t gstride,
-                                                         int64_t ustride) {
+// g, u: the gate and up outputs as Slices (common.h), so the split-K
+// partial sums of the GEMV are added here.
+__global__ __launch_bounds__(kSQT) void silu_mul_quant_k(Slices g, Slices u, int8_t* __restrict__ q,
+                                                         float* __restrict__ inv_scale, float* __restrict__ act,
+                                                         int n) {
     __shared__ float red[kSQT / 64];
     const int r = blockIdx.x, tid = threadIdx.x;
-    const float* gr = g + r * gstride;
-    const float* ur = u + r * ustride;
     float gv[kSQ], uv[kSQ];
+    if (g.n == 1 && u.n == 1) {
+        const float* gr = g.p + r * g.ts;
+        const float* ur = u.p + r * u.ts;
 #pragma unroll
-    for (int j = 0; j < kSQ; ++j) {
-        const int i = tid + j * kSQT;
-        gv[j] = i < n ? gr[i] : 0.0f;
-        uv[j] = i < n ? ur[i] : 0.0f;
+        for (int j = 0; j < kSQ; ++j) {
+            const int i = tid + j * kSQT;
+            gv[j] = i < n ? gr[i] : 0.0f;
+            uv[j] = i < n ? ur[i] : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kSQ; ++j) {
+            const int i = tid + j * kSQT;
+            gv[j] = i < n ? slice_value(g, r, i) : 0.0f;
+            uv[j] = i < n ? slice_value(u, r, i) : 0.0f;
+        }
     }
     float m = 0.0f;
 #pragma unroll
@@ -523,13 +577,20 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
-hipError_t launch_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim,
-                           float eps, hipStream_t s) {
-    if (dim % 4 == 0 && dim < (1ll << 31) && al16(x) && al16(y) && al16(gamma) && (!t || al16(t)))
+hipError_t launch_rms_norm_slices(float* x, const Slices& t, const float* gamma, float* y, int64_t rows, int64_t dim,
+                                  float eps, hipStream_t s) {
+    const bool t_al = t.n == 0 || (al16(t.p) && t.ts % 4 == 0 && t.zs % 4 == 0);
+    if (dim % 4 == 0 && dim < (1ll << 31) && al16(x) && al16(y) && al16(gamma) && t_al)
         rms_norm_k<<<(unsigned)rows, kRN, 0, s>>>(x, t, gamma, y, (int)dim, eps);
     else
         rms_norm_any_k<<<(unsigned)rows, kT, 0, s>>>(x, t, gamma, y, dim, eps);
     return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim,
+                           float eps, hipStream_t s) {
+    const Slices ts = t ? plain_slices(t, dim) : Slices{nullptr, 0, 0, 0, 1.0f, nullptr};
+    return launch_rms_norm_slices(x, ts, gamma, y, rows, dim, eps, s);
 }
 
 hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t n, int64_t gstride,
@@ -571,7 +632,7 @@ bool attention_supported(int head_dim, int max_seq) {
 }
 
 template <bool ROPE, typename KV>
-static hipError_t run_attention(const float* q, const float* k, const float* v, const float* cos_t,
+static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
                                 const float* sin_t, KV* kc, KV* vc, float* out, const int* step, int ctx0,
                                 int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
     const float scale = 1.0f / sqrtf((float)head_dim);
@@ -591,13 +652,24 @@ static hipError_t run_attention(const float* q, const float* k, const float* v, 
 
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
                             int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
-    return run_attention<false, float>(q, nullptr, nullptr, nullptr, nullptr, (float*)kc, (float*)vc, out, step,
-                                       ctx0, batch, heads, kv_heads, head_dim, max_seq, s);
+    const Slices qs = plain_slices(q, (int64_t)heads * head_dim), none{nullptr, 0, 0, 0, 1.0f, nullptr};
+    return run_attention<false, float>(qs, none, none, nullptr, nullptr, (float*)kc, (float*)vc, out, step, ctx0,
+                                       batch, heads, kv_heads, head_dim, max_seq, s);
 }
 
 hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
                                  const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out, const int* step,
                                  int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
+    return launch_rope_attention_slices(plain_slices(q, (int64_t)heads * head_dim),
+                                        plain_slices(k, (int64_t)kv_heads * head_dim),
+                                        plain_slices(v, (int64_t)kv_heads * head_dim), cos_t, sin_t, kc, vc, kv_bf16,
+                                        out, step, batch, heads, kv_heads, head_dim, max_seq, s);
+}
+
+hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
+                                        const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out,
+                                        const int* step, int64_t batch, int heads, int kv_heads, int head_dim,
+                                        int max_seq, hipStream_t s) {
     if (kv_bf16)
         return run_attention<true, uint16_t>(q, k, v, cos_t, sin_t, (uint16_t*)kc, (uint16_t*)vc, out, step, 0,
                                              batch, heads, kv_heads, head_dim, max_seq, s);
@@ -607,10 +679,16 @@ hipError_t launch_rope_attention(const float* q, const float* k, const float* v,
 
 bool silu_mul_quant_supported(int64_t n) { return n > 0 && n <= (int64_t)kSQT * kSQ; }
 
+hipError_t launch_silu_mul_quant_slices(const Slices& g, const Slices& u, int8_t* q, float* inv_scale, float* act,
+                                        int64_t rows, int64_t n, hipStream_t s) {
+    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, q, inv_scale, act, (int)n);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, float* act,
                                  int64_t rows, int64_t n, int64_t gstride, int64_t ustride, hipStream_t s) {
-    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, q, inv_scale, act, (int)n, gstride, ustride);
-    return hipGetLastError();
+    return launch_silu_mul_quant_slices(plain_slices(g, gstride), plain_slices(u, ustride), q, inv_scale, act, rows,
+                                        n, s);
 }
 
 int argmax_chunks(int64_t n) { return (int)((n + kArgChunk - 1) / kArgChunk); }

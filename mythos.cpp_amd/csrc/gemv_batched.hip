@@ -188,7 +188,7 @@ inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // dot product to FP32 accuracy.  Three FP16 MFMAs cost a sixth of the
 // sixteen FP32 MFMAs (v_mfma_f32_16x16x4_f32) the same 512 products take.
 //
-// Tiling.  Workgroup = 4 waves x NT tiles of 16 rows, one K slice of
+// Tiling.  Workgroup = WV waves x NT tiles of 16 rows, one K slice of
 // 128 PH columns.  Per 128-column phase a wave loads each tile in two
 // 128-byte-per-row instructions (rows 0-7, rows 8-15, 8 lanes per row) and
 // a DPP row rotation hands lane (j = l % 16, q = l / 16) the 32 index bytes
@@ -197,16 +197,17 @@ inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // 256-entry table of (hi, lo) pairs sits in LDS (one ds_read_b32 gather per
 // weight gives both parts); the slice's activations for 16 tokens are
 // converted once into hi / lo B fragments in LDS (8 KB per phase) and read
-// by all waves, so the main loop has no barrier.  All weight loads of the
-// slice are issued before the conversion.  Slices (grid.y) write partial
-// sums that oil8_seg_reduce adds in slice order (deterministic).
+// by all waves, so the main loop has no barrier.  Every load is issued up
+// front, activations of all waves before any weights (see the kernel).
+// Slices (grid.y) write partial sums that oil8_seg_reduce adds in slice
+// order (deterministic).
 //
 // Non-finite values.  Inf cannot be split (Inf - Inf is NaN), so a
 // workgroup whose codebook or activations hold a non-finite value computes
 // its outputs with FP32 FMAs over the reference's products in column order
 // instead (a uniform branch; same outputs up to the summation order).
 constexpr int kH3Tok = 16;
-constexpr int kH3Hdr = 1280;   // table (1 KB), token shifts, wave maxima
+constexpr int kH3Hdr = 1280;   // table (1 KB), token maxima, wave maxima
 constexpr int kH3Phase = 8192; // B of one 128-column phase: hi 4 KB, then lo 4 KB
 
 // B slot (MFMA m, column group q, token n): 16 bytes, tokens XOR-permuted
@@ -234,63 +235,73 @@ __device__ __forceinline__ uint32_t h3_pair(float c) {
     return (uint32_t)__builtin_bit_cast(uint16_t, h) | ((uint32_t)__builtin_bit_cast(uint16_t, l) << 16);
 }
 
-template <int NT, int PH>
-__global__ __launch_bounds__(256) void oil8_gemv_h3(Oil8SegArgs sg, const float* x, float* __restrict__ partial,
-                                                    int K, int batch) {
+template <int WV, int NT, int PH>
+__global__ __launch_bounds__(WV * 64) void oil8_gemv_h3(Oil8SegArgs sg, const float* x, float* __restrict__ partial,
+                                                        int K, int batch) {
     constexpr int KS = 128 * PH;
+    constexpr int XG = WV / 4;          // thread groups of 256; phase p is converted by group p % XG
+    constexpr int XP = PH / XG;         // phases converted per thread
+    static_assert(PH % XG == 0, "phases split over the thread groups");
     __shared__ __align__(16) uint8_t lds[kH3Hdr + PH * kH3Phase];
     uint32_t* tab = (uint32_t*)lds;
-    int* shifts = (int*)(lds + 1024);
-    float* wmax = (float*)(lds + 1024 + 4 * kH3Tok);
+    float* tmax = (float*)(lds + 1024);          // [XG][16] token maxima
+    float* wmax = (float*)(lds + 1024 + 4 * 2 * kH3Tok);
     uint8_t* bsm = lds + kH3Hdr;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
     const int sgi = seg_of_group(sg, blockIdx.x);
     const uint8_t* idx = sg.idx[sgi];
     const int M = sg.rows[sgi];
-    const int row0w = (blockIdx.x - sg.g0[sgi]) * (64 * NT) + wave * 16 * NT;
+    const int row0w = (blockIdx.x - sg.g0[sgi]) * (WV * 16 * NT) + wave * 16 * NT;
     const int k0 = blockIdx.y * KS;
 
-    // ---- activations of the slice (thread -> token tt, columns 8u .. 8u+7
-    // of every phase), the thread's codebook entry, then every weight load
-    const int tt = tid >> 4, u = tid & 15;
+    // ---- loads.  The CU returns loads in issue order, across its waves: so
+    // every wave first issues the small operands (its codebook entry and the
+    // activations it converts: token tt, columns 8u .. 8u+7 of the phases
+    // p = xg, xg + XG, ...), and only after a barrier the weights, phase by
+    // phase with a barrier between phases.  The activations then arrive
+    // ahead of the weight stream and are converted while it streams, and
+    // each phase's MFMAs wait only for that phase.
+    const int tt = (tid >> 4) & 15, u = tid & 15, xg = tid >> 8;
     const bool tok = tt < batch;
     const float* xr = x + (int64_t)(tok ? tt : 0) * K + k0 + 8 * u;
-    float4 xa[PH], xb[PH];
+    const float cbv = sg.cb[sgi][tid & 255];
+    float4 xa[XP], xb[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        xa[i] = ldf4(xr + 128 * (XG * i + xg));
+        xb[i] = ldf4(xr + 128 * (XG * i + xg) + 4);
+    }
+    const uint8_t* px[NT];
+    const uint8_t* py[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        px[t] = idx + (int64_t)min(row0w + 16 * t + jj8, M - 1) * K + k0 + 16 * (2 * q + hi8);
+        py[t] = idx + (int64_t)min(row0w + 16 * t + 8 + jj8, M - 1) * K + k0 + 16 * (2 * q + hi8);
+    }
+    uint4 wx[NT][PH], wy[NT][PH];
 #pragma unroll
     for (int p = 0; p < PH; ++p) {
-        xa[p] = ldf4(xr + 128 * p);
-        xb[p] = ldf4(xr + 128 * p + 4);
-    }
-    const float cbv = sg.cb[sgi][tid];
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 wx[NT][PH], wy[NT][PH];
-    {
-        const uint8_t* px[NT];
-        const uint8_t* py[NT];
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            px[t] = idx + (int64_t)min(row0w + 16 * t + jj8, M - 1) * K + k0 + 16 * (2 * q + hi8);
-            py[t] = idx + (int64_t)min(row0w + 16 * t + 8 + jj8, M - 1) * K + k0 + 16 * (2 * q + hi8);
+            wx[t][p] = ld_stream(px[t] + 128 * p);
+            wy[t][p] = ld_stream(py[t] + 128 * p);
         }
-#pragma unroll
-        for (int p = 0; p < PH; ++p)
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                wx[t][p] = ld_stream(px[t] + 128 * p);
-                wy[t][p] = ld_stream(py[t] + 128 * p);
-            }
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- scales: token max over the slice (its 16 threads form one DPP
-    // row), codebook max over the workgroup; any non-finite value -> FMA path
+    // ---- scales: token max over the slice (16 threads of one DPP row per
+    // phase group, then the groups through LDS), codebook max over the first
+    // 256 threads; any non-finite value -> FMA path
     float xm = 0.0f;
     bool fin = __builtin_isfinite(cbv);
     if (tok) {
 #pragma unroll
-        for (int p = 0; p < PH; ++p) {
-            const float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+        for (int i = 0; i < XP; ++i) {
+            const float v[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 xm = fmaxf(xm, fabsf(v[e]));
@@ -298,20 +309,27 @@ __global__ __launch_bounds__(256) void oil8_gemv_h3(Oil8SegArgs sg, const float*
             }
         }
     }
-    const int sx = fp16_scale_shift(row16_max(xm));
+    xm = row16_max(xm);
     const float cm = wave_max(fabsf(cbv));
-    if (lane == 0) wmax[wave] = cm;
-    if (u == 0) shifts[tt] = sx;
+    if (wave < 4 && lane == 0) wmax[wave] = cm;
+    if (u == 0) tmax[xg * kH3Tok + tt] = xm;
     const bool special = __syncthreads_or(!fin) != 0;
 
-    floatx4 acc[NT];
-    int unscale = 0;
+    auto token_shift = [&](int n) {
+        float m = tmax[n];
+#pragma unroll
+        for (int g = 1; g < XG; ++g) m = fmaxf(m, tmax[g * kH3Tok + n]);
+        return fp16_scale_shift(m);
+    };
+    floatx4 ysum[NT];
     if (!special) {
         const int sw = fp16_scale_shift(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
-        tab[tid] = h3_pair(ldexpf(cbv, sw));
+        if (tid < 256) tab[tid] = h3_pair(ldexpf(cbv, sw));
+        const int sx = token_shift(tt);
 #pragma unroll
-        for (int p = 0; p < PH; ++p) {
-            const float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+        for (int i = 0; i < XP; ++i) {
+            const int p = XG * i + xg;
+            const float v[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
             half8 vh, vl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -326,6 +344,7 @@ __global__ __launch_bounds__(256) void oil8_gemv_h3(Oil8SegArgs sg, const float*
         }
         __syncthreads();
 
+        floatx4 acc[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -362,9 +381,16 @@ __global__ __launch_bounds__(256) void oil8_gemv_h3(Oil8SegArgs sg, const float*
                 }
             }
         }
-        unscale = sw + shifts[j];
-    } else {
-        // FP32 FMAs over the slice's columns in order (rows 4q + i, token j)
+        const int un = sw + token_shift(j);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ysum[t][i] = ldexpf(acc[t][i], -un);
+    }
+
+    if (special) {
+        // a non-finite codebook entry or activation: FP32 FMAs over the
+        // slice's columns in order instead (rows 4q + i, token j)
         const float* cb = sg.cb[sgi];
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -377,24 +403,30 @@ __global__ __launch_bounds__(256) void oil8_gemv_h3(Oil8SegArgs sg, const float*
                     const float* xx = x + (int64_t)j * K + k0;
                     for (int k = 0; k < KS; ++k) sum = fmaf(cb[wr[k]], xx[k], sum);
                 }
-                acc[t][i] = sum;
+                ysum[t][i] = sum;
             }
     }
 
-    // ---- D[4q + i][j]: rows row0w + 16t + 4q + i, token j
+    // ---- D[4q + i][j]: rows row0w + 16t + 4q + i of token j, consecutive in
+    // y and in the partial layout [slice][token][rows]: one 16-byte store
+    // where all four rows exist and the address is aligned
     if (j >= batch) return;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0w + 16 * t + 4 * q + i;
-            if (row >= M) continue;
-            const float v = ldexpf(acc[t][i], -unscale);
-            if (gridDim.y == 1)
-                sg.y[sgi][(int64_t)j * M + row] = v;
-            else
-                partial[((int64_t)blockIdx.y * kH3Tok + j) * sg.mtot + sg.off[sgi] + row] = v;
+    for (int t = 0; t < NT; ++t) {
+        const int row = row0w + 16 * t + 4 * q;
+        if (row >= M) continue;
+        float* dst = gridDim.y == 1 ? sg.y[sgi] + (int64_t)j * M + row
+                                    : partial + ((int64_t)blockIdx.y * kH3Tok + j) * sg.mtot + sg.off[sgi] + row;
+        const float4 v = make_float4(ysum[t][0], ysum[t][1], ysum[t][2], ysum[t][3]);
+        if (row + 3 < M && ((uintptr_t)dst & 15u) == 0) {
+            *(float4*)dst = v;
+        } else {
+            dst[0] = v.x;
+            if (row + 1 < M) dst[1] = v.y;
+            if (row + 2 < M) dst[2] = v.z;
+            if (row + 3 < M) dst[3] = v.w;
         }
+    }
 }
 
 // y of segment s, token t, row r = sum over slices z = 0, 1, ... of
@@ -422,16 +454,24 @@ __global__ __launch_bounds__(256) void oil8_seg_reduce(const float* __restrict__
 // phases of 128 columns per K slice
 inline int h3_phases(int64_t K) { return K % 512 == 0 ? 4 : (K % 256 == 0 ? 2 : 1); }
 
-// tiles per wave: two once the grid has enough workgroups without them
-inline int h3_tiles(int groups64, int64_t slices) { return (int64_t)groups64 * slices >= 2048 ? 2 : 1; }
-
-template <int NT, int PH>
-void run_h3(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int b, float* partial, hipStream_t s) {
-    const Oil8SegArgs a = make_seg_args(seg, nseg, 64 * NT);
+template <int WV, int NT, int PH>
+void run_h3(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int b, float* partial, bool reduce,
+            hipStream_t s) {
+    const Oil8SegArgs a = make_seg_args(seg, nseg, WV * 16 * NT);
     const int S = (int)(K / (128 * PH));
-    const dim3 grid((unsigned)seg_groups(seg, nseg, 64 * NT), (unsigned)S);
-    oil8_gemv_h3<NT, PH><<<grid, 256, 0, s>>>(a, x, partial, (int)K, b);
-    if (S > 1) oil8_seg_reduce<<<ceil_div_i((int64_t)b * a.mtot, 256), 256, 0, s>>>(partial, a, b, S);
+    const dim3 grid((unsigned)seg_groups(seg, nseg, WV * 16 * NT), (unsigned)S);
+    oil8_gemv_h3<WV, NT, PH><<<grid, WV * 64, 0, s>>>(a, x, partial, (int)K, b);
+    if (S > 1 && reduce) oil8_seg_reduce<<<ceil_div_i((int64_t)b * a.mtot, 256), 256, 0, s>>>(partial, a, b, S);
+}
+
+// 8 waves (128 rows) share one activation staging where the phases split
+// over two thread groups
+void h3_dispatch(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int b, float* partial, bool reduce,
+                 hipStream_t s) {
+    const int ph = h3_phases(K);
+    if (ph == 4) run_h3<8, 1, 4>(seg, nseg, x, K, b, partial, reduce, s);
+    else if (ph == 2) run_h3<8, 1, 2>(seg, nseg, x, K, b, partial, reduce, s);
+    else run_h3<4, 1, 1>(seg, nseg, x, K, b, partial, reduce, s);
 }
 
 // phases of 256 columns per K slice: 4 (K a multiple of 1024, K >= 2048) or 2
@@ -439,12 +479,23 @@ inline int bt_nph(int64_t K) { return (K >= 2048 && K % 1024 == 0) ? 4 : 2; }
 
 template <int NPH, bool SHARED>
 void run_bt(const uint8_t* nib, const uint16_t* cbs, const float* x, float* y, float* partial, int64_t M, int64_t K,
-            int batch, hipStream_t s) {
+            int batch, bool reduce, hipStream_t s) {
     const int nslice = (int)(K / (256 * NPH));
     const dim3 grid(ceil_div_i(M, kBtRows), (unsigned)nslice);
     oil4_gemv_bt<NPH, SHARED><<<grid, 256, 0, s>>>(nib, cbs, x, y, partial, (int)M, (int)K, batch);
-    if (nslice > 1)
+    if (nslice > 1 && reduce)
         oil4_bt_reduce<<<ceil_div_i((int64_t)batch * M, 256), 256, 0, s>>>(partial, y, (int)M, batch, nslice);
+}
+
+void bt_dispatch(const uint8_t* nib, const uint16_t* cbs, bool sh, const float* x, float* y, float* partial,
+                 int64_t M, int64_t K, int b, bool reduce, hipStream_t s) {
+    if (bt_nph(K) == 4) {
+        if (sh) run_bt<4, true>(nib, cbs, x, y, partial, M, K, b, reduce, s);
+        else run_bt<4, false>(nib, cbs, x, y, partial, M, K, b, reduce, s);
+    } else {
+        if (sh) run_bt<2, true>(nib, cbs, x, y, partial, M, K, b, reduce, s);
+        else run_bt<2, false>(nib, cbs, x, y, partial, M, K, b, reduce, s);
+    }
 }
 
 }  // namespace
@@ -482,9 +533,6 @@ bool oil8_bt_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K, int64_t batch
 
 hipError_t launch_oil8_gemv_bt_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
                                     float* partial, hipStream_t s) {
-    const int ph = h3_phases(K);
-    const int64_t S = K / (128 * ph);
-    const int nt = h3_tiles(seg_groups(seg, nseg, 64), S);
     // groups of 16 tokens, one launch each (the weights are read per group)
     for (int64_t t0 = 0; t0 < batch; t0 += kH3Tok) {
         const int b = (int)(batch - t0 < kH3Tok ? batch - t0 : kH3Tok);
@@ -494,19 +542,25 @@ hipError_t launch_oil8_gemv_bt_segs(const Oil8Seg* seg, int nseg, const float* x
             g[i].y = seg[i].y + t0 * seg[i].rows;
         }
         const float* xg = x + t0 * K;
-        if (nt == 2) {
-            if (ph == 4) run_h3<2, 4>(g, nseg, xg, K, b, partial, s);
-            else if (ph == 2) run_h3<2, 2>(g, nseg, xg, K, b, partial, s);
-            else run_h3<2, 1>(g, nseg, xg, K, b, partial, s);
-        } else {
-            if (ph == 4) run_h3<1, 4>(g, nseg, xg, K, b, partial, s);
-            else if (ph == 2) run_h3<1, 2>(g, nseg, xg, K, b, partial, s);
-            else run_h3<1, 1>(g, nseg, xg, K, b, partial, s);
-        }
+        h3_dispatch(g, nseg, xg, K, b, partial, true, s);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+int oil8_bt_slices(int64_t K) { return (int)(K / (128 * h3_phases(K))); }
+
+hipError_t launch_oil8_gemv_bt_segs_slices(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
+                                           float* partial, Slices* out, hipStream_t s) {
+    h3_dispatch(seg, nseg, x, K, (int)batch, partial, false, s);
+    const int S = oil8_bt_slices(K);
+    int64_t mtot = 0;
+    for (int i = 0; i < nseg; ++i) mtot += seg[i].rows;
+    for (int i = 0, off = 0; i < nseg; off += (int)seg[i].rows, ++i)
+        out[i] = S == 1 ? plain_slices(seg[i].y, seg[i].rows)
+                        : Slices{partial + off, mtot, kH3Tok * mtot, S, 1.0f, nullptr};
+    return hipGetLastError();
 }
 
 hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
@@ -521,15 +575,7 @@ hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t 
     // groups of 16 tokens, one launch each (the weights are read per group)
     for (int64_t t0 = 0; t0 < batch; t0 += kBtTok) {
         const int b = (int)(batch - t0 < kBtTok ? batch - t0 : kBtTok);
-        const float* xg = x + t0 * K;
-        float* yg = y + t0 * M;
-        if (bt_nph(K) == 4) {
-            if (sh) run_bt<4, true>(nib, cbs, xg, yg, partial, M, K, b, s);
-            else run_bt<4, false>(nib, cbs, xg, yg, partial, M, K, b, s);
-        } else {
-            if (sh) run_bt<2, true>(nib, cbs, xg, yg, partial, M, K, b, s);
-            else run_bt<2, false>(nib, cbs, xg, yg, partial, M, K, b, s);
-        }
+        bt_dispatch(nib, cbs, sh, x + t0 * K, y + t0 * M, partial, M, K, b, true, s);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

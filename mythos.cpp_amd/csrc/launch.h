@@ -56,6 +56,11 @@ size_t oil8_bt_partial_bytes(int64_t M, int64_t K);
 hipError_t launch_oil8_gemv_bt(const uint8_t* idx, const float* cb, const float* x, float* y, int64_t M, int64_t K,
                                int64_t batch, float* partial, hipStream_t s);
 bool oil8_bt_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K, int64_t batch);
+// Batches of at most 16 without the slice reduction: the outputs as Slices
+// (common.h), one per segment, valid until the workspace is reused.
+int oil8_bt_slices(int64_t K);
+hipError_t launch_oil8_gemv_bt_segs_slices(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
+                                           float* partial, Slices* out, hipStream_t s);
 hipError_t launch_oil8_gemv_bt_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
                                     float* partial, hipStream_t s);
 // Reference per-(m,n) indexing with one codebook (src/kernel_oil4.cpp:41-52).
@@ -79,6 +84,11 @@ bool i2s_bt_supported(int64_t M, int64_t K, int64_t batch);
 size_t i2s_bt_partial_bytes(int64_t M, int64_t K);
 hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale, float* y,
                               int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
+// Batches of at most 16 without the slice reduction (Slices with the I2_S
+// epilogue, common.h).
+hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
+                                    float* y, int64_t M, int64_t K, int64_t batch, float* partial, Slices* out,
+                                    hipStream_t s);
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 // ws: null (one wave per output) or i2s_gemm_workspace_bytes(M, N, K) bytes of
@@ -108,6 +118,9 @@ hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* n
 // x <- t + x (when t), then y = rms_norm(x) * gamma per row of dim.
 hipError_t launch_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim,
                            float eps, hipStream_t s);
+// The same with t read as Slices (t.n == 0: no residual add).
+hipError_t launch_rms_norm_slices(float* x, const Slices& t, const float* gamma, float* y, int64_t rows, int64_t dim,
+                                  float eps, hipStream_t s);
 // y[r][i] = silu(g[r*gstride + i]) * u[r*ustride + i], i < n
 hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t n, int64_t gstride,
                            int64_t ustride, hipStream_t s);
@@ -128,9 +141,17 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
 hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
                                  const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out, const int* step,
                                  int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s);
+// q/k/v as Slices (common.h): rows of heads*head_dim / kv_heads*head_dim.
+hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
+                                        const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out,
+                                        const int* step, int64_t batch, int heads, int kv_heads, int head_dim,
+                                        int max_seq, hipStream_t s);
 // silu(g) * u then quantize_per_token: q [rows][n] int8, inv_scale [rows];
 // act (nullable) receives the FP32 activations [rows][n].
 bool silu_mul_quant_supported(int64_t n);
+// g/u as Slices (common.h)
+hipError_t launch_silu_mul_quant_slices(const Slices& g, const Slices& u, int8_t* q, float* inv_scale, float* act,
+                                        int64_t rows, int64_t n, hipStream_t s);
 hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, float* act,
                                  int64_t rows, int64_t n, int64_t gstride, int64_t ustride, hipStream_t s);
 // Greedy argmax in two launches; pv/pi: rows * argmax_chunks(n) partials.

@@ -841,6 +841,16 @@ hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t
     return hipSuccess;
 }
 
+hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
+                                    float* y, int64_t M, int64_t K, int64_t batch, float* partial, Slices* out,
+                                    hipStream_t s) {
+    const int S = ib_slices(M, K);
+    i2s_gemv_bt<<<dim3(ceil_div(M, kIbRows), (unsigned)S), kWG, 0, s>>>(packed, w_scale, act, act_scale, y, partial,
+                                                                        (int)M, (int)K, (int)batch);
+    *out = S == 1 ? plain_slices(y, M) : Slices{partial, M, kIbTok * M, S, w_scale, act_scale};
+    return hipGetLastError();
+}
+
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o, int64_t M, int64_t N, int64_t K,
                            hipStream_t s) {
     i2s_gemm_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);

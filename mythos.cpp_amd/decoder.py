@@ -21,7 +21,8 @@ VP, I64, I32, F32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
 
 EXPORTS = ("mth_decoder_create", "mth_decoder_destroy", "mth_decoder_set_layer", "mth_decoder_set_globals",
            "mth_decoder_start", "mth_decoder_step", "mth_decoder_buffers", "mth_decoder_read",
-           "mth_decoder_steps_done", "mth_decoder_set_taps", "mth_decoder_tap_floats", "mth_decoder_read_kv")
+           "mth_decoder_steps_done", "mth_decoder_set_taps", "mth_decoder_tap_floats", "mth_decoder_read_kv",
+           "mth_decoder_launches")
 
 CONFIG_KEYS = ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ffn", "max_seq", "cb_block",
                "max_batch")
@@ -63,6 +64,8 @@ _lib.mth_decoder_read.argtypes = [VP, VP, VP, VP]
 _lib.mth_decoder_read.restype = I32
 _lib.mth_decoder_steps_done.argtypes = [VP]
 _lib.mth_decoder_steps_done.restype = I64
+_lib.mth_decoder_launches.argtypes = [VP]
+_lib.mth_decoder_launches.restype = I64
 _lib.mth_decoder_set_taps.argtypes = [VP, VP]
 _lib.mth_decoder_set_taps.restype = I32
 _lib.mth_decoder_tap_floats.argtypes = [VP]
@@ -138,6 +141,11 @@ class Decoder:
     @property
     def steps_done(self) -> int:
         return int(_lib.mth_decoder_steps_done(self._h))
+
+    @property
+    def launches_per_step(self) -> int:
+        """Kernel launches of one graph step (0 before the first graph step)."""
+        return int(_lib.mth_decoder_launches(self._h))
 
     def _buffers(self):
         lg, hist, stride = VP(), VP(), I64()
