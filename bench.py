@@ -164,11 +164,11 @@ def bench_ternary_gemm(mth, dev, M, N, K, steps, warmup):
 
 def bench_decode(dev, batches=(1, 16), kv_dtype="bf16"):
     """Config 5: the 32-layer mixed-format decoder, greedy, 64-token random
-    prompts, 128 generated tokens per sequence, bf16 KV cache.  The prompt is
-    fed through the same decode step (64 steps, the last one yielding the
-    first token); the remaining 127 tokens take 127 steps, timed with HIP
-    events on the launch stream.  Each step is one replay of the captured step
-    graph.  Roofline bytes per step: every weight byte once plus the KV cache
+    prompts, 128 generated tokens per sequence, bf16 KV cache.  The prompt
+    runs as one forward pass (mth_decoder_prefill: all B x 64 prompt rows
+    through the layer stack, yielding the first token); the remaining 127
+    tokens take 127 steps, timed with HIP events on the launch stream.  Each
+    step is one replay of the captured step graph.  Roofline bytes per step: every weight byte once plus the KV cache
     rows the attention reads (positions 0 .. pos-1 of every layer, sequence
     and kv head, K and V) and the row it appends, averaged over the timed
     steps."""
@@ -192,12 +192,13 @@ def bench_decode(dev, batches=(1, 16), kv_dtype="bf16"):
     for B in batches:
         prompts = synth.decoder_prompts(cfg, B, P)
         dec.start(prompts)                 # warm-up: graph capture + one full run
-        dec.step(P + G - 1)
+        dec.prefill()
+        dec.step(G - 1)
         torch.cuda.synchronize()
         dec.start(prompts)
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         e[0].record(s)
-        dec.step(P)
+        dec.prefill()
         e[1].record(s)
         dec.step(G - 1)
         e[2].record(s)

@@ -94,6 +94,17 @@ int mth_decoder_buffers(const mth_decoder* d, float** logits, int32_t** hist, in
  * [batch][vocab] and token history [batch][max_seq + 1]; either may be null. */
 int mth_decoder_read(const mth_decoder* d, float* logits, int32_t* hist, mth_stream_t stream);
 
+/* The whole prompt as one forward pass (src/generator.cpp:33-38: prefill,
+ * then sampling of the last position): every prompt position of every
+ * started sequence runs through the layer stack as a row of batched launches
+ * (chunks of up to 1024 rows), filling the KV caches, then the last
+ * positions' logits give the first generated token.  Afterwards the decoder
+ * is where prompt_len mth_decoder_step calls would leave it (steps done =
+ * prompt_len, logits and history likewise), so decoding continues with
+ * mth_decoder_step.  Only right after mth_decoder_start (MTH_EINVAL
+ * otherwise).  Runs its launches directly on the stream (no graph). */
+int mth_decoder_prefill(mth_decoder* d, mth_stream_t stream);
+
 /* Steps run since the last start (host-side count). */
 int64_t mth_decoder_steps_done(const mth_decoder* d);
 

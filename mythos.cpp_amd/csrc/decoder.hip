@@ -49,6 +49,12 @@ struct mth_decoder {
     int64_t graph_batch = 0, graph_prompt = 0;
     size_t graph_nodes = 0;
 
+    // prefill (mth_decoder_prefill): pf_rows rows of (sequence, position)
+    int64_t pf_rows = 0;
+    float *pf_x = nullptr, *pf_h = nullptr, *pf_t = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    float *pf_att = nullptr, *pf_gu = nullptr, *pf_inv = nullptr;
+    int8_t* pf_aq = nullptr;
+
     void drop_graph() {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
@@ -64,40 +70,124 @@ using mth::api_ok;
 
 size_t round_up(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// y[B][M] = W x for an OIL4 weight, picking the batched kernel when it applies.
+// y[rows][M] = W x for an OIL4 weight, picking the batched kernel when it applies.
 hipError_t oil4(const mth_decoder* d, const uint8_t* w, const uint16_t* cb, const float* x, float* y, int64_t M,
-                int64_t K, hipStream_t s) {
+                int64_t K, hipStream_t s, int64_t rows = 0) {
+    if (!rows) rows = d->batch;
     const bool aligned = (((uintptr_t)w | (uintptr_t)cb | (uintptr_t)x) & 15u) == 0;
-    if (aligned && mth::oil4_bt_supported(M, K, d->c.cb_block, d->batch))
-        return mth::launch_oil4_gemv_bt(w, cb, d->c.cb_block, x, y, M, K, d->batch, d->bt_partial, s);
-    return mth::launch_oil4_gemv(w, cb, d->c.cb_block, x, y, M, K, d->batch, s);
+    if (aligned && mth::oil4_bt_supported(M, K, d->c.cb_block, rows))
+        return mth::launch_oil4_gemv_bt(w, cb, d->c.cb_block, x, y, M, K, rows, d->bt_partial, s);
+    return mth::launch_oil4_gemv(w, cb, d->c.cb_block, x, y, M, K, rows, s);
 }
 
-// y[B][M] = W x for an OIL8 weight: MFMA kernel for batches of 2 and more.
+// y[rows][M] = W x for an OIL8 weight: MFMA kernel for batches of 2 and more.
 hipError_t oil8(const mth_decoder* d, const uint8_t* w, const float* cb, const float* x, float* y, int64_t M,
-                int64_t K, hipStream_t s) {
+                int64_t K, hipStream_t s, int64_t rows = 0) {
+    if (!rows) rows = d->batch;
     const bool aligned = (((uintptr_t)w | (uintptr_t)x) & 15u) == 0;
-    if (aligned && mth::oil8_bt_supported(M, K, d->batch))
-        return mth::launch_oil8_gemv_bt(w, cb, x, y, M, K, d->batch, d->bt_partial, s);
-    return mth::launch_oil8_gemv(w, cb, x, y, M, K, d->batch, s);
+    if (aligned && mth::oil8_bt_supported(M, K, rows))
+        return mth::launch_oil8_gemv_bt(w, cb, x, y, M, K, rows, d->bt_partial, s);
+    return mth::launch_oil8_gemv(w, cb, x, y, M, K, rows, s);
 }
 
-// Q, K and V projections of the normed input: one launch over the three
-// matrices (each with its own codebook) where the kernels take them.
-hipError_t qkv(const mth_decoder* d, const mth_decoder_layer& L, hipStream_t s) {
+// Q, K and V projections of the normed input h (rows) into q, k, v: one
+// launch over the three matrices (each with its own codebook) where the
+// kernels take them.
+hipError_t qkv(const mth_decoder* d, const mth_decoder_layer& L, const float* h, float* q, float* k, float* v,
+               int64_t rows, hipStream_t s) {
     const mth_decoder_config& c = d->c;
     const int64_t H = c.hidden, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
-    const mth::Oil8Seg seg[3] = {{L.wq, L.cbq, d->q, QD}, {L.wk, L.cbk, d->k, KD}, {L.wv, L.cbv, d->v, KD}};
-    if (d->batch >= 2) {
-        if (mth::oil8_bt_segs_fusable(seg, 3, H, d->batch))
-            return mth::launch_oil8_gemv_bt_segs(seg, 3, d->h, H, d->batch, d->bt_partial, s);
-    } else if (mth::oil8_segs_fusable(seg, 3, H)) {
-        return mth::launch_oil8_gemv_segs(seg, 3, d->h, H, d->batch, s);
+    const mth::Oil8Seg seg[3] = {{L.wq, L.cbq, q, QD}, {L.wk, L.cbk, k, KD}, {L.wv, L.cbv, v, KD}};
+    if (((uintptr_t)h & 15u) == 0) {
+        if (rows >= 2) {
+            if (mth::oil8_bt_segs_fusable(seg, 3, H, rows))
+                return mth::launch_oil8_gemv_bt_segs(seg, 3, h, H, rows, d->bt_partial, s);
+        } else if (mth::oil8_segs_fusable(seg, 3, H)) {
+            return mth::launch_oil8_gemv_segs(seg, 3, h, H, rows, s);
+        }
     }
-    hipError_t e = oil8(d, L.wq, L.cbq, d->h, d->q, QD, H, s);
-    if (e == hipSuccess) e = oil8(d, L.wk, L.cbk, d->h, d->k, KD, H, s);
-    if (e == hipSuccess) e = oil8(d, L.wv, L.cbv, d->h, d->v, KD, H, s);
+    hipError_t e = oil8(d, L.wq, L.cbq, h, q, QD, H, s, rows);
+    if (e == hipSuccess) e = oil8(d, L.wk, L.cbk, h, k, KD, H, s, rows);
+    if (e == hipSuccess) e = oil8(d, L.wv, L.cbv, h, v, KD, H, s, rows);
     return e;
+}
+
+// gate and up adjacent in one [2*ffn][hidden] weight with adjacent codebooks
+bool gate_up_fused(const mth_decoder* d, const mth_decoder_layer& L) {
+    const int64_t H = d->c.hidden, F = d->c.ffn, nb = d->c.cb_block ? H / d->c.cb_block : 1;
+    return L.wup == L.wgate + F * (H / 2) && (d->c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
+}
+
+// The prompt as one forward pass (src/generator.cpp:36): every prompt
+// position of every sequence is a row of the same layer stack (the batched
+// GEMVs in groups of 16 rows, one RoPE + KV append and one causal attention
+// launch per layer over all rows), in chunks of pf_rows rows (whole
+// positions, all sequences); the attention of a chunk reads the earlier
+// chunks' positions from the cache.  Then the final norm, lm_head and argmax
+// of each sequence's last position: the decoder is left as after prompt_len
+// decode steps (step counter prompt_len, the first generated token in the
+// history, its logits in the logits buffer).
+hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
+    const mth_decoder_config& c = d->c;
+    const int64_t B = d->batch, P = d->prompt_len, H = c.hidden, F = c.ffn, QD = c.heads * c.head_dim;
+    const bool bf16 = c.kv_dtype == 1;
+    const int64_t C = std::max<int64_t>(1, d->pf_rows / B);  // positions per chunk
+    hipError_t e;
+#define TRY(call)                        \
+    do {                                 \
+        if ((e = (call)) != hipSuccess) return e; \
+    } while (0)
+    int64_t np = 0;
+    for (int64_t p0 = 0; p0 < P; p0 += C) {
+        np = std::min(C, P - p0);
+        const int64_t R = B * np;
+        TRY(mth::launch_embed_rows(d->g.emb, d->hist, (int)d->hist_stride, d->pf_x, R, (int)np, (int)p0, (int)H,
+                                   (int)c.vocab, s));
+        for (int64_t l = 0; l < c.layers; l++) {
+            const mth_decoder_layer& L = d->layers[(size_t)l];
+            char* kc = d->kc + l * d->layer_kv * d->kv_elem;
+            char* vc = d->vc + l * d->layer_kv * d->kv_elem;
+            TRY(mth::launch_rms_norm(d->pf_x, l == 0 ? nullptr : d->pf_t, L.attn_norm, d->pf_h, R, H, c.eps, s));
+            TRY(qkv(d, L, d->pf_h, d->pf_q, d->pf_k, d->pf_v, R, s));
+            TRY(mth::launch_rope_kv_rows(d->pf_q, d->pf_k, d->pf_v, d->rope_cos, d->rope_sin, kc, vc, bf16, R,
+                                         (int)np, (int)p0, (int)c.heads, (int)c.kv_heads, (int)c.head_dim,
+                                         (int)c.max_seq, s));
+            TRY(mth::launch_attention_rows(d->pf_q, kc, vc, bf16, d->pf_att, R, (int)np, (int)p0, (int)c.heads,
+                                           (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
+            TRY(oil8(d, L.wo, L.cbo, d->pf_att, d->pf_t, H, QD, s, R));
+            TRY(mth::launch_rms_norm(d->pf_x, d->pf_t, L.ffn_norm, d->pf_h, R, H, c.eps, s));
+            if (gate_up_fused(d, L)) {
+                TRY(oil4(d, L.wgate, L.cbgate, d->pf_h, d->pf_gu, 2 * F, H, s, R));
+                TRY(mth::launch_silu_mul_quant(d->pf_gu, d->pf_gu + F, d->pf_aq, d->pf_inv, nullptr, R, F, 2 * F,
+                                               2 * F, s));
+            } else {
+                TRY(oil4(d, L.wgate, L.cbgate, d->pf_h, d->pf_gu, F, H, s, R));
+                TRY(oil4(d, L.wup, L.cbup, d->pf_h, d->pf_gu + R * F, F, H, s, R));
+                TRY(mth::launch_silu_mul_quant(d->pf_gu, d->pf_gu + R * F, d->pf_aq, d->pf_inv, nullptr, R, F, F, F,
+                                               s));
+            }
+            if ((((uintptr_t)L.wdown | (uintptr_t)d->pf_aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, R))
+                TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->pf_aq, d->pf_inv, d->pf_t, H, F, R,
+                                            d->bt_partial, s));
+            else
+                TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->pf_aq, d->pf_inv, d->pf_t, H, F, R, s));
+        }
+    }
+    // each sequence's last position (row b*np + np-1 of the last chunk): its
+    // residual stream and last FFN output, then the final norm and lm_head
+    TRY(hipMemcpy2DAsync(d->x, (size_t)H * 4, d->pf_x + (np - 1) * H, (size_t)(np * H) * 4, (size_t)H * 4, (size_t)B,
+                         hipMemcpyDeviceToDevice, s));
+    TRY(hipMemcpy2DAsync(d->t, (size_t)H * 4, d->pf_t + (np - 1) * H, (size_t)(np * H) * 4, (size_t)H * 4, (size_t)B,
+                         hipMemcpyDeviceToDevice, s));
+    TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, B, H, c.eps, s));
+    TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
+    // the argmax of step prompt_len - 1 writes the token after the prompt and
+    // advances the step counter to prompt_len
+    TRY(hipMemsetD32Async((hipDeviceptr_t)d->step, (int)(P - 1), 1, s));
+    TRY(mth::launch_argmax(d->logits, B, c.vocab, d->ids, d->hist, d->step, (int)d->hist_stride, (int)d->prompt_len,
+                           d->arg_v, d->arg_i, s));
+#undef TRY
+    return hipSuccess;
 }
 
 hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
@@ -146,7 +236,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
             TRY(mth::launch_oil8_gemv_bt_segs_slices(qkv_seg, 3, d->h, H, B, d->bt_partial, o, s));
             sq = o[0], sk = o[1], sv = o[2];
         } else {
-            TRY(qkv(d, L, s));
+            TRY(qkv(d, L, d->h, d->q, d->k, d->v, B, s));
         }
         TRY(mth::launch_rope_attention_slices(sq, sk, sv, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
                                               d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim,
@@ -162,8 +252,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         }
         TRY(mth::launch_rms_norm_slices(d->x, so, L.ffn_norm, d->h, B, H, c.eps, s));
         if (tp) TRY(tap_copy(tp, d->x, (size_t)(B * H) * 4));
-        const int64_t nb = c.cb_block ? H / c.cb_block : 1;
-        const bool fused = L.wup == L.wgate + F * (H / 2) && (c.cb_block == 0 ? false : L.cbup == L.cbgate + F * nb * 16);
+        const bool fused = gate_up_fused(d, L);
         // gate/up, then silu(gate)*up quantised to int8 per token (once, not
         // per workgroup of the down projection), then the ternary GEMV on the
         // int8 activations
@@ -248,6 +337,9 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     d->hist_stride = c.max_seq + 1;
     d->layer_kv = B * KD * c.max_seq;
     d->kv_elem = c.kv_dtype == 1 ? 2 : 4;
+    // prefill chunk: up to 1024 rows of (sequence, position)
+    const int64_t PR = std::min<int64_t>(B * c.max_seq, 1024);
+    d->pf_rows = PR;
     // workspace of the batched GEMVs: the largest of every projection's need
     const size_t partial = std::max({mth::oil4_bt_partial_bytes(2 * F, H), mth::oil8_bt_partial_bytes(QD + 2 * KD, H),
                                      mth::oil8_bt_partial_bytes(H, QD),
@@ -271,6 +363,11 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->bt_partial, partial},
         {(void**)&d->hist, (size_t)(B * d->hist_stride) * 4},
         {(void**)&d->step, 4},                      {(void**)&d->ids, (size_t)B * 4},
+        {(void**)&d->pf_x, (size_t)(PR * H) * 4},   {(void**)&d->pf_h, (size_t)(PR * H) * 4},
+        {(void**)&d->pf_t, (size_t)(PR * H) * 4},   {(void**)&d->pf_q, (size_t)(PR * QD) * 4},
+        {(void**)&d->pf_k, (size_t)(PR * KD) * 4},  {(void**)&d->pf_v, (size_t)(PR * KD) * 4},
+        {(void**)&d->pf_att, (size_t)(PR * QD) * 4}, {(void**)&d->pf_gu, (size_t)(PR * 2 * F) * 4},
+        {(void**)&d->pf_aq, (size_t)(PR * F)},      {(void**)&d->pf_inv, (size_t)PR * 4},
     };
     size_t total = 0;
     for (const Slot& sl : slots) total += round_up(sl.bytes);
@@ -394,6 +491,22 @@ int mth_decoder_step(mth_decoder* d, int64_t n, int use_graph, mth_stream_t stre
     }
     if (e != hipSuccess) return api_fail(MTH_EDEVICE, "mth_decoder_step: %s", hipGetErrorString(e));
     d->steps += n;
+    return api_ok();
+}
+
+int mth_decoder_prefill(mth_decoder* d, mth_stream_t stream) {
+    if (!d) return api_fail(MTH_EINVAL, "mth_decoder_prefill: null decoder");
+    if (d->batch == 0) return api_fail(MTH_EINVAL, "mth_decoder_prefill: no sequences started");
+    if (d->steps != 0)
+        return api_fail(MTH_EINVAL, "mth_decoder_prefill: %lld steps already run since the start",
+                        (long long)d->steps);
+    for (int64_t l = 0; l < d->c.layers; l++)
+        if (!d->layer_set[(size_t)l]) return api_fail(MTH_EINVAL, "mth_decoder_prefill: layer %lld has no weights",
+                                                      (long long)l);
+    if (!d->globals_set) return api_fail(MTH_EINVAL, "mth_decoder_prefill: embedding / lm_head not set");
+    const hipError_t e = enqueue_prefill(d, (hipStream_t)stream);
+    if (e != hipSuccess) return api_fail(MTH_EDEVICE, "mth_decoder_prefill: %s", hipGetErrorString(e));
+    d->steps = d->prompt_len;
     return api_ok();
 }
 

@@ -264,11 +264,14 @@ __device__ __forceinline__ uint2 kv_raw4(const uint16_t* p) { return *(const uin
 // and all ctx rows come from the cache.
 // KV: the cache element type (float, or uint16_t holding bf16 bits); with
 // bf16, the current position's k/v are rounded in LDS as the cache stores them.
+// Rows: grid.y = rows of q/out; row r is position (step ? *step : 0) + ctx0 +
+// r % np of sequence r / np (np = 1: one position per sequence, decode; np
+// > 1: the prompt rows of a prefill chunk, each attending causally).
 template <int D, bool ROPE, typename KV>
 __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices vin, const float* __restrict__ cos_t,
                                                   const float* __restrict__ sin_t, KV* kc, KV* vc,
                                                   float* __restrict__ out, const int* __restrict__ step, int ctx0,
-                                                  int heads, int kv_heads, int max_seq, float scale) {
+                                                  int np, int heads, int kv_heads, int max_seq, float scale) {
     typedef typename KvRaw4<KV>::type Raw;
     constexpr int G = D / 4;        // float4 column groups
     constexpr int SL = kT / G;      // position slices in P*V
@@ -277,8 +280,8 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     __shared__ __align__(16) float qs[D], ks[D], vs[D];
     __shared__ float4 part[SL][G];
     __shared__ float redf[4];
-    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    const int pos = (step ? *step : 0) + ctx0;  // the last position attended to
+    const int h = blockIdx.x, row = blockIdx.y, b = row / np, tid = threadIdx.x;
+    const int pos = (step ? *step : 0) + ctx0 + row % np;  // the last position attended to
     const int ctx = pos + 1;
     const int kh = h % kv_heads;
     const int64_t crow = ((int64_t)b * kv_heads + kh) * max_seq;  // cache row of position 0
@@ -290,17 +293,17 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         const float* sr = sin_t + (int64_t)pos * (D / 2);
         if (tid < D / 2) {
             const float c = cr[tid], s = sr[tid];
-            const float q1 = slice_value(q, b, h * D + tid), q2 = slice_value(q, b, h * D + tid + D / 2);
+            const float q1 = slice_value(q, row, h * D + tid), q2 = slice_value(q, row, h * D + tid + D / 2);
             qs[tid] = q1 * c - q2 * s;
             qs[tid + D / 2] = q1 * s + q2 * c;
-            const float k1 = slice_value(kin, b, kh * D + tid), k2 = slice_value(kin, b, kh * D + tid + D / 2);
+            const float k1 = slice_value(kin, row, kh * D + tid), k2 = slice_value(kin, row, kh * D + tid + D / 2);
             ks[tid] = kv_rounded(k1 * c - k2 * s, KV{});
             ks[tid + D / 2] = kv_rounded(k1 * s + k2 * c, KV{});
-            vs[tid] = kv_rounded(slice_value(vin, b, kh * D + tid), KV{});
-            vs[tid + D / 2] = kv_rounded(slice_value(vin, b, kh * D + tid + D / 2), KV{});
+            vs[tid] = kv_rounded(slice_value(vin, row, kh * D + tid), KV{});
+            vs[tid + D / 2] = kv_rounded(slice_value(vin, row, kh * D + tid + D / 2), KV{});
         }
     } else {
-        if (tid < D) qs[tid] = slice_value(q, b, h * D + tid);
+        if (tid < D) qs[tid] = slice_value(q, row, h * D + tid);
     }
     // cache rows: this thread's K row of the first tile, then its V rows
     Raw kr0[D / 4];
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
             r.z += o.z;
             r.w += o.w;
         }
-        *(float4*)(out + ((int64_t)b * heads + h) * D + 4 * tid) = r;
+        *(float4*)(out + ((int64_t)row * heads + h) * D + 4 * tid) = r;
     }
 }
 
@@ -572,6 +575,54 @@ __global__ __launch_bounds__(kT) void embed_k(const float* __restrict__ emb, con
     for (int i = threadIdx.x * 4; i < dim; i += kT * 4) *(float4*)(dst + i) = ldf4(src + i);
 }
 
+// Prefill rows: row r is position p0 + r % np of sequence r / np.
+// x[r] = emb[id], id = hist[r / np][p0 + r % np] (ids outside [0, vocab) -> 0).
+__global__ __launch_bounds__(kT) void embed_rows_k(const float* __restrict__ emb, const int* __restrict__ hist,
+                                                   int hist_stride, float* __restrict__ x, int dim, int vocab, int np,
+                                                   int p0) {
+    const int r = blockIdx.x;
+    int id = hist[(int64_t)(r / np) * hist_stride + p0 + r % np];
+    if (id < 0 || id >= vocab) id = 0;
+    const float* src = emb + (int64_t)id * dim;
+    float* dst = x + (int64_t)r * dim;
+    for (int i = threadIdx.x * 4; i < dim; i += kT * 4) *(float4*)(dst + i) = ldf4(src + i);
+}
+
+// RoPE of row r's q (in place) and k at its position, k and v appended to
+// the caches at that position (rope_kv_k per row; KV: cache element type,
+// values stored as the decode attention stores them).
+template <typename KV>
+__global__ __launch_bounds__(kT) void rope_kv_rows_k(float* __restrict__ q, const float* __restrict__ k,
+                                                     const float* __restrict__ v, const float* __restrict__ cos_t,
+                                                     const float* __restrict__ sin_t, KV* __restrict__ kc,
+                                                     KV* __restrict__ vc, int np, int p0, int heads, int kv_heads,
+                                                     int D, int max_seq) {
+    const int r = blockIdx.x, b = r / np, pos = p0 + r % np;
+    const int h2 = D / 2;
+    const float* cr = cos_t + (int64_t)pos * h2;
+    const float* sr = sin_t + (int64_t)pos * h2;
+    float* qb = q + (int64_t)r * heads * D;
+    for (int i = threadIdx.x; i < heads * h2; i += kT) {
+        const int h = i / h2, d = i % h2;
+        float* p = qb + h * D;
+        const float x1 = p[d], x2 = p[d + h2], c = cr[d], s = sr[d];
+        p[d] = x1 * c - x2 * s;
+        p[d + h2] = x1 * s + x2 * c;
+    }
+    const float* kb = k + (int64_t)r * kv_heads * D;
+    const float* vb = v + (int64_t)r * kv_heads * D;
+    for (int i = threadIdx.x; i < kv_heads * h2; i += kT) {
+        const int h = i / h2, d = i % h2;
+        const float* p = kb + h * D;
+        const float x1 = p[d], x2 = p[d + h2], c = cr[d], s = sr[d];
+        const int64_t row = (((int64_t)b * kv_heads + h) * max_seq + pos) * D;
+        kc[row + d] = kv_store_value(x1 * c - x2 * s, KV{});
+        kc[row + d + h2] = kv_store_value(x1 * s + x2 * c, KV{});
+        vc[row + d] = kv_store_value(vb[h * D + d], KV{});
+        vc[row + d + h2] = kv_store_value(vb[h * D + d + h2], KV{});
+    }
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + kT - 1) / kT); }
 inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -634,18 +685,19 @@ bool attention_supported(int head_dim, int max_seq) {
 template <bool ROPE, typename KV>
 static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
                                 const float* sin_t, KV* kc, KV* vc, float* out, const int* step, int ctx0,
-                                int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
+                                int64_t rows, int np, int heads, int kv_heads, int head_dim, int max_seq,
+                                hipStream_t s) {
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
-    const dim3 grid((unsigned)heads, (unsigned)batch);
+    const dim3 grid((unsigned)heads, (unsigned)rows);
     if (head_dim == 64)
-        attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+        attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, np, heads,
                                                         kv_heads, max_seq, scale);
     else if (head_dim == 128)
-        attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+        attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, np, heads,
                                                          kv_heads, max_seq, scale);
     else
-        attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, heads,
+        attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, np, heads,
                                                          kv_heads, max_seq, scale);
     return hipGetLastError();
 }
@@ -654,7 +706,18 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
                             int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
     const Slices qs = plain_slices(q, (int64_t)heads * head_dim), none{nullptr, 0, 0, 0, 1.0f, nullptr};
     return run_attention<false, float>(qs, none, none, nullptr, nullptr, (float*)kc, (float*)vc, out, step, ctx0,
-                                       batch, heads, kv_heads, head_dim, max_seq, s);
+                                       batch, 1, heads, kv_heads, head_dim, max_seq, s);
+}
+
+hipError_t launch_attention_rows(const float* q, const void* kc, const void* vc, bool kv_bf16, float* out,
+                                 int64_t rows, int np, int p0, int heads, int kv_heads, int head_dim, int max_seq,
+                                 hipStream_t s) {
+    const Slices qs = plain_slices(q, (int64_t)heads * head_dim), none{nullptr, 0, 0, 0, 1.0f, nullptr};
+    if (kv_bf16)
+        return run_attention<false, uint16_t>(qs, none, none, nullptr, nullptr, (uint16_t*)kc, (uint16_t*)vc, out,
+                                              nullptr, p0, rows, np, heads, kv_heads, head_dim, max_seq, s);
+    return run_attention<false, float>(qs, none, none, nullptr, nullptr, (float*)kc, (float*)vc, out, nullptr, p0,
+                                       rows, np, heads, kv_heads, head_dim, max_seq, s);
 }
 
 hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
@@ -672,8 +735,8 @@ hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const 
                                         int max_seq, hipStream_t s) {
     if (kv_bf16)
         return run_attention<true, uint16_t>(q, k, v, cos_t, sin_t, (uint16_t*)kc, (uint16_t*)vc, out, step, 0,
-                                             batch, heads, kv_heads, head_dim, max_seq, s);
-    return run_attention<true, float>(q, k, v, cos_t, sin_t, (float*)kc, (float*)vc, out, step, 0, batch, heads,
+                                             batch, 1, heads, kv_heads, head_dim, max_seq, s);
+    return run_attention<true, float>(q, k, v, cos_t, sin_t, (float*)kc, (float*)vc, out, step, 0, batch, 1, heads,
                                       kv_heads, head_dim, max_seq, s);
 }
 
@@ -698,6 +761,24 @@ hipError_t launch_argmax(const float* logits, int64_t rows, int64_t n, int* ids,
     const int nc = argmax_chunks(n);
     argmax_part_k<<<dim3((unsigned)nc, (unsigned)rows), kT, 0, s>>>(logits, n, kArgChunk, pv, pi);
     argmax_final_k<<<1, kT, 0, s>>>(pv, pi, nc, (int)rows, ids, hist, step, hist_stride, prompt_len);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const float* emb, const int* hist, int hist_stride, float* x, int64_t rows, int np, int p0,
+                             int dim, int vocab, hipStream_t s) {
+    embed_rows_k<<<(unsigned)rows, kT, 0, s>>>(emb, hist, hist_stride, x, dim, vocab, np, p0);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
+                               void* kc, void* vc, bool kv_bf16, int64_t rows, int np, int p0, int heads, int kv_heads,
+                               int head_dim, int max_seq, hipStream_t s) {
+    if (kv_bf16)
+        rope_kv_rows_k<uint16_t><<<(unsigned)rows, kT, 0, s>>>(q, k, v, cos_t, sin_t, (uint16_t*)kc, (uint16_t*)vc, np,
+                                                               p0, heads, kv_heads, head_dim, max_seq);
+    else
+        rope_kv_rows_k<float><<<(unsigned)rows, kT, 0, s>>>(q, k, v, cos_t, sin_t, (float*)kc, (float*)vc, np, p0,
+                                                            heads, kv_heads, head_dim, max_seq);
     return hipGetLastError();
 }
 

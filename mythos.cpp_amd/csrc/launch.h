@@ -146,6 +146,18 @@ hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const 
                                         const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out,
                                         const int* step, int64_t batch, int heads, int kv_heads, int head_dim,
                                         int max_seq, hipStream_t s);
+// Prefill rows: row r is position p0 + r % np of sequence r / np.
+// Attention of each row over the cache positions 0 .. its own (q rotated).
+hipError_t launch_attention_rows(const float* q, const void* kc, const void* vc, bool kv_bf16, float* out,
+                                 int64_t rows, int np, int p0, int heads, int kv_heads, int head_dim, int max_seq,
+                                 hipStream_t s);
+// RoPE of each row's q (in place) and k; k, v appended to the caches.
+hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
+                               void* kc, void* vc, bool kv_bf16, int64_t rows, int np, int p0, int heads, int kv_heads,
+                               int head_dim, int max_seq, hipStream_t s);
+// x[r] = emb[hist[r / np][p0 + r % np]]
+hipError_t launch_embed_rows(const float* emb, const int* hist, int hist_stride, float* x, int64_t rows, int np, int p0,
+                             int dim, int vocab, hipStream_t s);
 // silu(g) * u then quantize_per_token: q [rows][n] int8, inv_scale [rows];
 // act (nullable) receives the FP32 activations [rows][n].
 bool silu_mul_quant_supported(int64_t n);

@@ -22,7 +22,7 @@ VP, I64, I32, F32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
 EXPORTS = ("mth_decoder_create", "mth_decoder_destroy", "mth_decoder_set_layer", "mth_decoder_set_globals",
            "mth_decoder_start", "mth_decoder_step", "mth_decoder_buffers", "mth_decoder_read",
            "mth_decoder_steps_done", "mth_decoder_set_taps", "mth_decoder_tap_floats", "mth_decoder_read_kv",
-           "mth_decoder_launches")
+           "mth_decoder_launches", "mth_decoder_prefill")
 
 CONFIG_KEYS = ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ffn", "max_seq", "cb_block",
                "max_batch")
@@ -64,6 +64,7 @@ _lib.mth_decoder_read.argtypes = [VP, VP, VP, VP]
 _lib.mth_decoder_read.restype = I32
 _lib.mth_decoder_steps_done.argtypes = [VP]
 _lib.mth_decoder_steps_done.restype = I64
+_lib.mth_decoder_prefill.argtypes = [VP, VP]
 _lib.mth_decoder_launches.argtypes = [VP]
 _lib.mth_decoder_launches.restype = I64
 _lib.mth_decoder_set_taps.argtypes = [VP, VP]
@@ -137,6 +138,11 @@ class Decoder:
 
     def step(self, n: int = 1, graph: bool = True, stream=None):
         _check(_lib.mth_decoder_step(self._h, n, int(graph), mythos_oil._stream(stream)))
+
+    def prefill(self, stream=None):
+        """The prompt as one forward pass (mth_decoder_prefill): afterwards
+        as after prompt_len steps."""
+        _check(_lib.mth_decoder_prefill(self._h, mythos_oil._stream(stream)))
 
     @property
     def steps_done(self) -> int:
@@ -215,10 +221,15 @@ class Decoder:
             k, v = ((a.astype(np.uint32) << 16).view(np.float32) for a in (k, v))
         return k, v
 
-    def generate(self, prompts: np.ndarray, max_tokens: int, graph: bool = True) -> np.ndarray:
+    def generate(self, prompts: np.ndarray, max_tokens: int, graph: bool = True, prefill: bool = True) -> np.ndarray:
         """Generator::generate_tokens with greedy sampling and no EOS stop:
-        prompt_len + max_tokens ids per sequence."""
+        prompt_len + max_tokens ids per sequence.  The prompt runs as one
+        forward pass (prefill), or with prefill=False as prompt_len steps."""
         self.start(prompts)
-        self.step(self.prompt_len + max_tokens - 1, graph=graph)
+        if prefill:
+            self.prefill()
+            self.step(max_tokens - 1, graph=graph)
+        else:
+            self.step(self.prompt_len + max_tokens - 1, graph=graph)
         return self.tokens()[:, :self.prompt_len + max_tokens]
 

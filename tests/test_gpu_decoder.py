@@ -150,6 +150,86 @@ def test_gqa_teacher_forced(batch, oracle):
     dec.close()
 
 
+def prefill_vs_oracle(cfg, model, B, P, kv, oracle, seed, extra_steps=2):
+    """mth_decoder_prefill against the oracle's P teacher-forced steps per
+    sequence: the last position's logits, every layer's K/V cache rows
+    0..P-1, the first generated token (greedy on the GPU's logits), then
+    decode steps continuing from the prefilled cache."""
+    prompts = synth.decoder_prompts(cfg, B, P, config=seed)
+    print(f"decoder prefill B={B} P={P} kv={kv}", flush=True)
+    dec = make(cfg, model, B, kv)
+    dec.start(prompts)
+    dec.prefill()
+    assert dec.steps_done == P
+    orc = oracle.decoder(oracle_cfg(cfg, kv), model)
+    caches = [orc.new_cache() for _ in range(B)]
+    want = np.stack([[orc.step(*caches[b], pos, int(prompts[b, pos]), threads=THREADS) for pos in range(P)][-1]
+                     for b in range(B)])
+    got = dec.logits()
+    for b in range(B):
+        assert rel(got[b], want[b]) < TOL, (b, rel(got[b], want[b]))
+    for l in range(cfg["layers"]):
+        kg, vg = dec.read_kv(l)
+        for b in range(B):
+            for name, got_c, want_c in (("K", kg[b, :, :P], caches[b][0][l, :, :P]),
+                                        ("V", vg[b, :, :P], caches[b][1][l, :, :P])):
+                if kv == "bf16" and l == 0:  # exact inputs: values on a rounding boundary may round one ulp apart
+                    d = np.abs(got_c.astype(np.float64) - want_c)
+                    ok = d <= 2.0 ** -7 * np.abs(want_c) + 1e-5 * np.abs(want_c).max()
+                    assert ok.all() and (d > 0).mean() < 0.01, (l, b, name, int((~ok).sum()), (d > 0).mean())
+                elif kv == "bf16":  # inputs carry the earlier layers' FP32 differences, then bf16 rounding
+                    assert rel(got_c, want_c) < 1e-3, (l, b, name, rel(got_c, want_c))
+                else:
+                    assert rel(got_c, want_c) < TOL, (l, b, name, rel(got_c, want_c))
+    toks = dec.tokens()
+    assert toks.shape[1] == P + 1 and np.array_equal(toks[:, :P], prompts)
+    assert np.array_equal(toks[:, P], np.argmax(got, axis=1))
+    for st in range(extra_steps):
+        dec.step(1)
+        lg, toks = dec.logits(), dec.tokens()
+        for b in range(B):
+            w = orc.step(*caches[b], P + st, int(toks[b, P + st]), threads=THREADS)
+            assert rel(lg[b], w) < TOL, (st, b, rel(lg[b], w))
+    dec.close()
+
+
+@pytest.mark.parametrize("B,kv", [(1, "f32"), (3, "bf16")])
+def test_prefill_matches_oracle(B, kv, small, oracle):
+    cfg, model = small
+    prefill_vs_oracle(cfg, model, B, 12, kv, oracle, seed=70 + B)
+
+
+def test_prefill_chunks_and_gqa(oracle):
+    """16 sequences x 70 prompt positions = 1120 rows: two chunks (64
+    positions, then 6) whose second attends to the first's cache rows;
+    grouped-query heads."""
+    cfg = synth.decoder_config(**dict(MID, max_seq=80, heads=8, kv_heads=4, head_dim=64))
+    model = synth.decoder_model(cfg, config=68, random_gamma=True)
+    prefill_vs_oracle(cfg, model, 16, 70, "bf16", oracle, seed=69)
+
+
+def test_prefill_then_generate_follows_oracle(small, oracle):
+    """generate() (prefill, then graph steps): greedy tokens follow the
+    oracle's argmax except at near ties."""
+    cfg, model = small
+    P, G = 6, 12
+    prompts = synth.decoder_prompts(cfg, 1, P, config=75)
+    dec = make(cfg, model, 1)
+    toks = dec.generate(prompts, G)[0]
+    assert np.array_equal(toks[:P], prompts[0]) and len(toks) == P + G
+    orc = oracle.decoder(cfg, model)
+    kc, vc = orc.new_cache()
+    for pos in range(P + G - 1):
+        lg = orc.step(kc, vc, pos, int(toks[pos])).astype(np.float64)
+        if pos + 1 < P:
+            continue
+        top = np.sort(lg)[-2:]
+        assert toks[pos + 1] == int(np.argmax(lg)) or top[1] - top[0] <= TOL * np.linalg.norm(lg), pos
+    with pytest.raises(Exception, match="steps already run"):
+        dec.prefill()
+    dec.close()
+
+
 def test_step_limits(small):
     import mythos_oil
     cfg, model = small
