@@ -163,6 +163,46 @@ __device__ __forceinline__ float4 slice_value4(const Slices& s, int t, int64_t m
     return sum;
 }
 
+// ---- RMSNorm split over the launches around it ---------------------------
+// y = W rms_norm(v) * gamma = inv * (W (v * gamma)), inv = 1 / sqrt(mean(v^2)
+// + eps), so a GEMV can take xg = v * gamma and its consumer scale the output
+// by inv.  The producer of the residual delta finishes the residual stream
+// in its epilogue (ResidOut): x <- y + x (the norm's residual add), xg = x *
+// gamma of the next norm, and per workgroup the sum of its rows' x^2 (double)
+// in ssp[token][workgroup].  The next small consumer (attention, SwiGLU)
+// reads NormScale: the sum over the nparts partials, in order.
+struct ResidOut {
+    float* x;             // null: off (plain output)
+    const float* gamma;
+    float* xg;
+    double* ssp;
+};
+struct NormScale {
+    const double* ssp;    // null: off
+    int nparts;
+    float dim, eps;
+};
+__device__ __forceinline__ double wave_sum_dbl(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+// 1 / sqrt(sum / dim + eps) of token t, computed by a whole workgroup of
+// NW waves (red: NW doubles of LDS); every thread gets it.
+template <int NW>
+__device__ __forceinline__ float norm_scale(const NormScale& ns, int t, double* red) {
+    double s = 0.0;
+    for (int i = threadIdx.x; i < ns.nparts; i += NW * 64) s += ns.ssp[(int64_t)t * ns.nparts + i];
+    s = wave_sum_dbl(s);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    s = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += red[w];
+    return (float)(1.0 / sqrt(s / (double)ns.dim + (double)ns.eps));
+}
+
 // ---- int8 helpers ---------------------------------------------------------
 // sum_{i<4} (int8)a.byte[i] * (int8)b.byte[i] + c   (v_dot4_i32_i8)
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

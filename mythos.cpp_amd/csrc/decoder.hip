@@ -38,6 +38,7 @@ struct mth_decoder {
     size_t kv_elem = 4;
     float* taps = nullptr;              // mth_decoder_set_taps
     float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr, *arg_v = nullptr;
+    double* ssp = nullptr;  // per-workgroup sums of squares of the split RMSNorm (ResidOut)
     int8_t* aq = nullptr;
     int *hist = nullptr, *step = nullptr, *ids = nullptr, *arg_i = nullptr;
     int64_t hist_stride = 0, layer_kv = 0;
@@ -190,6 +191,56 @@ hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
     return hipSuccess;
 }
 
+// One decode step of a single sequence with the RMSNorms split over the
+// launches around them (see enqueue_step).
+hipError_t enqueue_step_split_norm(const mth_decoder* d, hipStream_t s) {
+    const mth_decoder_config& c = d->c;
+    const int64_t H = c.hidden, F = c.ffn, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
+    hipError_t e;
+#define TRY(call)                        \
+    do {                                 \
+        if ((e = (call)) != hipSuccess) return e; \
+    } while (0)
+    using mth::plain_slices;
+    // x: residual stream, h: x * gamma of the next norm
+    mth::ResidOut ro{d->x, d->layers[0].attn_norm, d->h, d->ssp};
+    mth::NormScale ns{d->ssp, 1, (float)H, c.eps};
+    TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, 1, (int)H, (int)c.vocab, s, ro));
+    for (int64_t l = 0; l < c.layers; l++) {
+        const mth_decoder_layer& L = d->layers[(size_t)l];
+        char* kc = d->kc + l * d->layer_kv * d->kv_elem;
+        char* vc = d->vc + l * d->layer_kv * d->kv_elem;
+        TRY(qkv(d, L, d->h, d->q, d->k, d->v, 1, s));
+        TRY(mth::launch_rope_attention_slices(plain_slices(d->q, QD), plain_slices(d->k, KD), plain_slices(d->v, KD),
+                                              ns, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att, d->step,
+                                              1, (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
+        ro.gamma = L.ffn_norm;
+        TRY(mth::launch_oil8_gemv_resid(mth::Oil8Seg{L.wo, L.cbo, nullptr, H}, d->att, QD, ro, &ns.nparts, s));
+        if (gate_up_fused(d, L)) {
+            TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
+            TRY(mth::launch_silu_mul_quant_slices(plain_slices(d->gu, 2 * F), plain_slices(d->gu + F, 2 * F), ns,
+                                                  d->aq, d->a_inv, nullptr, 1, F, s));
+        } else {
+            TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
+            TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + F, F, H, s));
+            TRY(mth::launch_silu_mul_quant_slices(plain_slices(d->gu, F), plain_slices(d->gu + F, F), ns, d->aq,
+                                                  d->a_inv, nullptr, 1, F, s));
+        }
+        if (l + 1 < c.layers) {
+            ro.gamma = d->layers[(size_t)l + 1].attn_norm;
+            TRY(mth::launch_i2s_gemv_resid(L.wdown, L.down_scale, d->aq, d->a_inv, H, F, ro, &ns.nparts, s));
+        } else {
+            TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, 1, s));
+        }
+    }
+    TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, 1, H, c.eps, s));
+    TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
+    TRY(mth::launch_argmax(d->logits, 1, c.vocab, d->ids, d->hist, d->step, (int)d->hist_stride, (int)d->prompt_len,
+                           d->arg_v, d->arg_i, s));
+#undef TRY
+    return hipSuccess;
+}
+
 hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     const mth_decoder_config& c = d->c;
     const int64_t B = d->batch, H = c.hidden, F = c.ffn, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
@@ -208,6 +259,20 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     // only then overwritten.  Taps copy whole outputs, so they take the
     // reduced path (same sums in the same order).
     const bool fold = B >= 2 && B <= 16 && !d->taps;
+    // A single sequence splits each RMSNorm over the launches around it
+    // (ResidOut / NormScale, common.h): the O and down projections finish
+    // the residual stream and write x * gamma of the next norm with partial
+    // sums of squares, the Q/K/V and gate/up GEMVs take x * gamma as is, and
+    // the attention and the SwiGLU apply 1 / rms: no norm launches but the
+    // final one.
+    bool fold1 = B == 1 && !d->taps;
+    for (int64_t l = 0; fold1 && l < c.layers; l++) {
+        const mth_decoder_layer& L = d->layers[(size_t)l];
+        const mth::Oil8Seg o_seg{L.wo, L.cbo, nullptr, H};
+        fold1 = mth::oil8_segs_fusable(&o_seg, 1, QD) && ((uintptr_t)d->att & 15u) == 0 &&
+                (l + 1 == c.layers || mth::i2s_resid_supported(L.wdown, d->aq, H, F));
+    }
+    if (fold1) return enqueue_step_split_norm(d, s);
     const Slices none{nullptr, 0, 0, 0, 1.0f, nullptr};
     const int64_t tap_floats = mth_decoder_tap_floats(d);
     auto tap_copy = [&](float* dst, const void* src, size_t bytes) {
@@ -238,7 +303,8 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         } else {
             TRY(qkv(d, L, d->h, d->q, d->k, d->v, B, s));
         }
-        TRY(mth::launch_rope_attention_slices(sq, sk, sv, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
+        TRY(mth::launch_rope_attention_slices(sq, sk, sv, mth::NormScale{}, d->rope_cos, d->rope_sin, kc, vc,
+                                              c.kv_dtype == 1, d->att,
                                               d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim,
                                               (int)c.max_seq, s));
         // O projection; its output is added to the residual by the FFN norm
@@ -262,7 +328,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
             // to read the gate/up slices as fast as the reduction kernel)
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
             if (tp) TRY(tap_copy(tp_gu, d->gu, (size_t)(B * 2 * F) * 4));
-            TRY(mth::launch_silu_mul_quant_slices(sg, su, d->aq, d->a_inv, tp_act, B, F, s));
+            TRY(mth::launch_silu_mul_quant_slices(sg, su, mth::NormScale{}, d->aq, d->a_inv, tp_act, B, F, s));
         } else {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
@@ -368,6 +434,7 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->pf_k, (size_t)(PR * KD) * 4},  {(void**)&d->pf_v, (size_t)(PR * KD) * 4},
         {(void**)&d->pf_att, (size_t)(PR * QD) * 4}, {(void**)&d->pf_gu, (size_t)(PR * 2 * F) * 4},
         {(void**)&d->pf_aq, (size_t)(PR * F)},      {(void**)&d->pf_inv, (size_t)PR * 4},
+        {(void**)&d->ssp, (size_t)(H / 4 + 2) * 8},
     };
     size_t total = 0;
     for (const Slot& sl : slots) total += round_up(sl.bytes);

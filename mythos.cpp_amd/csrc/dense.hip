@@ -267,11 +267,14 @@ __device__ __forceinline__ uint2 kv_raw4(const uint16_t* p) { return *(const uin
 // Rows: grid.y = rows of q/out; row r is position (step ? *step : 0) + ctx0 +
 // r % np of sequence r / np (np = 1: one position per sequence, decode; np
 // > 1: the prompt rows of a prefill chunk, each attending causally).
+// ns (ROPE, NormScale in common.h): q/k/v are projections of x * gamma and
+// get the RMSNorm's 1 / rms here.
 template <int D, bool ROPE, typename KV>
-__global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices vin, const float* __restrict__ cos_t,
-                                                  const float* __restrict__ sin_t, KV* kc, KV* vc,
-                                                  float* __restrict__ out, const int* __restrict__ step, int ctx0,
-                                                  int np, int heads, int kv_heads, int max_seq, float scale) {
+__global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices vin, NormScale ns,
+                                                  const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                  KV* kc, KV* vc, float* __restrict__ out, const int* __restrict__ step,
+                                                  int ctx0, int np, int heads, int kv_heads, int max_seq,
+                                                  float scale) {
     typedef typename KvRaw4<KV>::type Raw;
     constexpr int G = D / 4;        // float4 column groups
     constexpr int SL = kT / G;      // position slices in P*V
@@ -289,18 +292,21 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     const int g = tid % G, sl = tid / G;
 
     if (ROPE) {
+        __shared__ double nred[kT / 64];
+        const float ni = ns.ssp ? norm_scale<kT / 64>(ns, row, nred) : 1.0f;
+        auto val = [&](const Slices& sl, int i) { return ns.ssp ? slice_value(sl, row, i) * ni : slice_value(sl, row, i); };
         const float* cr = cos_t + (int64_t)pos * (D / 2);
         const float* sr = sin_t + (int64_t)pos * (D / 2);
         if (tid < D / 2) {
             const float c = cr[tid], s = sr[tid];
-            const float q1 = slice_value(q, row, h * D + tid), q2 = slice_value(q, row, h * D + tid + D / 2);
+            const float q1 = val(q, h * D + tid), q2 = val(q, h * D + tid + D / 2);
             qs[tid] = q1 * c - q2 * s;
             qs[tid + D / 2] = q1 * s + q2 * c;
-            const float k1 = slice_value(kin, row, kh * D + tid), k2 = slice_value(kin, row, kh * D + tid + D / 2);
+            const float k1 = val(kin, kh * D + tid), k2 = val(kin, kh * D + tid + D / 2);
             ks[tid] = kv_rounded(k1 * c - k2 * s, KV{});
             ks[tid + D / 2] = kv_rounded(k1 * s + k2 * c, KV{});
-            vs[tid] = kv_rounded(slice_value(vin, row, kh * D + tid), KV{});
-            vs[tid + D / 2] = kv_rounded(slice_value(vin, row, kh * D + tid + D / 2), KV{});
+            vs[tid] = kv_rounded(val(vin, kh * D + tid), KV{});
+            vs[tid + D / 2] = kv_rounded(val(vin, kh * D + tid + D / 2), KV{});
         }
     } else {
         if (tid < D) qs[tid] = slice_value(q, row, h * D + tid);
@@ -428,10 +434,13 @@ constexpr int kSQT = 1024, kSQ = 12;
 // act (optional): the FP32 activations, [rows][n].
 // g, u: the gate and up outputs as Slices (common.h), so the split-K
 // partial sums of the GEMV are added here.
-__global__ __launch_bounds__(kSQT) void silu_mul_quant_k(Slices g, Slices u, int8_t* __restrict__ q,
+// ns (NormScale, common.h): g/u are projections of x * gamma and get the
+// RMSNorm's 1 / rms here.
+__global__ __launch_bounds__(kSQT) void silu_mul_quant_k(Slices g, Slices u, NormScale ns, int8_t* __restrict__ q,
                                                          float* __restrict__ inv_scale, float* __restrict__ act,
                                                          int n) {
     __shared__ float red[kSQT / 64];
+    __shared__ double nred[kSQT / 64];
     const int r = blockIdx.x, tid = threadIdx.x;
     float gv[kSQ], uv[kSQ];
     if (g.n == 1 && u.n == 1) {
@@ -449,6 +458,14 @@ __global__ __launch_bounds__(kSQT) void silu_mul_quant_k(Slices g, Slices u, int
             const int i = tid + j * kSQT;
             gv[j] = i < n ? slice_value(g, r, i) : 0.0f;
             uv[j] = i < n ? slice_value(u, r, i) : 0.0f;
+        }
+    }
+    if (ns.ssp) {
+        const float ni = norm_scale<kSQT / 64>(ns, r, nred);
+#pragma unroll
+        for (int j = 0; j < kSQ; ++j) {
+            gv[j] *= ni;
+            uv[j] *= ni;
         }
     }
     float m = 0.0f;
@@ -564,15 +581,31 @@ __global__ __launch_bounds__(kT) void argmax_final_k(const float* __restrict__ p
 }
 
 // x[b] = emb[id] with id = hist[b][*step] (ids outside [0, vocab) -> 0).
+// ro.x set: also xg = x * ro.gamma and ro.ssp[b] = sum x^2 (ResidOut,
+// common.h; one partial per token).
 __global__ __launch_bounds__(kT) void embed_k(const float* __restrict__ emb, const int* __restrict__ hist,
                                               const int* __restrict__ step, int hist_stride, float* __restrict__ x,
-                                              int dim, int vocab) {
+                                              int dim, int vocab, ResidOut ro) {
+    __shared__ double red[kT / 64];
     const int b = blockIdx.x;
     int id = hist[(int64_t)b * hist_stride + *step];
     if (id < 0 || id >= vocab) id = 0;
     const float* src = emb + (int64_t)id * dim;
     float* dst = x + (int64_t)b * dim;
-    for (int i = threadIdx.x * 4; i < dim; i += kT * 4) *(float4*)(dst + i) = ldf4(src + i);
+    double sq = 0.0;
+    for (int i = threadIdx.x * 4; i < dim; i += kT * 4) {
+        const float4 v = ldf4(src + i);
+        *(float4*)(dst + i) = v;
+        if (ro.x) {
+            const float4 g = ldf4(ro.gamma + i);
+            *(float4*)(ro.xg + (int64_t)b * dim + i) = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
+            sq += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+        }
+    }
+    if (ro.x) {
+        sq = block_sum(sq, red);
+        if (threadIdx.x == 0) ro.ssp[b] = sq;
+    }
 }
 
 // Prefill rows: row r is position p0 + r % np of sequence r / np.
@@ -683,30 +716,30 @@ bool attention_supported(int head_dim, int max_seq) {
 }
 
 template <bool ROPE, typename KV>
-static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
-                                const float* sin_t, KV* kc, KV* vc, float* out, const int* step, int ctx0,
-                                int64_t rows, int np, int heads, int kv_heads, int head_dim, int max_seq,
+static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& v, const NormScale& ns,
+                                const float* cos_t, const float* sin_t, KV* kc, KV* vc, float* out, const int* step,
+                                int ctx0, int64_t rows, int np, int heads, int kv_heads, int head_dim, int max_seq,
                                 hipStream_t s) {
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
     const dim3 grid((unsigned)heads, (unsigned)rows);
     if (head_dim == 64)
-        attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, np, heads,
-                                                        kv_heads, max_seq, scale);
+        attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
+                                                        heads, kv_heads, max_seq, scale);
     else if (head_dim == 128)
-        attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, np, heads,
-                                                         kv_heads, max_seq, scale);
+        attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
+                                                         heads, kv_heads, max_seq, scale);
     else
-        attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, cos_t, sin_t, kc, vc, out, step, ctx0, np, heads,
-                                                         kv_heads, max_seq, scale);
+        attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
+                                                         heads, kv_heads, max_seq, scale);
     return hipGetLastError();
 }
 
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const int* step, int ctx0,
                             int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
     const Slices qs = plain_slices(q, (int64_t)heads * head_dim), none{nullptr, 0, 0, 0, 1.0f, nullptr};
-    return run_attention<false, float>(qs, none, none, nullptr, nullptr, (float*)kc, (float*)vc, out, step, ctx0,
-                                       batch, 1, heads, kv_heads, head_dim, max_seq, s);
+    return run_attention<false, float>(qs, none, none, NormScale{}, nullptr, nullptr, (float*)kc, (float*)vc, out,
+                                       step, ctx0, batch, 1, heads, kv_heads, head_dim, max_seq, s);
 }
 
 hipError_t launch_attention_rows(const float* q, const void* kc, const void* vc, bool kv_bf16, float* out,
@@ -714,10 +747,11 @@ hipError_t launch_attention_rows(const float* q, const void* kc, const void* vc,
                                  hipStream_t s) {
     const Slices qs = plain_slices(q, (int64_t)heads * head_dim), none{nullptr, 0, 0, 0, 1.0f, nullptr};
     if (kv_bf16)
-        return run_attention<false, uint16_t>(qs, none, none, nullptr, nullptr, (uint16_t*)kc, (uint16_t*)vc, out,
-                                              nullptr, p0, rows, np, heads, kv_heads, head_dim, max_seq, s);
-    return run_attention<false, float>(qs, none, none, nullptr, nullptr, (float*)kc, (float*)vc, out, nullptr, p0,
-                                       rows, np, heads, kv_heads, head_dim, max_seq, s);
+        return run_attention<false, uint16_t>(qs, none, none, NormScale{}, nullptr, nullptr, (uint16_t*)kc,
+                                              (uint16_t*)vc, out, nullptr, p0, rows, np, heads, kv_heads, head_dim,
+                                              max_seq, s);
+    return run_attention<false, float>(qs, none, none, NormScale{}, nullptr, nullptr, (float*)kc, (float*)vc, out,
+                                       nullptr, p0, rows, np, heads, kv_heads, head_dim, max_seq, s);
 }
 
 hipError_t launch_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
@@ -725,33 +759,33 @@ hipError_t launch_rope_attention(const float* q, const float* k, const float* v,
                                  int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s) {
     return launch_rope_attention_slices(plain_slices(q, (int64_t)heads * head_dim),
                                         plain_slices(k, (int64_t)kv_heads * head_dim),
-                                        plain_slices(v, (int64_t)kv_heads * head_dim), cos_t, sin_t, kc, vc, kv_bf16,
-                                        out, step, batch, heads, kv_heads, head_dim, max_seq, s);
+                                        plain_slices(v, (int64_t)kv_heads * head_dim), NormScale{}, cos_t, sin_t, kc,
+                                        vc, kv_bf16, out, step, batch, heads, kv_heads, head_dim, max_seq, s);
 }
 
-hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
-                                        const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out,
-                                        const int* step, int64_t batch, int heads, int kv_heads, int head_dim,
-                                        int max_seq, hipStream_t s) {
+hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const Slices& v, const NormScale& ns,
+                                        const float* cos_t, const float* sin_t, void* kc, void* vc, bool kv_bf16,
+                                        float* out, const int* step, int64_t batch, int heads, int kv_heads,
+                                        int head_dim, int max_seq, hipStream_t s) {
     if (kv_bf16)
-        return run_attention<true, uint16_t>(q, k, v, cos_t, sin_t, (uint16_t*)kc, (uint16_t*)vc, out, step, 0,
+        return run_attention<true, uint16_t>(q, k, v, ns, cos_t, sin_t, (uint16_t*)kc, (uint16_t*)vc, out, step, 0,
                                              batch, 1, heads, kv_heads, head_dim, max_seq, s);
-    return run_attention<true, float>(q, k, v, cos_t, sin_t, (float*)kc, (float*)vc, out, step, 0, batch, 1, heads,
-                                      kv_heads, head_dim, max_seq, s);
+    return run_attention<true, float>(q, k, v, ns, cos_t, sin_t, (float*)kc, (float*)vc, out, step, 0, batch, 1,
+                                      heads, kv_heads, head_dim, max_seq, s);
 }
 
 bool silu_mul_quant_supported(int64_t n) { return n > 0 && n <= (int64_t)kSQT * kSQ; }
 
-hipError_t launch_silu_mul_quant_slices(const Slices& g, const Slices& u, int8_t* q, float* inv_scale, float* act,
-                                        int64_t rows, int64_t n, hipStream_t s) {
-    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, q, inv_scale, act, (int)n);
+hipError_t launch_silu_mul_quant_slices(const Slices& g, const Slices& u, const NormScale& ns, int8_t* q,
+                                        float* inv_scale, float* act, int64_t rows, int64_t n, hipStream_t s) {
+    silu_mul_quant_k<<<(unsigned)rows, kSQT, 0, s>>>(g, u, ns, q, inv_scale, act, (int)n);
     return hipGetLastError();
 }
 
 hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, float* act,
                                  int64_t rows, int64_t n, int64_t gstride, int64_t ustride, hipStream_t s) {
-    return launch_silu_mul_quant_slices(plain_slices(g, gstride), plain_slices(u, ustride), q, inv_scale, act, rows,
-                                        n, s);
+    return launch_silu_mul_quant_slices(plain_slices(g, gstride), plain_slices(u, ustride), NormScale{}, q, inv_scale,
+                                        act, rows, n, s);
 }
 
 int argmax_chunks(int64_t n) { return (int)((n + kArgChunk - 1) / kArgChunk); }
@@ -783,8 +817,8 @@ hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const f
 }
 
 hipError_t launch_embed(const float* emb, const int* hist, const int* step, int hist_stride, float* x, int64_t batch,
-                        int dim, int vocab, hipStream_t s) {
-    embed_k<<<(unsigned)batch, kT, 0, s>>>(emb, hist, step, hist_stride, x, dim, vocab);
+                        int dim, int vocab, hipStream_t s, const ResidOut& ro) {
+    embed_k<<<(unsigned)batch, kT, 0, s>>>(emb, hist, step, hist_stride, x, dim, vocab, ro);
     return hipGetLastError();
 }
 

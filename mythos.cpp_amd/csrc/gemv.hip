@@ -88,7 +88,7 @@ __device__ __forceinline__ float transposed_sum(float (&v)[R], int lane) {
 // save).
 template <int R>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4, 4)))
-void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch) {
+void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch, ResidOut ro) {
     __shared__ float tab[256];
     __shared__ float part[kWaves][R];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -141,8 +141,25 @@ void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch) {
         constexpr int L = MTH_WAVE / R;
         if ((lane % L) == 0) part[wave][lane / L] = s;
         __syncthreads();
-        if (tid < R && m0 + tid < M)
-            y[(int64_t)t * M + m0 + tid] = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+        if (wave == 0) {
+            const bool wr = lane < R && m0 + lane < M;
+            const float v = lane < R ? ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane] : 0.0f;
+            const int64_t i = (int64_t)t * M + m0 + lane;
+            if (!ro.x) {
+                if (wr) y[i] = v;
+            } else {
+                // residual epilogue (ResidOut, common.h): rows of this workgroup
+                double sq = 0.0;
+                if (wr) {
+                    const float r = v + ro.x[i];
+                    ro.x[i] = r;
+                    ro.xg[i] = r * ro.gamma[m0 + lane];
+                    sq = (double)r * r;
+                }
+                sq = wave_sum_dbl(sq);
+                if (lane == 0) ro.ssp[(int64_t)t * gridDim.x + blockIdx.x] = sq;
+            }
+        }
         __syncthreads();
     }
 }
@@ -683,7 +700,16 @@ hipError_t launch_oil8_gemv_segs(const Oil8Seg* seg, int nseg, const float* x, i
                                  hipStream_t s) {
     constexpr int R = 4;
     const Oil8SegArgs a = make_seg_args(seg, nseg, R);
-    oil8_gemv_k<R><<<seg_groups(seg, nseg, R), kWG, 0, s>>>(a, x, (int)K, (int)batch);
+    oil8_gemv_k<R><<<seg_groups(seg, nseg, R), kWG, 0, s>>>(a, x, (int)K, (int)batch, ResidOut{});
+    return hipGetLastError();
+}
+
+hipError_t launch_oil8_gemv_resid(const Oil8Seg& seg, const float* x, int64_t K, const ResidOut& ro, int* nparts,
+                                  hipStream_t s) {
+    constexpr int R = 4;
+    const Oil8SegArgs a = make_seg_args(&seg, 1, R);
+    *nparts = seg_groups(&seg, 1, R);
+    oil8_gemv_k<R><<<*nparts, kWG, 0, s>>>(a, x, (int)K, 1, ro);
     return hipGetLastError();
 }
 

@@ -29,6 +29,10 @@ hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x,
 bool oil8_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K);
 hipError_t launch_oil8_gemv_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
                                  hipStream_t s);
+// Batch 1 with the residual epilogue (ResidOut, common.h) in place of y
+// (seg.y unused; oil8_segs_fusable(&seg, 1, K)); *nparts: partials per token.
+hipError_t launch_oil8_gemv_resid(const Oil8Seg& seg, const float* x, int64_t K, const ResidOut& ro, int* nparts,
+                                  hipStream_t s);
 // Reference per-(m,n) indexing (src/kernel_oil8.cpp:20-24):
 // out[r] = sum_k cb[idx[r*K + k]] * act[(r % N)*K + k],  r < M*N
 hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float* act, float* out,
@@ -89,6 +93,11 @@ hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t
 hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
                                     float* y, int64_t M, int64_t K, int64_t batch, float* partial, Slices* out,
                                     hipStream_t s);
+// Batch 1, int8 activations, with the residual epilogue (ResidOut,
+// common.h) in place of y; *nparts: partials per token.
+bool i2s_resid_supported(const uint8_t* packed, const int8_t* act, int64_t M, int64_t K);
+hipError_t launch_i2s_gemv_resid(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
+                                 int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s);
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 // ws: null (one wave per output) or i2s_gemm_workspace_bytes(M, N, K) bytes of
@@ -142,10 +151,11 @@ hipError_t launch_rope_attention(const float* q, const float* k, const float* v,
                                  const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out, const int* step,
                                  int64_t batch, int heads, int kv_heads, int head_dim, int max_seq, hipStream_t s);
 // q/k/v as Slices (common.h): rows of heads*head_dim / kv_heads*head_dim.
-hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const Slices& v, const float* cos_t,
-                                        const float* sin_t, void* kc, void* vc, bool kv_bf16, float* out,
-                                        const int* step, int64_t batch, int heads, int kv_heads, int head_dim,
-                                        int max_seq, hipStream_t s);
+// ns (common.h): q/k/v projected from x * gamma, scaled by the norm here.
+hipError_t launch_rope_attention_slices(const Slices& q, const Slices& k, const Slices& v, const NormScale& ns,
+                                        const float* cos_t, const float* sin_t, void* kc, void* vc, bool kv_bf16,
+                                        float* out, const int* step, int64_t batch, int heads, int kv_heads,
+                                        int head_dim, int max_seq, hipStream_t s);
 // Prefill rows: row r is position p0 + r % np of sequence r / np.
 // Attention of each row over the cache positions 0 .. its own (q rotated).
 hipError_t launch_attention_rows(const float* q, const void* kc, const void* vc, bool kv_bf16, float* out,
@@ -162,8 +172,8 @@ hipError_t launch_embed_rows(const float* emb, const int* hist, int hist_stride,
 // act (nullable) receives the FP32 activations [rows][n].
 bool silu_mul_quant_supported(int64_t n);
 // g/u as Slices (common.h)
-hipError_t launch_silu_mul_quant_slices(const Slices& g, const Slices& u, int8_t* q, float* inv_scale, float* act,
-                                        int64_t rows, int64_t n, hipStream_t s);
+hipError_t launch_silu_mul_quant_slices(const Slices& g, const Slices& u, const NormScale& ns, int8_t* q,
+                                        float* inv_scale, float* act, int64_t rows, int64_t n, hipStream_t s);
 hipError_t launch_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, float* act,
                                  int64_t rows, int64_t n, int64_t gstride, int64_t ustride, hipStream_t s);
 // Greedy argmax in two launches; pv/pi: rows * argmax_chunks(n) partials.
@@ -172,6 +182,6 @@ int argmax_chunks(int64_t n);
 hipError_t launch_argmax(const float* logits, int64_t rows, int64_t n, int* ids, int* hist, int* step,
                          int hist_stride, int prompt_len, float* pv, int* pi, hipStream_t s);
 hipError_t launch_embed(const float* emb, const int* hist, const int* step, int hist_stride, float* x, int64_t batch,
-                        int dim, int vocab, hipStream_t s);
+                        int dim, int vocab, hipStream_t s, const ResidOut& ro = ResidOut{});
 
 }  // namespace mth

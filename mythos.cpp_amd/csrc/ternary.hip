@@ -89,10 +89,11 @@ template <int LPR, int NSEG, bool FUSED>
 __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
     const uint8_t* packed, float w_scale, const float* __restrict__ x,
     const int8_t* __restrict__ act, const float* __restrict__ act_scale, float* __restrict__ y,
-    int M, int K, int batch) {
+    int M, int K, int batch, ResidOut res) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     int8_t* q = (int8_t*)lds_raw;
     __shared__ float red[kWaves];
+    __shared__ double rsq[kWaves];
     constexpr int RPP = MTH_WAVE / LPR;          // rows per wave
     constexpr int XQ = (64 * LPR * NSEG) / 1024;  // float4 of x per thread (K <= 64*LPR*NSEG)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -205,7 +206,24 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
                 acc = tdot16(sv ? w[s].w : pad, A[s][3], acc);
             }
             acc = group_sum_i<LPR>(acc - asum);
-            if (li == 0 && rv) y[(int64_t)t * M + row] = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
+            const float v = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
+            const int64_t i = (int64_t)t * M + row;
+            if (!res.x) {
+                if (li == 0 && rv) y[i] = v;
+            } else {
+                // residual epilogue (ResidOut, common.h): rows of this workgroup
+                double sq = 0.0;
+                if (li == 0 && rv) {
+                    const float r = v + res.x[i];
+                    res.x[i] = r;
+                    res.xg[i] = r * res.gamma[row];
+                    sq = (double)r * r;
+                }
+                sq = wave_sum_dbl(sq);
+                if (lane == 0) rsq[wave] = sq;
+                __syncthreads();
+                if (tid == 0) res.ssp[(int64_t)t * gridDim.x + blockIdx.x] = ((rsq[0] + rsq[1]) + rsq[2]) + rsq[3];
+            }
         }
     }
 }
@@ -759,10 +777,21 @@ hipError_t run_i2s_fast(const uint8_t* packed, float w_scale, const float* x, co
     const size_t lds = (size_t)((K + 15) / 16) * 16;
     if (x)
         i2s_gemv_fast<LPR, NSEG, true><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M,
-                                                               (int)K, (int)batch);
+                                                               (int)K, (int)batch, ResidOut{});
     else
         i2s_gemv_fast<LPR, NSEG, false><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M,
-                                                                (int)K, (int)batch);
+                                                                (int)K, (int)batch, ResidOut{});
+    return hipGetLastError();
+}
+
+template <int LPR, int NSEG>
+hipError_t run_i2s_fast_resid(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
+                              int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s) {
+    constexpr int RPP = MTH_WAVE / LPR;
+    *nparts = ceil_div(M, RPP * kWaves);
+    const size_t lds = (size_t)((K + 15) / 16) * 16;
+    i2s_gemv_fast<LPR, NSEG, false><<<*nparts, kWG, lds, s>>>(packed, w_scale, nullptr, act, act_scale, nullptr,
+                                                              (int)M, (int)K, 1, ro);
     return hipGetLastError();
 }
 
@@ -785,6 +814,21 @@ hipError_t launch_tl_precompute_lut(const int8_t* act, int8_t* lut, int64_t K, i
     if (groups == 0) return hipSuccess;
     tl_lut_k<<<ceil_div(groups, kWG), kWG, 0, s>>>(act, lut, groups, group);
     return hipGetLastError();
+}
+
+bool i2s_resid_supported(const uint8_t* packed, const int8_t* act, int64_t M, int64_t K) {
+    return K % 64 == 0 && K / 64 <= 256 && M < (1ll << 31) && aligned16(packed) && aligned16(act);
+}
+
+hipError_t launch_i2s_gemv_resid(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
+                                 int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s) {
+    const int64_t nseg = K / 64;
+    if (nseg <= 16) return run_i2s_fast_resid<16, 1>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
+    if (nseg <= 32) return run_i2s_fast_resid<16, 2>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
+    if (nseg <= 64) return run_i2s_fast_resid<32, 2>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
+    if (nseg <= 128) return run_i2s_fast_resid<32, 4>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
+    if (nseg <= 192) return run_i2s_fast_resid<64, 3>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
+    return run_i2s_fast_resid<64, 4>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
 }
 
 hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x, const int8_t* act,

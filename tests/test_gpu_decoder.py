@@ -326,6 +326,25 @@ def test_mid_batched_kernels_per_layer(batch, kv, mid, oracle):
     dec.close()
 
 
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_mid_b1_split_norm(kv, mid, oracle):
+    """Batch 1 with real ternary weights: the split RMSNorm (1 / rms applied
+    in the attention and in the SwiGLU) against the oracle's teacher-forced
+    logits, graph-replayed steps."""
+    cfg, model = mid
+    P = 6
+    prompts = synth.decoder_prompts(cfg, 1, P, config=79)
+    dec = make(cfg, model, 1, kv)
+    dec.start(prompts)
+    orc = oracle.decoder(oracle_cfg(cfg, kv), model)
+    kc, vc = orc.new_cache()
+    for pos in range(P):
+        dec.step(1)
+        err = rel(dec.logits()[0], orc.step(kc, vc, pos, int(prompts[0, pos]), threads=THREADS))
+        assert err < TOL, (pos, err)
+    dec.close()
+
+
 def test_mid_graph_batch_matches_taps_run(mid):
     """The graph-replayed batch-16 step gives the same logits, bit for bit,
     as the eager step with taps on (the taps only add copies)."""
@@ -348,6 +367,28 @@ def config5():
     cfg = synth.decoder_config()
     print("decoder config 5: generating weights", flush=True)
     return cfg, synth.decoder_model(cfg)
+
+
+def test_config5_b1_exact_path(config5, oracle):
+    """Config 5 at batch 1 (the RMSNorms split over the launches around
+    them: residual epilogues in the O / down projections, 1 / rms in the
+    attention) with every ternary down weight 0, so no int8 rounding
+    boundary is involved: logits within FP32 tolerance of the oracle over
+    three teacher-forced steps."""
+    cfg, model = config5
+    steps = 3
+    zero = dict(model, layers=[dict(ly, wdown=np.full_like(ly["wdown"], 0x55)) for ly in model["layers"]])
+    prompts = synth.decoder_prompts(cfg, 1, steps, config=66)
+    dec = make(cfg, zero, 1)
+    dec.start(prompts)
+    orc = oracle.decoder(dict(cfg, max_seq=steps), zero)
+    kc, vc = orc.new_cache()
+    for pos in range(steps):
+        print(f"decoder config 5 b=1 exact path: step {pos}", flush=True)
+        dec.step(1)
+        err = rel(dec.logits()[0], orc.step(kc, vc, pos, int(prompts[0, pos]), threads=THREADS))
+        assert err < TOL, (pos, err)
+    dec.close()
 
 
 def test_config5_b16_exact_path(config5, oracle):
