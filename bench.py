@@ -223,23 +223,34 @@ def bench_decode(dev, batches=(1, 16), kv_dtype="bf16"):
     return out
 
 
-def cpu_baseline_oil4(packed, cbs, x, M, K, block, budget_s):
+def cpu_baseline_oil4(packed, cbs, x, M, K, block, budget_s, threads=1):
     """Oracle (CPU restatement of src/kernel_oil4.cpp:31-54 with per-block
-    codebooks), one thread, whole GEMVs repeated for ~budget_s seconds."""
+    codebooks; OpenMP over rows), whole GEMVs repeated for ~budget_s
+    seconds on `threads` host threads."""
     sys.path.insert(0, ROOT)
     from oracle import Oracle
     o = Oracle()
     xb = np.ascontiguousarray(x[:1])
     pr = np.ascontiguousarray(packed.ravel())
-    o.oil4_gemv_blocked(pr, cbs, xb, M, K, 1, block, threads=1)  # warm-up
+    o.oil4_gemv_blocked(pr, cbs, xb, M, K, 1, block, threads=threads)  # warm-up
     t0, n = time.perf_counter(), 0
     while True:
-        o.oil4_gemv_blocked(pr, cbs, xb, M, K, 1, block, threads=1)
+        o.oil4_gemv_blocked(pr, cbs, xb, M, K, 1, block, threads=threads)
         n += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
     return el / n, n
+
+
+def cpu_threads():
+    """Host threads for the all-cores baseline: the cores this process may
+    use, at most 16 (one GPU's share of the host on the measurement box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 def cpu_reference_oil8(idx, cb, x, M, K, budget_s):
@@ -282,6 +293,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,prefill,ternary_gemm,decode (default all)")
+    ap.add_argument("--decode-batches", default="1,16", help="comma list of decode batch sizes (config 5)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -309,26 +321,26 @@ def main():
         r, _ = bench_oil4_gemv(mth, dev, 11008, 4096, 16, args.steps, args.warmup)
         gbs = r["bytes"] / r["sec"] / 1e9
         extra["oil4_gemv_11008x4096_b16"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                                 bytes=r["bytes"], copies=r["copies"])
+                                                 bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("oil4_gemv_11008x4096_b16"))
         log(f"oil4 b=16: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
     oil8_data = None
     if want("oil8"):
         r, oil8_data = bench_oil8_gemv(mth, dev, 4096, 4096, 1, args.steps, args.warmup)
         gbs = r["bytes"] / r["sec"] / 1e9
         extra["oil8_gemv_4096x4096_b1"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                               bytes=r["bytes"], copies=r["copies"])
+                                               bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("oil8_gemv_4096x4096_b1"))
         log(f"oil8 b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
     if want("oil8b16"):
         r, _ = bench_oil8_gemv(mth, dev, 4096, 4096, 16, args.steps, args.warmup)
         gbs = r["bytes"] / r["sec"] / 1e9
         extra["oil8_gemv_4096x4096_b16"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                                bytes=r["bytes"], copies=r["copies"])
+                                                bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("oil8_gemv_4096x4096_b16"))
         log(f"oil8 b=16: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
     if want("i2s"):
         r, _ = bench_i2s_gemv(mth, dev, 4096, 4096, 1, args.steps, args.warmup)
         gbs = r["bytes"] / r["sec"] / 1e9
         extra["i2s_gemv_4096x4096_b1"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                              bytes=r["bytes"], copies=r["copies"])
+                                              bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("i2s_gemv_4096x4096_b1"))
         log(f"i2s b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
     if want("prefill"):
         r = bench_prefill(mth, dev, 512, 14336, 4096, args.steps, args.warmup)
@@ -345,15 +357,22 @@ def main():
         log(f"ternary gemm: {r['sec']*1e6:.1f} us/launch, {tops:.0f} TOP/s ({tops/I8_PEAK_TOPS:.1%} of int8 MFMA)")
 
     if want("decode"):
-        extra.update(bench_decode(dev))
+        extra.update(bench_decode(dev, tuple(int(b) for b in args.decode_batches.split(","))))
 
     cpu = None
     if head is not None:
         packed, cbs, x = head["data"]
-        sec_cpu, n_cpu = cpu_baseline_oil4(packed, cbs, x, head["M"], head["K"], 128, args.cpu_seconds)
-        cpu = dict(value=head["r"]["bytes"] / sec_cpu / 1e9, unit="GB/s", cores=1, kind="port",
-                   sample=f"{n_cpu} whole OIL4 GEMVs 11008x4096 b=1 (oracle, 1 thread), {sec_cpu*1e3:.1f} ms each")
-        log(f"cpu port: {sec_cpu*1e3:.1f} ms/GEMV")
+        nt = cpu_threads()
+        sec_cpu, n_cpu = cpu_baseline_oil4(packed, cbs, x, head["M"], head["K"], 128, args.cpu_seconds / 2, nt)
+        cpu = dict(value=head["r"]["bytes"] / sec_cpu / 1e9, unit="GB/s", cores=nt, kind="port",
+                   sample=f"{n_cpu} whole OIL4 GEMVs 11008x4096 b=1 (oracle, {nt} OpenMP threads), "
+                          f"{sec_cpu*1e3:.2f} ms each")
+        log(f"cpu port, {nt} threads: {sec_cpu*1e3:.2f} ms/GEMV")
+        sec1, n1 = cpu_baseline_oil4(packed, cbs, x, head["M"], head["K"], 128, args.cpu_seconds / 2, 1)
+        extra["cpu_baseline_1thread"] = dict(value=head["r"]["bytes"] / sec1 / 1e9, unit="GB/s", cores=1,
+                                             kind="port", sample=f"{n1} whole OIL4 GEMVs 11008x4096 b=1 "
+                                                                 f"(oracle, 1 thread), {sec1*1e3:.1f} ms each")
+        log(f"cpu port, 1 thread: {sec1*1e3:.1f} ms/GEMV")
     if oil8_data is not None:
         idx, cb, x = oil8_data
         ref = cpu_reference_oil8(idx, cb, x, 4096, 4096, min(4.0, args.cpu_seconds / 3))
