@@ -14,8 +14,10 @@ import os
 import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmythos_oil.so")
-HOST_LIB_PATH = os.path.join(_HERE, "libmythos_host.so")
+# MYTHOS_OIL_LIB / MYTHOS_HOST_LIB select other builds of the two libraries
+# (the sanitizer builds of `make -C mythos.cpp_amd sanitize`, for example).
+LIB_PATH = os.environ.get("MYTHOS_OIL_LIB") or os.path.join(_HERE, "libmythos_oil.so")
+HOST_LIB_PATH = os.environ.get("MYTHOS_HOST_LIB") or os.path.join(_HERE, "libmythos_host.so")
 
 # Every extern "C" symbol declared in include/mythos_oil.h.
 EXPORTS = (

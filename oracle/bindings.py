@@ -16,7 +16,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def oracle_lib_path() -> str:
-    return os.path.join(_HERE, "liboracle.so")
+    """liboracle.so, or the build MYTHOS_ORACLE_LIB names (the sanitizer
+    build of `make -C oracle sanitize`)."""
+    return os.environ.get("MYTHOS_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 
 
 def ref_lib_path(variant: str = "avx2") -> str:
