@@ -129,6 +129,22 @@ def bench_i2s_gemv(mth, dev, M, K, batch, steps, warmup):
     return dict(sec=sec, steps=n, bytes=alg, copies=len(ps)), (packed, w_scale, x)
 
 
+def bench_i2s_gemv_i8(mth, dev, M, K, batch, steps, warmup):
+    """I2_S GEMV on int8 activations (the decoder's down projection)."""
+    import synth
+    import torch
+    packed, w_scale, x = synth.ternary(M, K, batch)
+    q = np.random.default_rng(7).integers(-127, 128, (batch, K), dtype=np.int8)
+    inv = np.full(batch, 0.01, np.float32)
+    p_d, q_d, inv_d = dev_copy(packed, dev), dev_copy(q, dev), dev_copy(inv, dev)
+    y_d = torch.empty(batch * M, dtype=torch.float32, device=dev)
+    ps = replicate(p_d, packed.nbytes)
+    sec, n = time_graph(lambda i: mth.i2s_gemv(ps[i], float(w_scale), q_d, inv_d, y_d, M, K, batch), len(ps), steps,
+                        warmup)
+    alg = packed.nbytes + 4 + q.nbytes + inv.nbytes + 4 * M * batch
+    return dict(sec=sec, steps=n, bytes=alg, copies=len(ps))
+
+
 def bench_prefill(mth, dev, M, N, K, steps, warmup, block=128):
     import synth
     import torch
@@ -292,7 +308,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,prefill,ternary_gemm,decode (default all)")
+    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,i2sb16,prefill,ternary_gemm,decode (default all)")
     ap.add_argument("--decode-batches", default="1,16", help="comma list of decode batch sizes (config 5)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -342,6 +358,12 @@ def main():
         extra["i2s_gemv_4096x4096_b1"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
                                               bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("i2s_gemv_4096x4096_b1"))
         log(f"i2s b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
+    if want("i2sb16"):
+        r = bench_i2s_gemv_i8(mth, dev, 4096, 11008, 16, args.steps, args.warmup)
+        gbs = r["bytes"] / r["sec"] / 1e9
+        extra["i2s_gemv_4096x11008_b16_int8"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
+                                                     bytes=r["bytes"], copies=r["copies"])
+        log(f"i2s b=16 (int8 acts, 4096x11008): {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
     if want("prefill"):
         r = bench_prefill(mth, dev, 512, 14336, 4096, args.steps, args.warmup)
         tf = r["flop"] / r["sec"] / 1e12

@@ -291,25 +291,26 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     const int nmem = ROPE ? pos : ctx;  // positions read from the cache
     const int g = tid % G, sl = tid / G;
 
+    // Every load before the first use, in order of use: the norm's partial
+    // sums and the current token's q/k/v (and RoPE angles), then this
+    // thread's K row of the first tile, then its V rows.
+    double nsum = 0.0;
+    if (ROPE && ns.ssp)
+        for (int i = tid; i < ns.nparts; i += kT) nsum += ns.ssp[(int64_t)row * ns.nparts + i];
+    float q1 = 0.0f, q2 = 0.0f, k1 = 0.0f, k2 = 0.0f, v1 = 0.0f, v2 = 0.0f, c = 0.0f, sn = 0.0f;
     if (ROPE) {
-        __shared__ double nred[kT / 64];
-        const float ni = ns.ssp ? norm_scale<kT / 64>(ns, row, nred) : 1.0f;
-        auto val = [&](const Slices& sl, int i) { return ns.ssp ? slice_value(sl, row, i) * ni : slice_value(sl, row, i); };
-        const float* cr = cos_t + (int64_t)pos * (D / 2);
-        const float* sr = sin_t + (int64_t)pos * (D / 2);
         if (tid < D / 2) {
-            const float c = cr[tid], s = sr[tid];
-            const float q1 = val(q, h * D + tid), q2 = val(q, h * D + tid + D / 2);
-            qs[tid] = q1 * c - q2 * s;
-            qs[tid + D / 2] = q1 * s + q2 * c;
-            const float k1 = val(kin, kh * D + tid), k2 = val(kin, kh * D + tid + D / 2);
-            ks[tid] = kv_rounded(k1 * c - k2 * s, KV{});
-            ks[tid + D / 2] = kv_rounded(k1 * s + k2 * c, KV{});
-            vs[tid] = kv_rounded(val(vin, kh * D + tid), KV{});
-            vs[tid + D / 2] = kv_rounded(val(vin, kh * D + tid + D / 2), KV{});
+            q1 = slice_value(q, row, h * D + tid);
+            q2 = slice_value(q, row, h * D + tid + D / 2);
+            k1 = slice_value(kin, row, kh * D + tid);
+            k2 = slice_value(kin, row, kh * D + tid + D / 2);
+            v1 = slice_value(vin, row, kh * D + tid);
+            v2 = slice_value(vin, row, kh * D + tid + D / 2);
+            c = cos_t[(int64_t)pos * (D / 2) + tid];
+            sn = sin_t[(int64_t)pos * (D / 2) + tid];
         }
-    } else {
-        if (tid < D) qs[tid] = slice_value(q, row, h * D + tid);
+    } else if (tid < D) {
+        q1 = slice_value(q, row, h * D + tid);
     }
     // cache rows: this thread's K row of the first tile, then its V rows
     Raw kr0[D / 4];
@@ -325,6 +326,30 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     for (int j = 0; j < VP; ++j) {
         const int t = sl + SL * j;
         vpre[j] = kv_raw4(vcol + (int64_t)(t < nmem ? t : 0) * D);
+    }
+    if (ROPE) {
+        __shared__ double nred[kT / 64];
+        float ni = 1.0f;
+        if (ns.ssp) {  // the RMSNorm's 1 / rms (NormScale): same sum as norm_scale
+            const double sum = wave_sum_dbl(nsum);
+            if ((tid & 63) == 0) nred[tid >> 6] = sum;
+            __syncthreads();
+            double t = 0.0;
+#pragma unroll
+            for (int w = 0; w < kT / 64; ++w) t += nred[w];
+            ni = (float)(1.0 / sqrt(t / (double)ns.dim + (double)ns.eps));
+            q1 *= ni, q2 *= ni, k1 *= ni, k2 *= ni, v1 *= ni, v2 *= ni;
+        }
+        if (tid < D / 2) {
+            qs[tid] = q1 * c - q2 * sn;
+            qs[tid + D / 2] = q1 * sn + q2 * c;
+            ks[tid] = kv_rounded(k1 * c - k2 * sn, KV{});
+            ks[tid + D / 2] = kv_rounded(k1 * sn + k2 * c, KV{});
+            vs[tid] = kv_rounded(v1, KV{});
+            vs[tid + D / 2] = kv_rounded(v2, KV{});
+        }
+    } else if (tid < D) {
+        qs[tid] = q1;
     }
     __syncthreads();  // qs, ks, vs
     if (ROPE && h < kv_heads && tid < D) {

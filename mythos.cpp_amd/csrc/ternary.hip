@@ -21,6 +21,8 @@
 //     computed once;
 //   * the int32 row sum is reduced across the LPR lanes and the epilogue is
 //     ((float)sum * w_scale) * inv_scale, exactly the reference's order.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
@@ -518,19 +520,25 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // ---------------------------------------------------------------------------
 // y[t][m] = ((float)sum_k t(m,k) * q[t][k] * w_scale) * act_scale[t], the
 // sum exact in int32, as src/kernel_i2s.cpp:32-40 per row and token.
-// Workgroup = 4 waves x 16 rows and a K slice of whole 256-column
-// super-chunks; grid = (ceil(M / 64), S).  Per super-chunk, lane l (row
-// r = l % 16, group g = l / 16) loads the 16 code bytes of its row at
-// columns 64g .. 64g + 63 and feeds 4 MFMAs; in MFMA j its A operand is the
-// u-codes (t + 1, code 3 read as 2) of columns 64g + 16j .. +15 in the byte
-// order (col 4i + s at byte i of dword s), and its B operand the activations
-// of token r at the same columns in the same order (transposed once per
-// workgroup while staging into LDS).  So D = sum (t + 1) q, and the kernel
-// subtracts sum q (accumulated while staging) to get sum t q.  With S > 1
-// every slice writes its exact integer partial (|sum| < 2^24, exact in
-// FP32) and i2s_bt_reduce adds them in order and applies the epilogue.
+// Workgroup = WV waves x 16 rows and a K slice of whole 256-column chunks;
+// grid = (ceil(M / (16 WV)), S).  Per chunk, lane l (row r = l % 16, group
+// g = l / 16) holds the 16 code bytes of its row at columns 64g .. 64g + 63
+// and feeds 4 MFMAs; in MFMA j its A operand is the u-codes (t + 1, code 3
+// read as 2) of columns 64g + 16j .. +15 in the byte order (col 4i + s at
+// byte i of dword s), and its B operand the activations of token r at the
+// same columns in the same order (transposed while staging into LDS).  So
+// D = sum (t + 1) q, and the kernel subtracts sum q (accumulated while
+// staging) to get sum t q.
+// Loads: the CU returns loads in issue order across its waves, so every
+// wave first issues the slice's activations (up to MAXC chunks: thread =
+// token, 16-column group), then, after a barrier, all its weight loads of
+// the slice; the activations are staged once and the chunk loop has no
+// barrier.  Slices longer than MAXC chunks run in rounds.  With S > 1 every
+// slice writes its exact integer partial (|sum| < 2^24, exact in FP32) and
+// i2s_bt_reduce (or the consumer, as Slices) adds them in order and applies
+// the epilogue.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-constexpr int kIbRows = 64, kIbTok = 16;
+constexpr int kIbWaves = 8, kIbRows = 16 * kIbWaves, kIbTok = 16, kIbChunks = 8, kIbTokStride = 68;
 
 __device__ __forceinline__ uint32_t byte_t4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, int s) {
     // byte i of the result = byte s of the i-th input
@@ -538,52 +546,93 @@ __device__ __forceinline__ uint32_t byte_t4x4(uint32_t a, uint32_t b, uint32_t c
            (((d >> (8 * s)) & 0xffu) << 24);
 }
 
-__global__ __launch_bounds__(kWG) void i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act,
-                                                   const float* __restrict__ act_scale, float* __restrict__ y,
-                                                   float* __restrict__ partial, int M, int K, int batch) {
-    __shared__ __align__(16) uint32_t qs[2][kIbTok * 16 * 4];  // [token][16-col group][4 dwords]
-    __shared__ int asum_p[kIbTok][16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.x * kIbRows + wave * 16;
-    const int nsc = K / 256, S = gridDim.y;
-    const int sc0 = (int)((int64_t)blockIdx.y * nsc / S), sc1 = (int)((int64_t)(blockIdx.y + 1) * nsc / S);
-    const int bpr = K / 4;
-    const uint8_t* wrow = packed + (int64_t)min(m0 + r, M - 1) * bpr + 16 * g;  // clamped rows
-    // staging: thread = (token st, 16-column group sg)
-    const int st = tid >> 4, sg = tid & 15;
-    const bool sv = st < batch;
-    const int8_t* arow = act + (int64_t)(sv ? st : 0) * K + 16 * sg;
-    uint4 an = sv ? ld16(arow + sc0 * 256) : make_uint4(0, 0, 0, 0);
-    uint4 wn = ld_stream(wrow + sc0 * 64);
-    int asum = 0;
-    i32x4 acc = {0, 0, 0, 0};
-    for (int c = sc0; c < sc1; ++c) {
-        uint32_t* qb = qs[c & 1];
-        {
-            const uint32_t a4[4] = {an.x, an.y, an.z, an.w};  // columns 16sg + 4i + s at byte s of a4[i]
+// One round of NC chunks (NC is the exact count, so every load below is
+// unconditional straight-line code and the waits before the staging and the
+// MFMAs count only what they need).
+template <int NC>
+__device__ __forceinline__ void ib_round(const uint8_t* wrow, const int8_t* arow, bool sv, bool stager, int c0,
+                                         bool first, uint32_t (*qs)[kIbTok * kIbTokStride], int st, int sg, int r,
+                                         int g, int& asum, i32x4& acc) {
+    uint4 an[NC], wv[NC];
+    if (stager) {
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) qb[(st * 16 + sg) * 4 + s2] = byte_t4x4(a4[0], a4[1], a4[2], a4[3], s2);
+        for (int c = 0; c < NC; ++c) an[c] = ld16(arow + (int64_t)(c0 + c) * 256);  // a clamped row if !sv
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();  // every wave's activations are issued before any weights
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) wv[c] = ld_stream(wrow + (int64_t)(c0 + c) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!first) __syncthreads();  // the previous round's chunks have been read
+    if (stager) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint32_t a4[4] = {sv ? an[c].x : 0u, sv ? an[c].y : 0u, sv ? an[c].z : 0u, sv ? an[c].w : 0u};
+            // col 16sg + 4i + s at byte s of a4[i]
+            uint4 o;
+            o.x = byte_t4x4(a4[0], a4[1], a4[2], a4[3], 0);
+            o.y = byte_t4x4(a4[0], a4[1], a4[2], a4[3], 1);
+            o.z = byte_t4x4(a4[0], a4[1], a4[2], a4[3], 2);
+            o.w = byte_t4x4(a4[0], a4[1], a4[2], a4[3], 3);
+            *(uint4*)&qs[c][st * kIbTokStride + sg * 4] = o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) asum = dot4(a4[i], 0x01010101u, asum);
         }
-        __syncthreads();
-        const uint4 w = wn;
-        if (c + 1 < sc1) {
-            wn = ld_stream(wrow + (c + 1) * 64);
-            if (sv) an = ld16(arow + (c + 1) * 256);
-        }
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t wd[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t u = ucode(wd[j]);
             const i32x4 a = {(int)(u & 0x03030303u), (int)((u >> 2) & 0x03030303u), (int)((u >> 4) & 0x03030303u),
                              (int)((u >> 6) & 0x03030303u)};
-            const i32x4 b = *(const i32x4*)(qb + (r * 16 + 4 * g + j) * 4);
+            const i32x4 b = *(const i32x4*)(&qs[c][r * kIbTokStride + (4 * g + j) * 4]);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
         }
     }
-    asum_p[st][sg] = asum;
+}
+
+template <int MAXC, int WV>
+__global__ __launch_bounds__(WV * 64) void i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act,
+                                                       const float* __restrict__ act_scale, float* __restrict__ y,
+                                                       float* __restrict__ partial, int M, int K, int batch) {
+    static_assert(MAXC >= 1 && MAXC <= 8, "ib_round is dispatched for 1..8 chunks");
+    // [chunk][token][16-col group][4 dwords], token stride kIbTokStride (64 + 4 dwords: the 16 tokens of an
+    // MFMA operand read land on distinct banks)
+    __shared__ __align__(16) uint32_t qs[MAXC][kIbTok * kIbTokStride];
+    __shared__ int asum_p[kIbTok][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.x * (WV * 16) + wave * 16;
+    const int nsc = K / 256, S = gridDim.y;
+    const int sc0 = (int)((int64_t)blockIdx.y * nsc / S), sc1 = (int)((int64_t)(blockIdx.y + 1) * nsc / S);
+    const int bpr = K / 4;
+    const uint8_t* wrow = packed + (int64_t)min(m0 + r, M - 1) * bpr + 16 * g;  // clamped rows
+    // staging by the first 4 waves: thread = token st, 16-column group sg
+    const int st = (tid >> 4) & 15, sg = tid & 15;
+    const bool stager = __builtin_amdgcn_readfirstlane(wave) < 4;
+    const bool sv = st < batch;
+    const int8_t* arow = act + (int64_t)(sv ? st : 0) * K + 16 * sg;
+    int asum = 0;
+    i32x4 acc = {0, 0, 0, 0};
+    for (int c0 = sc0; c0 < sc1; c0 += MAXC) {
+        const int nc = min(MAXC, sc1 - c0);
+        const bool first = c0 == sc0;
+        switch (nc) {
+            case 1: ib_round<1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 2: ib_round<2>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 3: ib_round<3>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 4: ib_round<4>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 5: ib_round<5 <= MAXC ? 5 : 1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 6: ib_round<6 <= MAXC ? 6 : 1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 7: ib_round<7 <= MAXC ? 7 : 1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            default: ib_round<MAXC>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+        }
+    }
+    if (stager) asum_p[st][sg] = asum;
     __syncthreads();
     // D: lane l holds rows 4g + i for token r
     const int t = r;
@@ -610,16 +659,25 @@ __global__ __launch_bounds__(kWG) void i2s_bt_reduce(const float* __restrict__ p
     if (i >= (int64_t)batch * M) return;
     const int64_t t = i / M, m = i - t * M;
     const float* p = partial + t * M + m;
-    float s = 0.0f;  // integers below 2^24: exact in any order
-    for (int z = 0; z < nslice; ++z) s += p[(int64_t)z * kIbTok * M];
+    const int64_t zs = (int64_t)kIbTok * M;
+    float v[kMaxSlices];  // every load before the first add (at most kMaxSlices slices)
+#pragma unroll
+    for (int z = 0; z < kMaxSlices; ++z) v[z] = z < nslice ? p[z * zs] : 0.0f;
+    float s = v[0];  // integers below 2^24: exact in any order
+#pragma unroll
+    for (int z = 1; z < kMaxSlices; ++z)
+        if (z < nslice) s += v[z];
     y[i] = __fmul_rn(__fmul_rn(s, w_scale), act_scale[t]);
 }
 
+// K slices of the batched I2_S GEMV: about one workgroup per CU (256), at
+// least 4 chunks of 256 columns per slice, at most kIbChunks where 16 slices
+// allow.
 inline int ib_slices(int64_t M, int64_t K) {
     const int64_t groups = (M + kIbRows - 1) / kIbRows, nsc = K / 256;
-    int S = 1;
-    while (S < 16 && groups * S < 256 && 2 * S <= nsc) S *= 2;
-    return S;
+    int64_t S = std::min<int64_t>((256 + groups - 1) / groups, std::max<int64_t>(1, nsc / 4));
+    S = std::max<int64_t>(S, (nsc + kIbChunks - 1) / kIbChunks);
+    return (int)std::max<int64_t>(1, std::min<int64_t>({S, 16, nsc}));
 }
 
 // ---------------------------------------------------------------------------
@@ -874,7 +932,7 @@ hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t
     const dim3 grid(ceil_div(M, kIbRows), (unsigned)S);
     for (int64_t t0 = 0; t0 < batch; t0 += kIbTok) {
         const int b = (int)(batch - t0 < kIbTok ? batch - t0 : kIbTok);
-        i2s_gemv_bt<<<grid, kWG, 0, s>>>(packed, w_scale, act + t0 * K, act_scale + t0, y + t0 * M, partial, (int)M,
+        i2s_gemv_bt<kIbChunks, kIbWaves><<<grid, kIbWaves * 64, 0, s>>>(packed, w_scale, act + t0 * K, act_scale + t0, y + t0 * M, partial, (int)M,
                                          (int)K, b);
         if (S > 1)
             i2s_bt_reduce<<<ceil_div((int64_t)b * M, kWG), kWG, 0, s>>>(partial, w_scale, act_scale + t0, y + t0 * M,
@@ -889,7 +947,7 @@ hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const
                                     float* y, int64_t M, int64_t K, int64_t batch, float* partial, Slices* out,
                                     hipStream_t s) {
     const int S = ib_slices(M, K);
-    i2s_gemv_bt<<<dim3(ceil_div(M, kIbRows), (unsigned)S), kWG, 0, s>>>(packed, w_scale, act, act_scale, y, partial,
+    i2s_gemv_bt<kIbChunks, kIbWaves><<<dim3(ceil_div(M, kIbRows), (unsigned)S), kIbWaves * 64, 0, s>>>(packed, w_scale, act, act_scale, y, partial,
                                                                         (int)M, (int)K, (int)batch);
     *out = S == 1 ? plain_slices(y, M) : Slices{partial, M, kIbTok * M, S, w_scale, act_scale};
     return hipGetLastError();
