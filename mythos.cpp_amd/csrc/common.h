@@ -203,6 +203,10 @@ __device__ __forceinline__ float norm_scale(const NormScale& ns, int t, double* 
     return (float)(1.0 / sqrt(s / (double)ns.dim + (double)ns.eps));
 }
 
+// silu(g) = g / (1 + e^-g), in FP32 with expf and an IEEE division (the
+// SwiGLU of every decoder path uses this one definition).
+__device__ __forceinline__ float silu1(float g) { return (g / (1.0f + expf(-g))); }
+
 // ---- int8 helpers ---------------------------------------------------------
 // sum_{i<4} (int8)a.byte[i] * (int8)b.byte[i] + c   (v_dot4_i32_i8)
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

@@ -38,7 +38,8 @@ struct mth_decoder {
     size_t kv_elem = 4;
     float* taps = nullptr;              // mth_decoder_set_taps
     float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr, *arg_v = nullptr;
-    double* ssp = nullptr;  // per-workgroup sums of squares of the split RMSNorm (ResidOut)
+    double* ssp = nullptr;  // per-workgroup sums of squares of the split RMSNorm (ResidOut): attention norm
+    double* ssp2 = nullptr;  // the same for the FFN norm (batch 1)
     int8_t* aq = nullptr;
     int *hist = nullptr, *step = nullptr, *ids = nullptr, *arg_i = nullptr;
     int64_t hist_stride = 0, layer_kv = 0;
@@ -202,36 +203,50 @@ hipError_t enqueue_step_split_norm(const mth_decoder* d, hipStream_t s) {
         if ((e = (call)) != hipSuccess) return e; \
     } while (0)
     using mth::plain_slices;
-    // x: residual stream, h: x * gamma of the next norm
+    // x: residual stream, h: x * gamma of the next norm.  The attention
+    // norm's partial sums are written to ssp (embedding, down projections),
+    // the FFN norm's to ssp2 (O projections), so the down projection with the
+    // SwiGLU fused in reads one buffer and writes the other.
     mth::ResidOut ro{d->x, d->layers[0].attn_norm, d->h, d->ssp};
-    mth::NormScale ns{d->ssp, 1, (float)H, c.eps};
+    mth::NormScale ns_attn{d->ssp, 1, (float)H, c.eps}, ns_ffn{d->ssp2, 1, (float)H, c.eps};
     TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, 1, (int)H, (int)c.vocab, s, ro));
     for (int64_t l = 0; l < c.layers; l++) {
         const mth_decoder_layer& L = d->layers[(size_t)l];
+        const bool last = l + 1 == c.layers;
         char* kc = d->kc + l * d->layer_kv * d->kv_elem;
         char* vc = d->vc + l * d->layer_kv * d->kv_elem;
         TRY(qkv(d, L, d->h, d->q, d->k, d->v, 1, s));
         TRY(mth::launch_rope_attention_slices(plain_slices(d->q, QD), plain_slices(d->k, KD), plain_slices(d->v, KD),
-                                              ns, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att, d->step,
-                                              1, (int)c.heads, (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
+                                              ns_attn, d->rope_cos, d->rope_sin, kc, vc, c.kv_dtype == 1, d->att,
+                                              d->step, 1, (int)c.heads, (int)c.kv_heads, (int)c.head_dim,
+                                              (int)c.max_seq, s));
         ro.gamma = L.ffn_norm;
-        TRY(mth::launch_oil8_gemv_resid(mth::Oil8Seg{L.wo, L.cbo, nullptr, H}, d->att, QD, ro, &ns.nparts, s));
+        ro.ssp = d->ssp2;
+        TRY(mth::launch_oil8_gemv_resid(mth::Oil8Seg{L.wo, L.cbo, nullptr, H}, d->att, QD, ro, &ns_ffn.nparts, s));
         if (gate_up_fused(d, L)) {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
-            TRY(mth::launch_silu_mul_quant_slices(plain_slices(d->gu, 2 * F), plain_slices(d->gu + F, 2 * F), ns,
-                                                  d->aq, d->a_inv, nullptr, 1, F, s));
         } else {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + F, F, H, s));
-            TRY(mth::launch_silu_mul_quant_slices(plain_slices(d->gu, F), plain_slices(d->gu + F, F), ns, d->aq,
-                                                  d->a_inv, nullptr, 1, F, s));
         }
-        if (l + 1 < c.layers) {
-            ro.gamma = d->layers[(size_t)l + 1].attn_norm;
-            TRY(mth::launch_i2s_gemv_resid(L.wdown, L.down_scale, d->aq, d->a_inv, H, F, ro, &ns.nparts, s));
-        } else {
+        ro.ssp = d->ssp;
+        if (!last) ro.gamma = d->layers[(size_t)l + 1].attn_norm;
+        if (mth::i2s_swiglu_supported(L.wdown, H, F)) {
+            // SwiGLU + int8 quantisation inside the down projection
+            if (!last)
+                TRY(mth::launch_i2s_swiglu(d->gu, d->gu + F, ns_ffn, L.wdown, L.down_scale, nullptr, H, F, ro,
+                                           &ns_attn.nparts, s));
+            else
+                TRY(mth::launch_i2s_swiglu(d->gu, d->gu + F, ns_ffn, L.wdown, L.down_scale, d->t, H, F,
+                                           mth::ResidOut{}, nullptr, s));
+            continue;
+        }
+        TRY(mth::launch_silu_mul_quant_slices(plain_slices(d->gu, F), plain_slices(d->gu + F, F), ns_ffn, d->aq,
+                                              d->a_inv, nullptr, 1, F, s));
+        if (!last)
+            TRY(mth::launch_i2s_gemv_resid(L.wdown, L.down_scale, d->aq, d->a_inv, H, F, ro, &ns_attn.nparts, s));
+        else
             TRY(mth::launch_i2s_gemv(L.wdown, L.down_scale, nullptr, d->aq, d->a_inv, d->t, H, F, 1, s));
-        }
     }
     TRY(mth::launch_rms_norm(d->x, d->t, d->g.final_norm, d->h, 1, H, c.eps, s));
     TRY(oil8(d, d->g.lm_idx, d->g.lm_cb, d->h, d->logits, c.vocab, H, s));
@@ -434,7 +449,7 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->pf_k, (size_t)(PR * KD) * 4},  {(void**)&d->pf_v, (size_t)(PR * KD) * 4},
         {(void**)&d->pf_att, (size_t)(PR * QD) * 4}, {(void**)&d->pf_gu, (size_t)(PR * 2 * F) * 4},
         {(void**)&d->pf_aq, (size_t)(PR * F)},      {(void**)&d->pf_inv, (size_t)PR * 4},
-        {(void**)&d->ssp, (size_t)(H / 4 + 2) * 8},
+        {(void**)&d->ssp, (size_t)(H / 4 + 2) * 8},  {(void**)&d->ssp2, (size_t)(H / 4 + 2) * 8},
     };
     size_t total = 0;
     for (const Slot& sl : slots) total += round_up(sl.bytes);

@@ -131,7 +131,6 @@ __global__ __launch_bounds__(kT) void rms_norm_any_k(float* x, Slices t, const f
 }
 
 // ---- SwiGLU and elementwise ------------------------------------------------
-__device__ __forceinline__ float silu1(float g) { return (g / (1.0f + expf(-g))); }
 
 // y[r][i] = silu(g) * u with g = gu[r][i], u = gu[r][n + i] (the gate and up
 // outputs of one fused GEMV, rows of 2n), or g/u from separate arrays.

@@ -474,6 +474,255 @@ void h3_dispatch(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int b,
     else run_h3<4, 1, 1>(seg, nseg, x, K, b, partial, reduce, s);
 }
 
+// ===================================================================
+// OIL4, batch 2..16, per-128-column codebooks: persistent workgroups
+// ===================================================================
+// The arithmetic of oil4_gemv_bt (same A and B fragments, same hi/lo MFMA
+// pair, same per-(token, phase) scale), organised so that the activations
+// are converted once per workgroup and the weight stream overlaps the
+// dequantisation:
+//   * about one 8-wave workgroup per CU.  Workgroup b owns K slice
+//     z = b % S (NPH phases of 256 columns) and the 16-row tiles [t0, t1)
+//     of share p = b / S; it converts the slice's activations for 16 tokens
+//     into hi / lo B fragments in LDS once and uses them for all its tiles;
+//   * its waves walk the (tile, phase) units of the range in tile-major
+//     order, wave w the contiguous run [w NU / A, (w + 1) NU / A) of the
+//     NU = (t1 - t0) NPH units (A = active waves), so runs differ by at
+//     most one unit;
+//   * each wave keeps kBpDepth units of weight loads in flight in a
+//     register ring, refilled as a unit is consumed;
+//   * a tile's sum is the sum of its runs' parts: the part of the run that
+//     covers its phase 0 goes to LDS slot 0, the other (if any) to slot 1,
+//     and the tile's result is slot 0 + slot 1 (fixed order:
+//     deterministic).  Runs are at least NPH units long (A = min(8, tiles)),
+//     so no tile has more than two parts.
+// Slices write partial sums for oil4_bt_reduce (or the consumer) as before.
+constexpr int kBpMaxTiles = 24;  // 16-row tiles per workgroup (LDS sums)
+constexpr int kBpDepth = 4;      // units in flight per wave
+constexpr int kBpCUs = 256;      // MI355X
+
+template <int NPH, int WV>
+struct BpLds {
+    static constexpr int frag = Oil4BtLds<NPH, false>::frag;  // B of one phase, hi or lo (8 KB)
+    static constexpr int bphase = 2 * frag;
+    static constexpr int stage = NPH * bphase;                // codebook stage: 2 KB per wave
+    static constexpr int sums = stage + WV * 2048;            // [tile][slot][token][row] f32
+    static constexpr int dummy = sums + kBpMaxTiles * 2 * 1024;  // 1 KB, shared: stores between tiles
+    static constexpr int shifts = dummy + 1024;
+    static constexpr int bytes = shifts + NPH * kBtTok * 4;
+};
+
+// Weight loads of one unit: 16 rows x 256 columns starting at column kcol
+// (two 8-row x 128-byte nibble reads), and the codebooks of the unit's phase
+// pair (two 8-row x 128-byte reads), in the layout of Oil4TileLoads.
+struct BpSlot {
+    uint4 c0, c1, wx, wy;
+};
+
+// Per-lane byte offsets of those reads from the tile's first row; rows past
+// M read row M - 1 (lim = M - 1 - row0 >= 15 for a full tile).
+struct BpOff {
+    uint32_t c0, c1, wx, wy;
+};
+
+__device__ __forceinline__ BpOff bp_off(int lim, int K, int lane) {
+    const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
+    const uint32_t hk = (uint32_t)K >> 1, cbr = (uint32_t)K >> 2;  // row bytes: nibbles, codebooks
+    BpOff o;
+    o.c0 = (uint32_t)min(lane >> 3, lim) * cbr + 16 * (lane & 7);
+    o.c1 = (uint32_t)min(8 + (lane >> 3), lim) * cbr + 16 * (lane & 7);
+    o.wx = (uint32_t)min(jj8, lim) * hk + 16 * (2 * q + hi8);
+    o.wy = (uint32_t)min(8 + jj8, lim) * hk + 16 * (2 * q + hi8);
+    return o;
+}
+
+// The tile base is uniform (scalar registers), the lane offsets 32-bit.
+__device__ __forceinline__ void bp_issue(BpSlot& s, const uint8_t* nib, const uint16_t* cbs, int row0, int K,
+                                         int kcol, const BpOff& o) {
+    const uint8_t* nb = nib + (int64_t)row0 * (K >> 1) + (kcol >> 1);
+    const uint8_t* cb = (const uint8_t*)cbs + (int64_t)row0 * (K >> 2) + (int64_t)((kcol >> 7) & ~3) * 32;
+    s.c0 = ld16(cb + o.c0);
+    s.c1 = ld16(cb + o.c1);
+    s.wx = ld_stream(nb + o.wx);
+    s.wy = ld_stream(nb + o.wy);
+}
+
+template <int NPH, int WV>
+__global__ __launch_bounds__(WV * 64) void oil4_gemv_bp(const uint8_t* nib, const uint16_t* cbs,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              float* __restrict__ partial, int M, int K, int batch,
+                                                              int tiles, int per_slice) {
+    using L = BpLds<NPH, WV>;
+    static_assert(WV >= 8, "the first 8 waves convert the activations");
+    __shared__ __align__(16) uint8_t lds[L::bytes];
+    int* shifts = (int*)(lds + L::shifts);
+    float* sums = (float*)(lds + L::sums);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, q = lane >> 4;
+    const int S = K / (256 * NPH);
+    const int z = blockIdx.x % S, p = blockIdx.x / S;
+    const int t0 = (int)((int64_t)p * tiles / per_slice), t1 = (int)((int64_t)(p + 1) * tiles / per_slice);
+    const int nt = t1 - t0;
+    if (nt <= 0) return;  // uniform, before any barrier
+    const int k0 = z * 256 * NPH;
+
+    // ---- activations of the slice first (loads return in issue order):
+    // thread of the first 8 waves -> token tt, 16-column group u, phases
+    // hp, hp + 2, ...
+    constexpr int XPH = NPH / 2;
+    const bool conv = wave < 8;  // uniform
+    const int tt = (tid >> 4) & 15, u = tid & 15, hp = (tid >> 8) & 1;
+    const bool tok = tt < batch;
+    const float* xr = x + (int64_t)(tok ? tt : 0) * K + k0 + 16 * u;
+    float4 xq[XPH][4];
+    if (conv) {
+#pragma unroll
+        for (int e = 0; e < XPH; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xq[e][i] = ldf4(xr + 256 * (hp + 2 * e) + 4 * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- this wave's run; the first kBpDepth units' loads
+    const int NU = nt * NPH, act = min(WV, nt);
+    const int u0 = wave < act ? (int)((int64_t)wave * NU / act) : NU;
+    const int u1 = wave < act ? (int)((int64_t)(wave + 1) * NU / act) : NU;
+    const int ulast = u0 < u1 ? u1 - 1 : 0;  // loads past the run repeat its last unit (cache hits)
+    const BpOff ofull = bp_off(15, K, lane), olast = bp_off(M - 1 - (tiles - 1) * 16, K, lane);
+    auto issue = [&](BpSlot& sl, int uu) {
+        const int t = t0 + uu / NPH;
+        const bool last = t == tiles - 1;  // uniform
+        BpOff o;
+        o.c0 = last ? olast.c0 : ofull.c0; o.c1 = last ? olast.c1 : ofull.c1;
+        o.wx = last ? olast.wx : ofull.wx; o.wy = last ? olast.wy : ofull.wy;
+        bp_issue(sl, nib, cbs, t * 16, K, k0 + 256 * (uu % NPH), o);
+    };
+    BpSlot ring[kBpDepth];
+#pragma unroll
+    for (int s = 0; s < kBpDepth; ++s) issue(ring[s], min(u0 + s, ulast));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- B fragments of the slice (the conversion of oil4_gemv_bt)
+#pragma unroll
+    for (int e = 0; e < (conv ? XPH : 0); ++e) {
+        const int ph = hp + 2 * e;
+        uint8_t* bbuf = lds + ph * L::bphase;
+        float xv[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[4 * i] = tok ? xq[e][i].x : 0.0f; xv[4 * i + 1] = tok ? xq[e][i].y : 0.0f;
+            xv[4 * i + 2] = tok ? xq[e][i].z : 0.0f; xv[4 * i + 3] = tok ? xq[e][i].w : 0.0f;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(xv[i]));
+        const int sh = fp16_scale_shift(row16_max(mx));  // the 16 threads of one (token, phase): one DPP row
+        if (u == 0) shifts[ph * kBtTok + tt] = sh;
+        const int qq = u >> 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int m = 2 * (u & 3) + h;
+            half8 vh, vl;
+#pragma unroll
+            for (int e2 = 0; e2 < 8; ++e2) {
+                const float xs = ldexpf(xv[8 * h + oil4_elem_col(e2)], sh);
+                const _Float16 hh = (_Float16)xs;
+                vh[e2] = hh;
+                vl[e2] = (_Float16)(xs - (float)hh);
+            }
+            *(half8*)(bbuf + bt_slot(m, qq, tt)) = vh;
+            *(half8*)(bbuf + L::frag + bt_slot(m, qq, tt)) = vl;
+        }
+    }
+    for (int i = tid; i < nt * 256; i += WV * 64) sums[(i >> 8) * 512 + 256 + (i & 255)] = 0.0f;  // slot 1
+    __syncthreads();
+
+    // ---- the run.  One unit: codebooks of the phase pair -> wave stage ->
+    // the block of this lane's columns; 8 x (lookup8, hi and lo MFMA); the
+    // phase's sum scaled back; at the end of a tile's part, the part to its
+    // LDS slot (between tiles the store goes to the wave's dummy row, so the
+    // loop body has no branch).
+    uint8_t* stage = lds + L::stage + wave * 2048;
+    constexpr int dummy_off = L::dummy / 4;  // in floats
+    floatx4 ysum = {0.0f, 0.0f, 0.0f, 0.0f};
+    int seg0 = u0 % NPH;  // phase at which the current tile's part began
+    auto unit = [&](const BpSlot& sl, int uu) {
+        const int ph = uu % NPH;
+        *(uint4*)(stage + oil4_stage_off(lane >> 3, lane & 7)) = sl.c0;
+        *(uint4*)(stage + oil4_stage_off(8 + (lane >> 3), lane & 7)) = sl.c1;
+        const int bi = 2 * (ph & 1) + (q >> 1);
+        const uint4 ca = *(const uint4*)(stage + oil4_stage_off(j, 2 * bi));
+        const uint4 cb = *(const uint4*)(stage + oil4_stage_off(j, 2 * bi + 1));
+        const CbPlanes pl = cb_planes(ca, cb);
+        uint4 xa, yb;
+        h3_exchange(sl.wx, sl.wy, lane, xa, yb);
+        const uint8_t* bbuf = lds + ph * L::bphase;
+        floatx4 acc_h = {0.0f, 0.0f, 0.0f, 0.0f}, acc_l = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const half8 a = lookup8(m < 4 ? u4get(xa, m) : u4get(yb, m - 4), pl);
+            const half8 bh = *(const half8*)(bbuf + bt_slot(m, q, j));
+            const half8 bl = *(const half8*)(bbuf + L::frag + bt_slot(m, q, j));
+            acc_h = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_h, 0, 0, 0);
+            acc_l = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_l, 0, 0, 0);
+        }
+        const int shn = shifts[ph * kBtTok + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ysum[i] += ldexpf(oil4_hi_lo(acc_h[i], acc_l[i]), -shn);
+        // end of this tile's part (uniform); selects as arithmetic on masks so
+        // that the compiler keeps the loop body one basic block
+        const int bnd = (int)(ph == NPH - 1) | (int)(uu == u1 - 1);
+        const int real = (int)(L::sums / 4) + (uu / NPH) * 512 + ((seg0 != 0) << 8);
+        const int off = dummy_off + bnd * (real - dummy_off);
+        *(floatx4*)((float*)lds + off + j * 16 + 4 * q) = ysum;
+        const uint32_t keep = (uint32_t)bnd - 1u;  // 0 at a boundary, all ones otherwise
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ysum[i] = __uint_as_float(__float_as_uint(ysum[i]) & keep);
+        seg0 &= (int)keep;
+    };
+    const int nfull = (u1 - u0) / kBpDepth;
+    int ub = u0;
+    for (int it = 0; it < nfull; ++it, ub += kBpDepth) {
+#pragma unroll
+        for (int s = 0; s < kBpDepth; ++s) {
+            unit(ring[s], ub + s);
+            issue(ring[s], min(ub + s + kBpDepth, ulast));
+        }
+    }
+    // the last (u1 - u0) % kBpDepth units sit in slots 0, 1, ...
+#pragma unroll
+    for (int s = 0; s < kBpDepth - 1; ++s)
+        if (ub + s < u1) unit(ring[s], ub + s);
+    __syncthreads();
+
+    // ---- tile sums: rows (t0 + tile) 16 + r, token tk
+    for (int i = tid; i < nt * 256; i += WV * 64) {
+        const int tl = i >> 8, tk = (i >> 4) & 15, r = i & 15;
+        const int row = (t0 + tl) * 16 + r;
+        if (tk < batch && row < M) {
+            const float v = sums[tl * 512 + tk * 16 + r] + sums[tl * 512 + 256 + tk * 16 + r];
+            if (S == 1) y[(int64_t)tk * M + row] = v;
+            else partial[((int64_t)z * kBtTok + tk) * M + row] = v;
+        }
+    }
+}
+
+template <int NPH, int WV = 8>
+void run_bp(const uint8_t* nib, const uint16_t* cbs, const float* x, float* y, float* partial, int64_t M, int64_t K,
+            int batch, bool reduce, hipStream_t s) {
+    const int S = (int)(K / (256 * NPH));
+    const int64_t tiles = (M + 15) / 16;
+    int64_t per = std::max<int64_t>((kBpCUs + S - 1) / S, (tiles + kBpMaxTiles - 1) / kBpMaxTiles);
+    per = std::min<int64_t>(per, tiles);
+    oil4_gemv_bp<NPH, WV><<<(unsigned)(S * per), WV * 64, 0, s>>>(nib, cbs, x, y, partial, (int)M, (int)K, batch,
+                                                                   (int)tiles, (int)per);
+    if (S > 1 && reduce)
+        oil4_bt_reduce<<<ceil_div_i((int64_t)batch * M, 256), 256, 0, s>>>(partial, y, (int)M, batch, S);
+}
+
 // phases of 256 columns per K slice: 4 (K a multiple of 1024, K >= 2048) or 2
 inline int bt_nph(int64_t K) { return (K >= 2048 && K % 1024 == 0) ? 4 : 2; }
 
@@ -491,10 +740,10 @@ void bt_dispatch(const uint8_t* nib, const uint16_t* cbs, bool sh, const float* 
                  int64_t M, int64_t K, int b, bool reduce, hipStream_t s) {
     if (bt_nph(K) == 4) {
         if (sh) run_bt<4, true>(nib, cbs, x, y, partial, M, K, b, reduce, s);
-        else run_bt<4, false>(nib, cbs, x, y, partial, M, K, b, reduce, s);
+        else run_bp<4>(nib, cbs, x, y, partial, M, K, b, reduce, s);
     } else {
         if (sh) run_bt<2, true>(nib, cbs, x, y, partial, M, K, b, reduce, s);
-        else run_bt<2, false>(nib, cbs, x, y, partial, M, K, b, reduce, s);
+        else run_bp<2>(nib, cbs, x, y, partial, M, K, b, reduce, s);
     }
 }
 

@@ -98,6 +98,12 @@ hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const
 bool i2s_resid_supported(const uint8_t* packed, const int8_t* act, int64_t M, int64_t K);
 hipError_t launch_i2s_gemv_resid(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
                                  int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s);
+// Batch 1: the SwiGLU and the per-token int8 quantisation of g, u (with the
+// RMSNorm's 1 / rms from ns) fused into the I2_S down projection; ro
+// (ResidOut) or y; ro.ssp must differ from ns.ssp.  *nparts: partials.
+bool i2s_swiglu_supported(const uint8_t* packed, int64_t M, int64_t K);
+hipError_t launch_i2s_swiglu(const float* g, const float* u, const NormScale& ns, const uint8_t* packed, float w_scale,
+                             float* y, int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s);
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 // ws: null (one wave per output) or i2s_gemm_workspace_bytes(M, N, K) bytes of

@@ -231,6 +231,150 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
 }
 
 // ---------------------------------------------------------------------------
+// SwiGLU + per-token int8 quantisation fused into the I2_S down projection
+// (decode batch 1).
+// ---------------------------------------------------------------------------
+//   a = silu(g * ni) * (u * ni)              (ni: the RMSNorm's 1 / rms, NormScale)
+//   q = quantize_per_token(a)                (src/int8_quant.cpp:8-31)
+//   y[m] = ((float)sum_k t(m, k) q[k] * w_scale) * (max|a| / 127)
+// Every workgroup (16 waves, one row per wave: 16 rows) first computes the
+// whole token's a exactly as silu_mul_quant_k does -- 1024 threads with the
+// same columns per thread, the same NormScale summation order, the same max
+// and rounding -- and keeps q in LDS; then each wave runs the i2s_gemv_fast
+// dot product of its row (64 lanes, NSEG 16-byte segments per lane).  The
+// SwiGLU is recomputed by every workgroup (one per CU at hidden 4096), which
+// costs less than the launch and the int8 round trip it replaces.
+// Loads in order of use: the norm's partial sums, g and u, then the row's
+// weights (the CU returns loads in issue order).
+// res (ResidOut): the residual epilogue of i2s_gemv_fast; its partial sums go
+// to res.ssp, which must not be ns.ssp (other workgroups may still read it).
+constexpr int kSwT = 1024, kSwQ = 12;  // as silu_mul_quant_k (kSQT, kSQ)
+
+template <int NSEG>
+__global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g, const float* __restrict__ u,
+                                                     NormScale ns, const uint8_t* packed, float w_scale,
+                                                     float* __restrict__ y, int M, int K, ResidOut res) {
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    int8_t* q = (int8_t*)lds_raw;  // K bytes
+    __shared__ double nred[kSwT / 64];
+    __shared__ float red[kSwT / 64];
+    __shared__ double rsq[kSwT / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = blockIdx.x * (kSwT / 64) + wave;
+    const int bpr = K >> 2, nseg = bpr >> 4;
+
+    double nsum = 0.0;
+    if (ns.ssp)
+        for (int i = tid; i < ns.nparts; i += kSwT) nsum += ns.ssp[i];
+    float gv[kSwQ], uv[kSwQ];
+#pragma unroll
+    for (int j = 0; j < kSwQ; ++j) {
+        const int i = tid + j * kSwT;
+        gv[j] = i < K ? g[i] : 0.0f;
+        uv[j] = i < K ? u[i] : 0.0f;
+    }
+    uint4 w[NSEG];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s)
+        w[s] = ld_stream(packed + (int64_t)min(row, M - 1) * bpr + (int64_t)min(lane + 64 * s, nseg - 1) * 16);
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (ns.ssp) {  // norm_scale<16>: per-thread sums, wave sums, waves in order
+        double sum = wave_sum_dbl(nsum);
+        if (lane == 0) nred[wave] = sum;
+        __syncthreads();
+        sum = 0.0;
+#pragma unroll
+        for (int w2 = 0; w2 < kSwT / 64; ++w2) sum += nred[w2];
+        const float ni = (float)(1.0 / sqrt(sum / (double)ns.dim + (double)ns.eps));
+#pragma unroll
+        for (int j = 0; j < kSwQ; ++j) {
+            gv[j] *= ni;
+            uv[j] *= ni;
+        }
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kSwQ; ++j) {
+        gv[j] = silu1(gv[j]) * uv[j];
+        m = fmaxf(m, fabsf(gv[j]));
+    }
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w2 = 1; w2 < kSwT / 64; ++w2) m = fmaxf(m, red[w2]);
+    if (m < 1e-10f) m = 1e-10f;
+    const float sc = __fdiv_rn(127.0f, m), inv = __fdiv_rn(m, 127.0f);
+#pragma unroll
+    for (int j = 0; j < kSwQ; ++j) {
+        const int i = tid + j * kSwT;
+        if (i < K) q[i] = (int8_t)quant_i8(gv[j], sc);
+    }
+    __syncthreads();
+
+    // lane's activations, transposed: A[s][d][j] byte b = a[seg*64 + 16d + 4b + j]
+    uint32_t A[NSEG][4][4];
+    int asum = 0;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        const int seg = lane + 64 * s;
+        if (seg < nseg) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint4 n = *(const uint4*)(q + seg * 64 + 16 * d);
+                const uint32_t N[4] = {n.x, n.y, n.z, n.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    A[s][d][j] = ((N[0] >> (8 * j)) & 0xffu) | (((N[1] >> (8 * j)) & 0xffu) << 8) |
+                                 (((N[2] >> (8 * j)) & 0xffu) << 16) | (((N[3] >> (8 * j)) & 0xffu) << 24);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asum = dot4(N[j], 0x01010101u, asum);
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) A[s][d][j] = 0;
+        }
+    }
+    int acc = 0;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        const bool sv = lane + 64 * s < nseg;
+        const uint32_t pad = 0x55555555u;  // t = 0 codes past the row (they meet A = 0)
+        acc = tdot16(sv ? w[s].x : pad, A[s][0], acc);
+        acc = tdot16(sv ? w[s].y : pad, A[s][1], acc);
+        acc = tdot16(sv ? w[s].z : pad, A[s][2], acc);
+        acc = tdot16(sv ? w[s].w : pad, A[s][3], acc);
+    }
+    acc = group_sum_i<64>(acc - asum);
+    const float v = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
+    const bool rv = row < M;
+    if (!res.x) {
+        if (lane == 0 && rv) y[row] = v;
+        return;
+    }
+    double sq = 0.0;
+    if (lane == 0 && rv) {
+        const float r = v + res.x[row];
+        res.x[row] = r;
+        res.xg[row] = r * res.gamma[row];
+        sq = (double)r * r;
+    }
+    if (lane == 0) rsq[wave] = sq;
+    __syncthreads();
+    if (tid == 0) {
+        double t = 0.0;
+#pragma unroll
+        for (int w2 = 0; w2 < kSwT / 64; ++w2) t += rsq[w2];
+        res.ssp[blockIdx.x] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // I2_S GEMV, batch 1 (i2s_gemv_rows): R rows per wave, 4R per workgroup.
 // ---------------------------------------------------------------------------
 // A 4 MB GEMV is latency-bound, so everything is requested up front: the
@@ -887,6 +1031,25 @@ hipError_t launch_i2s_gemv_resid(const uint8_t* packed, float w_scale, const int
     if (nseg <= 128) return run_i2s_fast_resid<32, 4>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
     if (nseg <= 192) return run_i2s_fast_resid<64, 3>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
     return run_i2s_fast_resid<64, 4>(packed, w_scale, act, act_scale, M, K, ro, nparts, s);
+}
+
+bool i2s_swiglu_supported(const uint8_t* packed, int64_t M, int64_t K) {
+    return K >= 64 && K % 64 == 0 && K <= kSwT * kSwQ && M < (1ll << 31) && aligned16(packed);
+}
+
+hipError_t launch_i2s_swiglu(const float* g, const float* u, const NormScale& ns, const uint8_t* packed, float w_scale,
+                             float* y, int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s) {
+    const int64_t nseg = K / 64;
+    const int grid = ceil_div(M, kSwT / 64);
+    const size_t lds = (size_t)K;
+    if (nseg <= 64)
+        i2s_swiglu_k<1><<<grid, kSwT, lds, s>>>(g, u, ns, packed, w_scale, y, (int)M, (int)K, ro);
+    else if (nseg <= 128)
+        i2s_swiglu_k<2><<<grid, kSwT, lds, s>>>(g, u, ns, packed, w_scale, y, (int)M, (int)K, ro);
+    else
+        i2s_swiglu_k<3><<<grid, kSwT, lds, s>>>(g, u, ns, packed, w_scale, y, (int)M, (int)K, ro);
+    if (nparts) *nparts = grid;
+    return hipGetLastError();
 }
 
 hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x, const int8_t* act,
