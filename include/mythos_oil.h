@@ -222,6 +222,35 @@ int mth_mul(const float* a, const float* b, float* c, int64_t n, mth_stream_t st
 /* oil::math::softmax over the last axis of [rows][dim] (src/math.cpp:207-249). */
 int mth_softmax(const float* x, float* y, int64_t rows, int64_t dim, mth_stream_t stream);
 
+/* ---- the rest of the ComputeBackend vtable's dense operators ------------
+ * (include/oil/backend.h:55-71; the reference's CPU backend calls math::*,
+ * src/backend.cpp:40-58).  Used by the HIP ComputeBackend of
+ * libmythos_host.so; x and y may be the same array in the elementwise ones. */
+
+/* oil::math::softmax along any axis (src/math.cpp:207-249): x, y viewed as
+ * [outer][dim][inner], softmax over dim for every (outer, inner). */
+int mth_softmax_axis(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, mth_stream_t stream);
+
+/* y = alpha * x + beta * y, each product and the sum rounded to FP32 (no
+ * fused multiply-add), y always read: the epilogue of math::gemm / gemv
+ * (src/math.cpp:70, :94), so NaN or Inf in y reaches the result as there. */
+int mth_axpby(float alpha, const float* x, float beta, float* y, int64_t n, mth_stream_t stream);
+
+/* oil::math::gemv (src/math.cpp:52-72): y[i] = alpha * sum_j A[i][j] x[j] +
+ * beta * y[i], A [M][N] row-major. */
+int mth_gemv_f32(float alpha, const float* A, const float* x, float beta, float* y, int64_t M, int64_t N,
+                 mth_stream_t stream);
+
+/* oil::math::relu, gelu (erf form), scale (src/math.cpp:99-117, :278-284). */
+int mth_relu(const float* x, float* y, int64_t n, mth_stream_t stream);
+int mth_gelu(const float* x, float* y, int64_t n, mth_stream_t stream);
+int mth_scale(float s, const float* x, float* y, int64_t n, mth_stream_t stream);
+
+/* oil::math::layer_norm over rows of dim (src/math.cpp:148-180): double mean
+ * and variance, y = (float)((x - mean) / sqrt(var + eps)) * gamma + beta. */
+int mth_layer_norm(const float* x, const float* gamma, const float* beta, float* y, int64_t rows, int64_t dim,
+                   float eps, mth_stream_t stream);
+
 /* RotaryEmbedding tables (src/transformer.cpp:102-117), computed on the host
  * in float: cos/sin [max_seq][head_dim/2] (host buffers). */
 int mth_rope_tables(int64_t head_dim, int64_t max_seq, float theta, float* cos_t, float* sin_t);

@@ -423,6 +423,57 @@ int mth_softmax(const float* x, float* y, int64_t rows, int64_t dim, mth_stream_
     return check_launch(mth::launch_softmax(x, y, rows, dim, S(stream)), "mth_softmax");
 }
 
+int mth_softmax_axis(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_softmax_axis: null pointer");
+    REQUIRE(outer > 0 && dim > 0 && inner > 0 && outer < kMaxDim && dim < kMaxDim && inner < kMaxDim &&
+                outer * inner < kMaxDim && dim * inner < kMaxDim && outer * dim * inner < kMaxDim,
+            "mth_softmax_axis: bad sizes outer=%lld dim=%lld inner=%lld", (long long)outer, (long long)dim,
+            (long long)inner);
+    REQUIRE(inner > 1 || outer < (1ll << 31), "mth_softmax_axis: outer=%lld too large", (long long)outer);
+    return check_launch(mth::launch_softmax_axis(x, y, outer, dim, inner, S(stream)), "mth_softmax_axis");
+}
+
+int mth_axpby(float alpha, const float* x, float beta, float* y, int64_t n, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_axpby: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_axpby: bad size n=%lld", (long long)n);
+    return check_launch(mth::launch_axpby(alpha, x, beta, y, n, S(stream)), "mth_axpby");
+}
+
+int mth_gemv_f32(float alpha, const float* A, const float* x, float beta, float* y, int64_t M, int64_t N,
+                 mth_stream_t stream) {
+    REQUIRE(A && x && y, "mth_gemv_f32: null pointer");
+    REQUIRE(M > 0 && N > 0 && M < (1ll << 31) && N < kMaxDim && M * N < kMaxDim,
+            "mth_gemv_f32: bad sizes M=%lld N=%lld", (long long)M, (long long)N);
+    return check_launch(mth::launch_gemv_f32(alpha, A, x, beta, y, M, N, S(stream)), "mth_gemv_f32");
+}
+
+int mth_relu(const float* x, float* y, int64_t n, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_relu: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_relu: bad size n=%lld", (long long)n);
+    return check_launch(mth::launch_relu(x, y, n, S(stream)), "mth_relu");
+}
+
+int mth_gelu(const float* x, float* y, int64_t n, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_gelu: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_gelu: bad size n=%lld", (long long)n);
+    return check_launch(mth::launch_gelu(x, y, n, S(stream)), "mth_gelu");
+}
+
+int mth_scale(float s, const float* x, float* y, int64_t n, mth_stream_t stream) {
+    REQUIRE(x && y, "mth_scale: null pointer");
+    REQUIRE(n > 0 && n < kMaxDim, "mth_scale: bad size n=%lld", (long long)n);
+    return check_launch(mth::launch_scale(s, x, y, n, S(stream)), "mth_scale");
+}
+
+int mth_layer_norm(const float* x, const float* gamma, const float* beta, float* y, int64_t rows, int64_t dim,
+                   float eps, mth_stream_t stream) {
+    REQUIRE(x && gamma && beta && y, "mth_layer_norm: null pointer");
+    REQUIRE(rows > 0 && rows < (1ll << 31) && dim > 0 && dim < kMaxDim && rows * dim < kMaxDim,
+            "mth_layer_norm: bad sizes rows=%lld dim=%lld", (long long)rows, (long long)dim);
+    REQUIRE(eps >= 0.0f, "mth_layer_norm: eps < 0");
+    return check_launch(mth::launch_layer_norm(x, gamma, beta, y, rows, dim, eps, S(stream)), "mth_layer_norm");
+}
+
 int mth_rope_tables(int64_t head_dim, int64_t max_seq, float theta, float* cos_t, float* sin_t) {
     REQUIRE(cos_t && sin_t, "mth_rope_tables: null pointer");
     REQUIRE(head_dim > 0 && head_dim % 2 == 0 && max_seq > 0 && head_dim * max_seq < kMaxDim,

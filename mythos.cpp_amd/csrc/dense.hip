@@ -178,6 +178,98 @@ __global__ __launch_bounds__(kT) void softmax_k(const float* __restrict__ x, flo
     for (int64_t i = threadIdx.x; i < dim; i += kT) yr[i] = (float)((double)yr[i] * inv);
 }
 
+// ---- the remaining dense operators of the ComputeBackend vtable ------------
+// (include/oil/backend.h:55-71, dispatched to math:: by the reference's CPU
+// backend, src/backend.cpp:40-58)
+//   math::gemv            src/math.cpp:52-72    s = sum_j A[i][j] x[j]; y = alpha*s + beta*y
+//   gemm's epilogue       src/math.cpp:74-97    C = alpha*(A B) + beta*C, C always read
+//   math::relu            src/math.cpp:99-105
+//   math::gelu            src/math.cpp:107-117  0.5f * v * (1 + erf(v * 1/sqrt 2))
+//   math::layer_norm      src/math.cpp:148-180  double mean, double variance of the
+//                                               deviations, (float)(d * inv) * gamma + beta
+//   math::softmax, axis   src/math.cpp:207-249  as softmax_k, along a strided axis
+//   math::scale           src/math.cpp:278-284
+__global__ __launch_bounds__(kT) void axpby_k(float alpha, const float* __restrict__ x, float beta,
+                                              float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kT + threadIdx.x;
+    if (i < n) y[i] = alpha * x[i] + beta * y[i];
+}
+
+// One wave per row; the row's products summed in FP32 per lane, then across
+// the wave.
+__global__ __launch_bounds__(kT) void gemv_f32_k(float alpha, const float* __restrict__ A,
+                                                 const float* __restrict__ x, float beta, float* __restrict__ y,
+                                                 int64_t M, int64_t N) {
+    const int64_t row = (int64_t)blockIdx.x * (kT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const float* a = A + row * N;
+    float s = 0.0f;
+    for (int64_t j = lane; j < N; j += 64) s += a[j] * x[j];
+    s = group_sum<64>(s);
+    if (lane == 0) y[row] = alpha * s + beta * y[row];
+}
+
+__global__ __launch_bounds__(kT) void relu_k(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kT + threadIdx.x;
+    if (i < n) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+__global__ __launch_bounds__(kT) void gelu_k(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kT + threadIdx.x;
+    if (i < n) {
+        const float v = x[i];
+        y[i] = 0.5f * v * (1.0f + erff(v * 0.7071067811865475f));
+    }
+}
+
+__global__ __launch_bounds__(kT) void scale_k(float s, const float* __restrict__ x, float* __restrict__ y,
+                                              int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kT + threadIdx.x;
+    if (i < n) y[i] = s * x[i];
+}
+
+// One workgroup per row.
+__global__ __launch_bounds__(kT) void layer_norm_k(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                   const float* __restrict__ beta, float* __restrict__ y,
+                                                   int64_t dim, float eps) {
+    __shared__ double red[4];
+    const float* xr = x + (int64_t)blockIdx.x * dim;
+    float* yr = y + (int64_t)blockIdx.x * dim;
+    double s = 0.0;
+    for (int64_t j = threadIdx.x; j < dim; j += kT) s += xr[j];
+    const double mu = block_sum(s, red) / (double)dim;
+    double v = 0.0;
+    for (int64_t j = threadIdx.x; j < dim; j += kT) {
+        const double d = (double)xr[j] - mu;
+        v += d * d;
+    }
+    const double var = block_sum(v, red) / (double)dim;
+    const double inv = 1.0 / sqrt(var + (double)eps);
+    for (int64_t j = threadIdx.x; j < dim; j += kT) yr[j] = (float)(((double)xr[j] - mu) * inv) * gamma[j] + beta[j];
+}
+
+// Softmax along a strided axis: thread = (outer o, inner i), the dim values
+// x[o][d][i] at stride inner.
+__global__ __launch_bounds__(kT) void softmax_strided_k(const float* __restrict__ x, float* __restrict__ y,
+                                                        int64_t outer, int64_t dim, int64_t inner) {
+    const int64_t t = (int64_t)blockIdx.x * kT + threadIdx.x;
+    if (t >= outer * inner) return;
+    const int64_t o = t / inner, i = t - o * inner;
+    const float* src = x + o * dim * inner + i;
+    float* dst = y + o * dim * inner + i;
+    float mx = -INFINITY;
+    for (int64_t d = 0; d < dim; ++d) mx = fmaxf(mx, src[d * inner]);
+    double sum = 0.0;
+    for (int64_t d = 0; d < dim; ++d) {
+        const float e = expf(src[d * inner] - mx);
+        dst[d * inner] = e;
+        sum += (double)e;
+    }
+    const double inv = 1.0 / sum;
+    for (int64_t d = 0; d < dim; ++d) dst[d * inner] = (float)((double)dst[d * inner] * inv);
+}
+
 // ---- rotary embedding + KV-cache append ------------------------------------
 // One workgroup per token b.  q [B][heads*D] rotated in place; k rotated and,
 // with v, written to the caches at position pos = *step (+ pos0):
@@ -724,6 +816,44 @@ hipError_t launch_mul(const float* a, const float* b, float* c, int64_t n, hipSt
 
 hipError_t launch_softmax(const float* x, float* y, int64_t rows, int64_t dim, hipStream_t s) {
     softmax_k<<<(unsigned)rows, kT, 0, s>>>(x, y, dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_axis(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, hipStream_t s) {
+    if (inner == 1) return launch_softmax(x, y, outer, dim, s);
+    softmax_strided_k<<<blocks_for(outer * inner), kT, 0, s>>>(x, y, outer, dim, inner);
+    return hipGetLastError();
+}
+
+hipError_t launch_axpby(float alpha, const float* x, float beta, float* y, int64_t n, hipStream_t s) {
+    axpby_k<<<blocks_for(n), kT, 0, s>>>(alpha, x, beta, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_f32(float alpha, const float* A, const float* x, float beta, float* y, int64_t M, int64_t N,
+                           hipStream_t s) {
+    gemv_f32_k<<<(unsigned)((M + kT / 64 - 1) / (kT / 64)), kT, 0, s>>>(alpha, A, x, beta, y, M, N);
+    return hipGetLastError();
+}
+
+hipError_t launch_relu(const float* x, float* y, int64_t n, hipStream_t s) {
+    relu_k<<<blocks_for(n), kT, 0, s>>>(x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu(const float* x, float* y, int64_t n, hipStream_t s) {
+    gelu_k<<<blocks_for(n), kT, 0, s>>>(x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale(float a, const float* x, float* y, int64_t n, hipStream_t s) {
+    scale_k<<<blocks_for(n), kT, 0, s>>>(a, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer_norm(const float* x, const float* gamma, const float* beta, float* y, int64_t rows,
+                             int64_t dim, float eps, hipStream_t s) {
+    layer_norm_k<<<(unsigned)rows, kT, 0, s>>>(x, gamma, beta, y, dim, eps);
     return hipGetLastError();
 }
 

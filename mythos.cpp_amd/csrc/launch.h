@@ -143,6 +143,16 @@ hipError_t launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
 hipError_t launch_mul(const float* a, const float* b, float* c, int64_t n, hipStream_t s);
 hipError_t launch_softmax(const float* x, float* y, int64_t rows, int64_t dim, hipStream_t s);
+// The ComputeBackend vtable's remaining dense operators (dense.hip).
+hipError_t launch_softmax_axis(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, hipStream_t s);
+hipError_t launch_axpby(float alpha, const float* x, float beta, float* y, int64_t n, hipStream_t s);
+hipError_t launch_gemv_f32(float alpha, const float* A, const float* x, float beta, float* y, int64_t M, int64_t N,
+                           hipStream_t s);
+hipError_t launch_relu(const float* x, float* y, int64_t n, hipStream_t s);
+hipError_t launch_gelu(const float* x, float* y, int64_t n, hipStream_t s);
+hipError_t launch_scale(float a, const float* x, float* y, int64_t n, hipStream_t s);
+hipError_t launch_layer_norm(const float* x, const float* gamma, const float* beta, float* y, int64_t rows,
+                             int64_t dim, float eps, hipStream_t s);
 // Position pos = (step ? *step : 0) + pos0; caches [batch][kv_heads][max_seq][head_dim].
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
                           float* kc, float* vc, const int* step, int pos0, int64_t batch, int heads, int kv_heads,

@@ -308,14 +308,17 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
     for (int w2 = 1; w2 < kSwT / 64; ++w2) m = fmaxf(m, red[w2]);
     if (m < 1e-10f) m = 1e-10f;
     const float sc = __fdiv_rn(127.0f, m), inv = __fdiv_rn(m, 127.0f);
+    // q is stored transposed within each 16-column group (column 4b + j of a
+    // group at byte 4j + b), the operand order of tdot16, so a row's operands
+    // are plain 16-byte reads
 #pragma unroll
     for (int j = 0; j < kSwQ; ++j) {
         const int i = tid + j * kSwT;
-        if (i < K) q[i] = (int8_t)quant_i8(gv[j], sc);
+        if (i < K) q[(i & ~15) | ((i & 3) << 2) | ((i >> 2) & 3)] = (int8_t)quant_i8(gv[j], sc);
     }
     __syncthreads();
 
-    // lane's activations, transposed: A[s][d][j] byte b = a[seg*64 + 16d + 4b + j]
+    // lane's activations: A[s][d][j] byte b = a[seg*64 + 16d + 4b + j]
     uint32_t A[NSEG][4][4];
     int asum = 0;
 #pragma unroll
@@ -325,13 +328,9 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
                 const uint4 n = *(const uint4*)(q + seg * 64 + 16 * d);
-                const uint32_t N[4] = {n.x, n.y, n.z, n.w};
+                A[s][d][0] = n.x, A[s][d][1] = n.y, A[s][d][2] = n.z, A[s][d][3] = n.w;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    A[s][d][j] = ((N[0] >> (8 * j)) & 0xffu) | (((N[1] >> (8 * j)) & 0xffu) << 8) |
-                                 (((N[2] >> (8 * j)) & 0xffu) << 16) | (((N[3] >> (8 * j)) & 0xffu) << 24);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) asum = dot4(N[j], 0x01010101u, asum);
+                for (int j = 0; j < 4; ++j) asum = dot4(A[s][d][j], 0x01010101u, asum);
             }
         } else {
 #pragma unroll

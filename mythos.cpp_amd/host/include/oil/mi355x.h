@@ -4,9 +4,19 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 
 namespace oil {
+namespace backend {
+class ComputeBackend;
+}
 namespace mi355x {
+
+// The HIP ComputeBackend (oil/backend.h) on HIP device device_id; the caller
+// owns it.  This is what ComputeBackend::create(GPU_CUDA) returns; the
+// reference's factory calls it from its GPU_CUDA case when built with
+// OIL_HAS_MI355X.
+backend::ComputeBackend* make_hip_backend(int64_t device_id);
 
 // Uploads [host, host + bytes) to device memory once.  Afterwards every
 // oil::kernel call whose weight operand (indices, packed weights, codebooks,

@@ -1,8 +1,10 @@
 // oil/tensor.h — minimal host Tensor for the operator signatures that take
-// tensors (i2s_gemm, tl1_gemm, tl2_gemm, i2s_gemm_avx2).  Matches the
-// reference's observable contract (include/oil/tensor.h:15-94,
-// src/tensor.cpp:74-82): Tensor(Shape, DType) owns numel*dtype_size bytes,
-// zero-filled and 64-byte aligned; data()/data<T>()/numel()/shape()/dtype().
+// tensors (i2s_gemm, tl1_gemm, tl2_gemm, i2s_gemm_avx2, the ComputeBackend
+// vtable).  Matches the reference's observable contract
+// (include/oil/tensor.h:15-94, src/tensor.cpp:74-82,233-246): Tensor(Shape,
+// DType) owns numel*dtype_size bytes, zero-filled and 64-byte aligned;
+// data()/data<T>()/numel()/shape()/dtype(); fill (every element as float),
+// zero_ (every byte), copy_from (equal numel, size_bytes copied).
 #pragma once
 
 #include <cstdlib>
@@ -34,6 +36,18 @@ public:
     const void* data() const { return buf_.get(); }
     template <typename T> T* data() { return static_cast<T*>(data()); }
     template <typename T> const T* data() const { return static_cast<const T*>(data()); }
+
+    void fill(float val) {
+        float* d = data<float>();
+        for (int64_t i = 0; i < numel(); i++) d[i] = val;
+    }
+    void zero_() {
+        if (data()) std::memset(data(), 0, size_bytes());
+    }
+    void copy_from(const Tensor& src) {
+        OIL_CHECK(numel() == src.numel(), "copy_from: size mismatch");
+        if (size_bytes()) std::memcpy(data(), src.data(), size_bytes());
+    }
 
 private:
     Shape shape_;

@@ -28,7 +28,8 @@ EXPORTS = (
     "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
     "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
     "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_silu_mul_quant", "mth_add", "mth_mul",
-    "mth_softmax",
+    "mth_softmax", "mth_softmax_axis", "mth_axpby", "mth_gemv_f32", "mth_relu", "mth_gelu", "mth_scale",
+    "mth_layer_norm",
     "mth_rope_tables", "mth_rope_kv", "mth_attention_decode", "mth_argmax",
 )
 
@@ -84,6 +85,13 @@ _SIG = {
     "mth_add": [VP, VP, VP, I64, VP],
     "mth_mul": [VP, VP, VP, I64, VP],
     "mth_softmax": [VP, VP, I64, I64, VP],
+    "mth_softmax_axis": [VP, VP, I64, I64, I64, VP],
+    "mth_axpby": [F32, VP, F32, VP, I64, VP],
+    "mth_gemv_f32": [F32, VP, VP, F32, VP, I64, I64, VP],
+    "mth_relu": [VP, VP, I64, VP],
+    "mth_gelu": [VP, VP, I64, VP],
+    "mth_scale": [F32, VP, VP, I64, VP],
+    "mth_layer_norm": [VP, VP, VP, VP, I64, I64, F32, VP],
     "mth_rope_tables": [I64, I64, F32, VP, VP],
     "mth_rope_kv": [VP, VP, VP, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP],
     "mth_attention_decode": [VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP],
@@ -311,6 +319,46 @@ def softmax(x, y, rows, dim, stream=None):
     t = _torch()
     _check(_lib.mth_softmax(_ptr(x, t.float32, rows * dim, "x"), _ptr(y, t.float32, rows * dim, "y"), rows, dim,
                             _stream(stream)))
+
+
+def softmax_axis(x, y, outer, dim, inner, stream=None):
+    t = _torch()
+    n = outer * dim * inner
+    _check(_lib.mth_softmax_axis(_ptr(x, t.float32, n, "x"), _ptr(y, t.float32, n, "y"), outer, dim, inner,
+                                 _stream(stream)))
+
+
+def axpby(alpha, x, beta, y, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_axpby(alpha, _ptr(x, t.float32, n, "x"), beta, _ptr(y, t.float32, n, "y"), n, _stream(stream)))
+
+
+def gemv_f32(alpha, A, x, beta, y, M, N, stream=None):
+    t = _torch()
+    _check(_lib.mth_gemv_f32(alpha, _ptr(A, t.float32, M * N, "A"), _ptr(x, t.float32, N, "x"), beta,
+                             _ptr(y, t.float32, M, "y"), M, N, _stream(stream)))
+
+
+def relu(x, y, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_relu(_ptr(x, t.float32, n, "x"), _ptr(y, t.float32, n, "y"), n, _stream(stream)))
+
+
+def gelu(x, y, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_gelu(_ptr(x, t.float32, n, "x"), _ptr(y, t.float32, n, "y"), n, _stream(stream)))
+
+
+def scale(s, x, y, n, stream=None):
+    t = _torch()
+    _check(_lib.mth_scale(s, _ptr(x, t.float32, n, "x"), _ptr(y, t.float32, n, "y"), n, _stream(stream)))
+
+
+def layer_norm(x, gamma, beta, y, rows, dim, eps=1e-5, stream=None):
+    t = _torch()
+    _check(_lib.mth_layer_norm(_ptr(x, t.float32, rows * dim, "x"), _ptr(gamma, t.float32, dim, "gamma"),
+                               _ptr(beta, t.float32, dim, "beta"), _ptr(y, t.float32, rows * dim, "y"), rows, dim,
+                               eps, _stream(stream)))
 
 
 def rope_tables(head_dim, max_seq, theta=10000.0):

@@ -104,6 +104,12 @@ class Oracle:
             "orc_tl1_precompute_lut": [VP, VP, I64],
             "orc_tl2_precompute_lut": [VP, VP, I64],
             "orc_gemv": [F32, VP, VP, F32, VP, I64, I64],
+            "orc_gemm": [F32, VP, VP, F32, VP, I64, I64, I64],
+            "orc_relu": [VP, VP, I64],
+            "orc_gelu": [VP, VP, I64],
+            "orc_scale": [F32, VP, VP, I64],
+            "orc_layer_norm": [VP, VP, VP, F32, VP, I64, I64],
+            "orc_softmax_axis": [VP, VP, I64, I64, I64],
             "orc_rms_norm": [VP, VP, F32, VP, I64, I64],
             "orc_silu": [VP, VP, I64],
             "orc_oil4_gemm_prefill": [VP, VP, VP, I64, VP, VP, I64, I64, I64, I32],
@@ -286,6 +292,37 @@ class Oracle:
     def rms_norm(self, x, g, eps, rows, dim):
         y = np.empty((rows, dim), np.float32)
         self.lib.orc_rms_norm(_p(x, np.float32), _p(g, np.float32), eps, _p(y, np.float32), rows, dim)
+        return y
+
+    def gemm(self, alpha, A, B, beta, C, M, N, K):
+        C = np.array(C, np.float32, copy=True).reshape(M, N)
+        self.lib.orc_gemm(alpha, _p(A, np.float32), _p(B, np.float32), beta, _p(C, np.float32), M, N, K)
+        return C
+
+    def relu(self, x):
+        y = np.empty_like(x, dtype=np.float32)
+        self.lib.orc_relu(_p(x, np.float32), _p(y, np.float32), x.size)
+        return y
+
+    def gelu(self, x):
+        y = np.empty_like(x, dtype=np.float32)
+        self.lib.orc_gelu(_p(x, np.float32), _p(y, np.float32), x.size)
+        return y
+
+    def scale(self, s, x):
+        y = np.empty_like(x, dtype=np.float32)
+        self.lib.orc_scale(s, _p(x, np.float32), _p(y, np.float32), x.size)
+        return y
+
+    def layer_norm(self, x, g, b, eps, rows, dim):
+        y = np.empty((rows, dim), np.float32)
+        self.lib.orc_layer_norm(_p(x, np.float32), _p(g, np.float32), _p(b, np.float32), eps, _p(y, np.float32),
+                                rows, dim)
+        return y
+
+    def softmax_axis(self, x, outer, dim, inner):
+        y = np.empty(outer * dim * inner, np.float32)
+        self.lib.orc_softmax_axis(_p(x, np.float32), _p(y, np.float32), outer, dim, inner)
         return y
 
     # -- config-5 decoder (decoder.c) -------------------------------------

@@ -497,6 +497,64 @@ void orc_rms_norm(const float* x, const float* gamma, float eps, float* y,
 void orc_silu(const float* x, float* y, int64_t n) {                     /* :119-128 */
     for (int64_t i = 0; i < n; i++) y[i] = x[i] / (1.0f + expf(-x[i]));
 }
+void orc_gemm(float alpha, const float* A, const float* B, float beta, float* C,
+              int64_t M, int64_t N, int64_t K) {                        /* :74-97 */
+    for (int64_t i = 0; i < M; i++)
+        for (int64_t j = 0; j < N; j++) {
+            float s = 0.0f;
+            for (int64_t k = 0; k < K; k++) s += A[i * K + k] * B[k * N + j];
+            C[i * N + j] = alpha * s + beta * C[i * N + j];
+        }
+}
+void orc_relu(const float* x, float* y, int64_t n) {                     /* :99-105 */
+    for (int64_t i = 0; i < n; i++) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+void orc_gelu(const float* x, float* y, int64_t n) {                     /* :107-117 */
+    const float s = 0.7071067811865475f;
+    for (int64_t i = 0; i < n; i++) {
+        const float v = x[i];
+        y[i] = 0.5f * v * (1.0f + erff(v * s));
+    }
+}
+void orc_scale(float s, const float* x, float* y, int64_t n) {           /* :278-284 */
+    for (int64_t i = 0; i < n; i++) y[i] = s * x[i];
+}
+void orc_layer_norm(const float* x, const float* gamma, const float* beta, float eps, float* y,
+                    int64_t rows, int64_t dim) {                         /* :148-180 */
+    for (int64_t i = 0; i < rows; i++) {
+        const float* r = x + i * dim;
+        double mu = 0.0;
+        for (int64_t j = 0; j < dim; j++) mu += r[j];
+        mu /= (double)dim;
+        double var = 0.0;
+        for (int64_t j = 0; j < dim; j++) {
+            const double d = r[j] - mu;
+            var += d * d;
+        }
+        var /= (double)dim;
+        const double inv = 1.0 / sqrt(var + (double)eps);
+        for (int64_t j = 0; j < dim; j++) y[i * dim + j] = (float)(((double)r[j] - mu) * inv) * gamma[j] + beta[j];
+    }
+}
+/* softmax along the middle axis of [outer][dim][inner] (:207-249): float
+ * max, float exp, double sum, (float)(e * (1/sum)). */
+void orc_softmax_axis(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner) {
+    for (int64_t o = 0; o < outer; o++)
+        for (int64_t i = 0; i < inner; i++) {
+            const float* s = x + o * dim * inner + i;
+            float* d = y + o * dim * inner + i;
+            float mx = -INFINITY;
+            for (int64_t k = 0; k < dim; k++) mx = s[k * inner] > mx ? s[k * inner] : mx;
+            double sum = 0.0;
+            for (int64_t k = 0; k < dim; k++) {
+                const float v = expf(s[k * inner] - mx);
+                d[k * inner] = v;
+                sum += v;
+            }
+            const double inv = 1.0 / sum;
+            for (int64_t k = 0; k < dim; k++) d[k * inner] = (float)((double)d[k * inner] * inv);
+        }
+}
 
 /* ------------------------------------------------------------------------ */
 /* OIL4 prefill GEMM reference                                              */

@@ -87,6 +87,14 @@ void orc_tl2_gemm(const uint8_t* w, const float* a, float* o,
 /* ---- dense FP32 math (src/math.cpp) --------------------------------------- */
 void orc_gemv(float alpha, const float* A, const float* x, float beta, float* y,
               int64_t M, int64_t N);                             /* :52-72 */
+void orc_gemm(float alpha, const float* A, const float* B, float beta, float* C,
+              int64_t M, int64_t N, int64_t K);                         /* src/math.cpp:74-97 */
+void orc_relu(const float* x, float* y, int64_t n);                      /* src/math.cpp:99-105 */
+void orc_gelu(const float* x, float* y, int64_t n);                      /* src/math.cpp:107-117 */
+void orc_scale(float s, const float* x, float* y, int64_t n);            /* src/math.cpp:278-284 */
+void orc_layer_norm(const float* x, const float* gamma, const float* beta, float eps, float* y,
+                    int64_t rows, int64_t dim);                          /* src/math.cpp:148-180 */
+void orc_softmax_axis(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner); /* :207-249 */
 void orc_rms_norm(const float* x, const float* gamma, float eps, float* y,
                   int64_t rows, int64_t dim);                    /* :182-205 */
 void orc_silu(const float* x, float* y, int64_t n);              /* :119-128 */

@@ -128,6 +128,11 @@ FACADE = [
     "oil::quantize_per_token(float const*, signed char*, long, long)",
     "oil::quantize_per_tensor(float const*, signed char*, long)",
     "oil::dequantize_per_tensor(signed char const*, float*, long, float)",
+    # include/oil/backend.h:79,87,96 (the HIP ComputeBackend behind the factory)
+    "oil::backend::ComputeBackend::create(oil::backend::BackendConfig const&)",
+    "oil::backend::is_cuda_available()",
+    "oil::backend::gpu_memory_free(long)",
+    "oil::mi355x::make_hip_backend(long)",
 ]
 
 
@@ -145,14 +150,16 @@ REF_INCLUDE = os.environ.get("MYTHOS_REFERENCE", "/root/reference") + "/include"
 
 @pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="reference headers not present on this host")
 def test_facade_compiles_against_reference_headers():
-    """The façade source builds against the reference's own oil/*.h (its
-    Tensor, Error, Int8QuantParams), so it links into the reference's tree in
-    place of its CPU kernel library."""
-    src = os.path.join(PKG, "host", "kernel.cpp")
-    r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++20", "-fsyntax-only", f"-I{REF_INCLUDE}",
-                        f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(PKG, 'host', 'include')}", src],
-                       capture_output=True, text=True)
-    assert r.returncode == 0, r.stderr
+    """The façade sources build against the reference's own oil/*.h (its
+    Tensor, Error, Int8QuantParams, and its ComputeBackend declaration, which
+    the HIP backend overrides), so they link into the reference's tree in
+    place of its CPU kernel library and its backend factory."""
+    for name, defs in (("kernel.cpp", []), ("backend.cpp", []), ("backend.cpp", ["-DOIL_HAS_MI355X=1"])):
+        src = os.path.join(PKG, "host", name)
+        r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++20", "-fsyntax-only", *defs, f"-I{REF_INCLUDE}",
+                            f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(PKG, 'host', 'include')}", src],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, (name, defs, r.stderr)
 
 
 def test_decoder_argument_errors(mth):

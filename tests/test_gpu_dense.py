@@ -119,6 +119,101 @@ def test_softmax(rows, dim, oracle, mth, dev):
     np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-30)
 
 
+# ---- the ComputeBackend vtable's remaining dense operators --------------------
+@pytest.mark.parametrize("outer,dim,inner", [(3, 41, 7), (1, 1000, 1), (2, 5, 300), (1, 1, 9)])
+def test_softmax_axis(outer, dim, inner, oracle, mth, dev):
+    import torch
+    print(f"softmax_axis {outer}x{dim}x{inner}", flush=True)
+    g = np.random.default_rng(outer * 100 + dim + inner)
+    x = g.normal(0, 5, outer * dim * inner).astype(np.float32)
+    y = torch.empty(outer * dim * inner, dtype=torch.float32, device=dev)
+    mth.softmax_axis(dev_t(x, dev), y, outer, dim, inner)
+    np.testing.assert_allclose(host(y), oracle.softmax_axis(x, outer, dim, inner), rtol=2e-6, atol=1e-30)
+
+
+def test_axpby_rounding_and_nan(oracle, mth, dev):
+    """alpha*x + beta*y with each product and the sum rounded (the gemm/gemv
+    epilogue, src/math.cpp:70,94): bit-exact against numpy's float32
+    operations; y is read even with beta = 0, so NaN/Inf there propagate."""
+    import torch
+    g = np.random.default_rng(31)
+    n = 70001
+    x = g.normal(0, 3, n).astype(np.float32)
+    y0 = g.normal(0, 3, n).astype(np.float32)
+    for alpha, beta in ((1.7, -0.3), (1.0, 0.0), (0.0, 2.5)):
+        y = dev_t(y0, dev)
+        mth.axpby(alpha, dev_t(x, dev), beta, y, n)
+        want = np.float32(alpha) * x + np.float32(beta) * y0
+        assert np.array_equal(host(y), want), (alpha, beta)
+    y0[[5, 17]] = np.nan, np.inf
+    y = dev_t(y0, dev)
+    mth.axpby(1.0, dev_t(x, dev), 0.0, y, n)
+    got = host(y)
+    assert np.isnan(got[5]) and np.isnan(got[17]) and np.array_equal(np.delete(got, [5, 17]), np.delete(x, [5, 17]))
+
+
+@pytest.mark.parametrize("M,N", [(4096, 4096), (37, 1001), (1, 64), (300, 3)])
+def test_gemv_f32(M, N, oracle, mth, dev):
+    import torch
+    from conftest import fp32_close
+    print(f"gemv_f32 M={M} N={N}", flush=True)
+    g = np.random.default_rng(M + 7 * N)
+    A = g.normal(0, 1, (M, N)).astype(np.float32)
+    x = g.normal(0, 1, N).astype(np.float32)
+    y0 = g.normal(0, 1, M).astype(np.float32)
+    y = dev_t(y0, dev)
+    mth.gemv_f32(0.75, dev_t(A, dev), dev_t(x, dev), -1.25, y, M, N)
+    want = oracle.gemv(0.75, A, x, -1.25, y0, M, N)
+    absw = 0.75 * (np.abs(A.astype(np.float64)) @ np.abs(x.astype(np.float64))) + 1.25 * np.abs(y0)
+    fp32_close(host(y), want, absw, 1e-5, "gemv_f32")
+    # integers: exact in any order
+    Ai = g.integers(-8, 9, (M, N)).astype(np.float32)
+    xi = g.integers(-8, 9, N).astype(np.float32)
+    y = dev_t(y0, dev)
+    mth.gemv_f32(1.0, dev_t(Ai, dev), dev_t(xi, dev), 0.0, y, M, N)
+    assert np.array_equal(host(y), oracle.gemv(1.0, Ai, xi, 0.0, y0, M, N))
+
+
+def test_relu_gelu_scale(oracle, mth, dev):
+    import torch
+    g = np.random.default_rng(32)
+    x = np.concatenate([g.normal(0, 3, 50000), np.linspace(-12, 12, 301),
+                        [0.0, -0.0, np.inf, -np.inf, np.nan]]).astype(np.float32)
+    n = x.size
+    dx, y = dev_t(x, dev), torch.empty(n, dtype=torch.float32, device=dev)
+    mth.relu(dx, y, n)
+    assert np.array_equal(host(y), oracle.relu(x))
+    mth.scale(-0.375, dx, y, n)
+    assert np.array_equal(host(y), oracle.scale(-0.375, x), equal_nan=True)
+    mth.gelu(dx, y, n)
+    got, want = host(y).astype(np.float64), oracle.gelu(x).astype(np.float64)
+    fin = np.isfinite(want)
+    # device erff vs the C library's: a few ulps of erf, amplified by the
+    # cancellation in 1 + erf for x << 0 (the reference's own FP32 form)
+    bound = 4e-7 * np.abs(want[fin]) + 2.5e-7 * np.abs(0.5 * x[fin].astype(np.float64)) + 1e-37
+    assert np.all(np.abs(got[fin] - want[fin]) <= bound)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~fin & ~np.isnan(want)], want[~fin & ~np.isnan(want)])
+
+
+@pytest.mark.parametrize("rows,dim", [(4, 4096), (3, 1000), (1, 7)])
+def test_layer_norm(rows, dim, oracle, mth, dev):
+    import torch
+    print(f"layer_norm rows={rows} dim={dim}", flush=True)
+    g = np.random.default_rng(rows * 13 + dim)
+    x = (g.normal(0, 2, (rows, dim)) + g.normal(0, 20, (rows, 1))).astype(np.float32)
+    gm = g.uniform(0.5, 1.5, dim).astype(np.float32)
+    bt = g.normal(0, 1, dim).astype(np.float32)
+    y = torch.empty((rows, dim), dtype=torch.float32, device=dev)
+    mth.layer_norm(dev_t(x, dev), dev_t(gm, dev), dev_t(bt, dev), y, rows, dim, 1e-5)
+    want = oracle.layer_norm(x, gm, bt, 1e-5, rows, dim)
+    # double statistics summed in another order: (float)(d * inv) may differ by
+    # one ulp, then * gamma + beta (two roundings)
+    z = np.abs(want.astype(np.float64) - bt)
+    bound = 3 * np.finfo(np.float32).eps * (z + np.abs(want)) + 1e-30
+    assert np.all(np.abs(host(y).astype(np.float64) - want) <= bound)
+
+
 @pytest.mark.parametrize("D", [64, 128, 256])
 def test_rope_kv_bit_exact(D, oracle, mth, dev):
     import torch

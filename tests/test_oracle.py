@@ -254,6 +254,87 @@ def test_rms_norm_and_silu(oracle):
     np.testing.assert_allclose(oracle.silu(s), s / (1 + np.exp(-s.astype(np.float64))), rtol=2e-6, atol=1e-30)
 
 
+def test_gemm_closed_forms(oracle):
+    """math::gemm (src/math.cpp:74-97): small-integer operands make every sum
+    exact, so C = alpha*(A B) + beta*C must equal the integer product; a
+    one-column B is math::gemv bit for bit (same sum order); C is read even
+    with beta = 0, so NaN/Inf there reach the result as in the reference."""
+    g = rng(21)
+    M, N, K = 7, 5, 33
+    A = g.integers(-8, 9, (M, K)).astype(np.float32)
+    B = g.integers(-8, 9, (K, N)).astype(np.float32)
+    C = g.integers(-8, 9, (M, N)).astype(np.float32)
+    want = 2.0 * (A.astype(np.int64) @ B.astype(np.int64)) - 0.5 * C
+    assert np.array_equal(oracle.gemm(2.0, A, B, -0.5, C, M, N, K), want.astype(np.float32))
+    x = g.normal(0, 1, K).astype(np.float32)
+    y0 = g.normal(0, 1, M).astype(np.float32)
+    col = oracle.gemm(1.5, A, x.reshape(K, 1).copy(), 0.25, y0.reshape(M, 1), M, 1, K)
+    assert np.array_equal(col.ravel(), oracle.gemv(1.5, A, x, 0.25, y0, M, K))
+    Cn = np.zeros((M, N), np.float32)
+    Cn[1, 2], Cn[3, 4] = np.nan, np.inf
+    out = oracle.gemm(1.0, A, B, 0.0, Cn, M, N, K)
+    assert np.isnan(out[1, 2]) and np.isnan(out[3, 4])  # 0 * NaN, 0 * Inf
+    assert np.isfinite(np.delete(out.ravel(), [1 * N + 2, 3 * N + 4])).all()
+
+
+def test_relu_gelu_scale(oracle):
+    """relu / gelu / scale (src/math.cpp:99-117, :278-284): relu exactly
+    max(x, 0) with NaN -> 0; gelu against float64 0.5 x (1 + erf(x/sqrt 2)),
+    the FP32 bound one ulp of 1 in (1 + erf) times |x|/2 (the sum cancels for
+    x << 0) plus a few ulps of the result; scale by powers of two is exact."""
+    import math
+    x = np.array([-3.0, -0.0, 0.0, 1e-30, 2.5, np.nan, np.inf, -np.inf], np.float32)
+    r = oracle.relu(x)
+    assert r.tolist()[:5] == [0.0, 0.0, 0.0, np.float32(1e-30), 2.5] and r[5] == 0.0
+    assert r[6] == np.inf and r[7] == 0.0
+    g = rng(22)
+    v = np.concatenate([g.normal(0, 3, 4000), np.linspace(-12, 12, 97), [0.0]]).astype(np.float32)
+    want = np.array([0.5 * t * (1.0 + math.erf(t / math.sqrt(2.0))) for t in v.astype(np.float64)])
+    got = oracle.gelu(v).astype(np.float64)
+    bound = 4e-7 * np.abs(want) + 2.5e-7 * np.abs(0.5 * v.astype(np.float64)) + 1e-37
+    assert np.all(np.abs(got - want) <= bound), float(np.max(np.abs(got - want) - bound))
+    assert oracle.gelu(np.array([0.0], np.float32))[0] == 0.0
+    for s in (0.5, 4.0, -2.0):
+        assert np.array_equal(oracle.scale(s, v), v * np.float32(s))
+
+
+def test_layer_norm_properties(oracle):
+    """layer_norm (src/math.cpp:148-180): gamma = 1, beta = 0 leaves every
+    row with mean 0 and (biased) variance var / (var + eps); gamma and beta
+    are an exact affine map of that output; against float64."""
+    g = rng(23)
+    rows, dim, eps = 5, 300, 1e-5
+    x = (g.normal(0, 2, (rows, dim)) + g.normal(0, 10, (rows, 1))).astype(np.float32)
+    one, zero = np.ones(dim, np.float32), np.zeros(dim, np.float32)
+    z = oracle.layer_norm(x, one, zero, eps, rows, dim).astype(np.float64)
+    xd = x.astype(np.float64)
+    var = xd.var(axis=1, keepdims=True)
+    assert np.abs(z.mean(axis=1)).max() < 1e-6
+    np.testing.assert_allclose(z.var(axis=1, keepdims=True), var / (var + eps), rtol=1e-6)
+    np.testing.assert_allclose(z, (xd - xd.mean(axis=1, keepdims=True)) / np.sqrt(var + eps), rtol=2e-6, atol=1e-6)
+    gam = g.uniform(0.5, 1.5, dim).astype(np.float32)
+    bet = g.normal(0, 1, dim).astype(np.float32)
+    y = oracle.layer_norm(x, gam, bet, eps, rows, dim)
+    assert np.array_equal(y, z.astype(np.float32) * gam + bet)
+
+
+def test_softmax_axis(oracle):
+    """softmax along any axis (src/math.cpp:207-249): inner = 1 is the
+    row softmax bit for bit; along axis 0 of [dim][inner] it is the row
+    softmax of the transpose bit for bit (same per-column order); every
+    column sums to 1."""
+    g = rng(24)
+    outer, dim, inner = 3, 41, 7
+    x = g.normal(0, 4, outer * dim * inner).astype(np.float32)
+    rows = oracle.softmax(x, outer * inner * dim // dim, dim)
+    assert np.array_equal(oracle.softmax_axis(x, outer * inner, dim, 1), rows.ravel())
+    y = oracle.softmax_axis(x, outer, dim, inner).reshape(outer, dim, inner)
+    xt = np.ascontiguousarray(x.reshape(outer, dim, inner).transpose(0, 2, 1)).ravel()
+    yt = oracle.softmax(xt, outer * inner, dim).reshape(outer, inner, dim).transpose(0, 2, 1)
+    assert np.array_equal(y, yt)
+    np.testing.assert_allclose(y.astype(np.float64).sum(axis=1), 1.0, rtol=1e-6)
+
+
 # -------------------------------------------------------------- prefill ---
 def test_prefill_reference(oracle):
     """C = bf16(sum_k A[m][k] W[n][k]): against a float64 contraction of the
