@@ -127,17 +127,37 @@ struct Slices {
 constexpr int kMaxSlices = 16;
 inline Slices plain_slices(const float* y, int64_t ts) { return Slices{y, ts, 0, 1, 1.0f, nullptr}; }
 
-__device__ __forceinline__ float slice_value(const Slices& s, int t, int64_t m) {
+// slice_value in two steps, so that a consumer can put the loads of several
+// values (and of its other operands) in flight before it waits for any:
+// slice_issue loads the n partials of value (t, m) into v (the rest are 0),
+// slice_sum adds them in the order above and applies the epilogue.
+__device__ __forceinline__ void slice_issue(const Slices& s, int t, int64_t m, float (&v)[kMaxSlices]) {
     const float* q = s.p + (int64_t)t * s.ts + m;
-    float v[kMaxSlices];
 #pragma unroll
-    for (int z = 0; z < kMaxSlices; ++z) v[z] = z < s.n ? q[z * s.zs] : 0.0f;  // every load before the first add
+    for (int z = 0; z < kMaxSlices; ++z) v[z] = z < s.n ? q[z * s.zs] : 0.0f;
+}
+// slice_issue with every load unconditional (n >= 1; slices z >= n re-read
+// slice n - 1, in bounds and from cache): no branch between the loads, so
+// the loads of several values stay in flight together.  slice_sum ignores
+// v[z] for z >= n.
+__device__ __forceinline__ void slice_issue_all(const Slices& s, int t, int64_t m, float (&v)[kMaxSlices]) {
+    const float* q = s.p + (int64_t)t * s.ts + m;
+    const int last = s.n - 1;
+#pragma unroll
+    for (int z = 0; z < kMaxSlices; ++z) v[z] = q[(int64_t)min(z, last) * s.zs];
+}
+__device__ __forceinline__ float slice_sum(const Slices& s, int t, const float (&v)[kMaxSlices]) {
     float sum = v[0];
 #pragma unroll
     for (int z = 1; z < kMaxSlices; ++z)
         if (z < s.n) sum += v[z];
     if (s.tscale) sum = __fmul_rn(__fmul_rn(sum, s.scale), s.tscale[t]);
     return sum;
+}
+__device__ __forceinline__ float slice_value(const Slices& s, int t, int64_t m) {
+    float v[kMaxSlices];
+    slice_issue(s, t, m, v);  // every load before the first add
+    return slice_sum(s, t, v);
 }
 // Four consecutive m (m % 4 == 0; 16-byte aligned rows).
 __device__ __forceinline__ float4 slice_value4(const Slices& s, int t, int64_t m) {
@@ -187,13 +207,34 @@ __device__ __forceinline__ double wave_sum_dbl(double v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// This thread's share of token t's NormScale sum: partials i = i0, i0 +
+// stride, ... added in order.  norm_issue loads the first kNormBatch of them
+// (clamped to the last partial, so every load is in bounds and none waits
+// on a branch) and norm_finish adds them, then any further ones.
+constexpr int kNormBatch = 4;
+__device__ __forceinline__ void norm_issue(const NormScale& ns, int t, int i0, int stride,
+                                           double (&v)[kNormBatch]) {
+    const double* p = ns.ssp + (int64_t)t * ns.nparts;
+    const int last = ns.nparts - 1;
+#pragma unroll
+    for (int j = 0; j < kNormBatch; ++j) v[j] = last >= 0 ? p[min(i0 + j * stride, last)] : 0.0;
+}
+__device__ __forceinline__ double norm_finish(const NormScale& ns, int t, int i0, int stride,
+                                              const double (&v)[kNormBatch]) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < kNormBatch; ++j)
+        if (i0 + j * stride < ns.nparts) s += v[j];
+    for (int i = i0 + kNormBatch * stride; i < ns.nparts; i += stride) s += ns.ssp[(int64_t)t * ns.nparts + i];
+    return s;
+}
 // 1 / sqrt(sum / dim + eps) of token t, computed by a whole workgroup of
 // NW waves (red: NW doubles of LDS); every thread gets it.
 template <int NW>
 __device__ __forceinline__ float norm_scale(const NormScale& ns, int t, double* red) {
-    double s = 0.0;
-    for (int i = threadIdx.x; i < ns.nparts; i += NW * 64) s += ns.ssp[(int64_t)t * ns.nparts + i];
-    s = wave_sum_dbl(s);
+    double v[kNormBatch];
+    norm_issue(ns, t, threadIdx.x, NW * 64, v);
+    double s = wave_sum_dbl(norm_finish(ns, t, threadIdx.x, NW * 64, v));
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();

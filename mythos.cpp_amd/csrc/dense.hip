@@ -382,26 +382,44 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     const int nmem = ROPE ? pos : ctx;  // positions read from the cache
     const int g = tid % G, sl = tid / G;
 
-    // Every load before the first use, in order of use: the norm's partial
-    // sums and the current token's q/k/v (and RoPE angles), then this
-    // thread's K row of the first tile, then its V rows.
-    double nsum = 0.0;
-    if (ROPE && ns.ssp)
-        for (int i = tid; i < ns.nparts; i += kT) nsum += ns.ssp[(int64_t)row * ns.nparts + i];
+    // Every load issued before the first wait, in order of use: the norm's
+    // partial sums and the current token's q/k/v partials (and RoPE angles),
+    // then this thread's K row of the first tile, then its V rows; the sums
+    // of both come after.
+    // Plain q/k/v (one slice, no epilogue: the decode GEMVs' own outputs)
+    // are six loads; split-K partials are loaded without branches
+    // (slice_issue_all) and added after the cache loads are issued.
+    double npart[kNormBatch];
+    if (ROPE && ns.ssp) norm_issue(ns, row, tid, kT, npart);
+    const bool plain = q.n == 1 && !q.tscale && (!ROPE || (kin.n == 1 && vin.n == 1 && !kin.tscale && !vin.tscale));
+    float raw[ROPE ? 6 : 1][kMaxSlices];
     float q1 = 0.0f, q2 = 0.0f, k1 = 0.0f, k2 = 0.0f, v1 = 0.0f, v2 = 0.0f, c = 0.0f, sn = 0.0f;
     if (ROPE) {
         if (tid < D / 2) {
-            q1 = slice_value(q, row, h * D + tid);
-            q2 = slice_value(q, row, h * D + tid + D / 2);
-            k1 = slice_value(kin, row, kh * D + tid);
-            k2 = slice_value(kin, row, kh * D + tid + D / 2);
-            v1 = slice_value(vin, row, kh * D + tid);
-            v2 = slice_value(vin, row, kh * D + tid + D / 2);
+            const int64_t qm = h * D + tid, km = kh * D + tid;
+            if (plain) {
+                q1 = q.p[row * q.ts + qm];
+                q2 = q.p[row * q.ts + qm + D / 2];
+                k1 = kin.p[row * kin.ts + km];
+                k2 = kin.p[row * kin.ts + km + D / 2];
+                v1 = vin.p[row * vin.ts + km];
+                v2 = vin.p[row * vin.ts + km + D / 2];
+            } else {
+                slice_issue_all(q, row, qm, raw[0]);
+                slice_issue_all(q, row, qm + D / 2, raw[1]);
+                slice_issue_all(kin, row, km, raw[2]);
+                slice_issue_all(kin, row, km + D / 2, raw[3]);
+                slice_issue_all(vin, row, km, raw[4]);
+                slice_issue_all(vin, row, km + D / 2, raw[5]);
+            }
             c = cos_t[(int64_t)pos * (D / 2) + tid];
             sn = sin_t[(int64_t)pos * (D / 2) + tid];
         }
     } else if (tid < D) {
-        q1 = slice_value(q, row, h * D + tid);
+        if (plain)
+            q1 = q.p[row * q.ts + h * D + tid];
+        else
+            slice_issue_all(q, row, h * D + tid, raw[0]);
     }
     // cache rows: this thread's K row of the first tile, then its V rows
     Raw kr0[D / 4];
@@ -418,11 +436,25 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         const int t = sl + SL * j;
         vpre[j] = kv_raw4(vcol + (int64_t)(t < nmem ? t : 0) * D);
     }
+    if (!plain) {
+        if (ROPE) {
+            if (tid < D / 2) {
+                q1 = slice_sum(q, row, raw[0]);
+                q2 = slice_sum(q, row, raw[1]);
+                k1 = slice_sum(kin, row, raw[2]);
+                k2 = slice_sum(kin, row, raw[3]);
+                v1 = slice_sum(vin, row, raw[4]);
+                v2 = slice_sum(vin, row, raw[5]);
+            }
+        } else if (tid < D) {
+            q1 = slice_sum(q, row, raw[0]);
+        }
+    }
     if (ROPE) {
         __shared__ double nred[kT / 64];
         float ni = 1.0f;
         if (ns.ssp) {  // the RMSNorm's 1 / rms (NormScale): same sum as norm_scale
-            const double sum = wave_sum_dbl(nsum);
+            const double sum = wave_sum_dbl(norm_finish(ns, row, tid, kT, npart));
             if ((tid & 63) == 0) nred[tid >> 6] = sum;
             __syncthreads();
             double t = 0.0;
@@ -874,6 +906,9 @@ static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& 
                                 const float* cos_t, const float* sin_t, KV* kc, KV* vc, float* out, const int* step,
                                 int ctx0, int64_t rows, int np, int heads, int kv_heads, int head_dim, int max_seq,
                                 hipStream_t s) {
+    // the kernel reads 1..kMaxSlices partials of q (and of k, v with RoPE)
+    auto bad = [](const Slices& x) { return x.n < 1 || x.n > kMaxSlices; };
+    if (bad(q) || (ROPE && (bad(k) || bad(v)))) return hipErrorInvalidValue;
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
     const dim3 grid((unsigned)heads, (unsigned)rows);

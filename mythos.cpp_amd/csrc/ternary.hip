@@ -263,9 +263,8 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
     const int row = blockIdx.x * (kSwT / 64) + wave;
     const int bpr = K >> 2, nseg = bpr >> 4;
 
-    double nsum = 0.0;
-    if (ns.ssp)
-        for (int i = tid; i < ns.nparts; i += kSwT) nsum += ns.ssp[i];
+    double npart[kNormBatch];
+    if (ns.ssp) norm_issue(ns, 0, tid, kSwT, npart);
     float gv[kSwQ], uv[kSwQ];
 #pragma unroll
     for (int j = 0; j < kSwQ; ++j) {
@@ -281,7 +280,7 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
     __builtin_amdgcn_sched_barrier(0);
 
     if (ns.ssp) {  // norm_scale<16>: per-thread sums, wave sums, waves in order
-        double sum = wave_sum_dbl(nsum);
+        double sum = wave_sum_dbl(norm_finish(ns, 0, tid, kSwT, npart));
         if (lane == 0) nred[wave] = sum;
         __syncthreads();
         sum = 0.0;
