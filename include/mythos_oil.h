@@ -215,6 +215,27 @@ int mth_silu_mul(const float* g, const float* u, float* y, int64_t rows, int64_t
 int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_scale, int64_t rows, int64_t n,
                        int64_t gstride, int64_t ustride, mth_stream_t stream);
 
+/* The FFN of one token in two launches (the decoder's batch-1 path; no
+ * single counterpart in the reference, which runs FFN::forward,
+ * src/transformer.cpp:373-406, as separate GEMVs and elementwise ops):
+ *
+ * mth_oil4_gemv_swiglu: the gate and up projections of one OIL4 weight of
+ * 2F rows (gate rows first, then up; per-128 codebooks as mth_oil4_gemv with
+ * cb_block 128) and the SwiGLU in the same launch: act[F] = silu(g) * u,
+ * bit-identical to mth_oil4_gemv over the 2F rows followed by mth_silu_mul,
+ * and amax[F / 8] = max |act| over rows 8t..8t+7.  F % 8 == 0, K % 1024 ==
+ * 0, K <= 4096, 16-byte aligned packed / codebooks / x.
+ *
+ * mth_i2s_gemv_act: y = the I2_S GEMV of quantize_per_token(act) (the
+ * quantisation done inside the launch), bit-identical to
+ * mth_quantize_per_token followed by mth_i2s_gemv; amax as written by
+ * mth_oil4_gemv_swiglu (the maxima of |act| over groups of 8).  K % 64 ==
+ * 0, K <= 12288, 16-byte aligned packed. */
+int mth_oil4_gemv_swiglu(const uint8_t* packed, const uint16_t* codebooks, const float* x, float* act,
+                         float* amax, int64_t F, int64_t K, mth_stream_t stream);
+int mth_i2s_gemv_act(const uint8_t* packed, float w_scale, const float* act, const float* amax, float* y,
+                     int64_t M, int64_t K, mth_stream_t stream);
+
 /* oil::math::add / mul (src/math.cpp:251-258, :269-276). */
 int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);
 int mth_mul(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);

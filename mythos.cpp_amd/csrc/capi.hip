@@ -405,6 +405,30 @@ int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_sca
                         "mth_silu_mul_quant");
 }
 
+int mth_oil4_gemv_swiglu(const uint8_t* packed, const uint16_t* codebooks, const float* x, float* act,
+                         float* amax, int64_t F, int64_t K, mth_stream_t stream) {
+    REQUIRE(packed && codebooks && x && act && amax, "mth_oil4_gemv_swiglu: null pointer");
+    REQUIRE(mth::oil4_swiglu_supported(packed, codebooks, x, F, K),
+            "mth_oil4_gemv_swiglu: F=%lld K=%lld not supported (F %% 8 == 0, K %% 1024 == 0, K <= 4096, "
+            "16-byte aligned packed/codebooks/x)",
+            (long long)F, (long long)K);
+    return check_launch(mth::launch_oil4_swiglu(packed, codebooks, x, mth::NormScale{}, act, amax, F, K, S(stream)),
+                        "mth_oil4_gemv_swiglu");
+}
+
+int mth_i2s_gemv_act(const uint8_t* packed, float w_scale, const float* act, const float* amax, float* y,
+                     int64_t M, int64_t K, mth_stream_t stream) {
+    REQUIRE(packed && act && amax && y, "mth_i2s_gemv_act: null pointer");
+    REQUIRE(M > 0 && K > 0 && M < kMaxDim, "mth_i2s_gemv_act: bad sizes M=%lld K=%lld", (long long)M,
+            (long long)K);
+    REQUIRE(mth::i2s_swiglu_supported(packed, M, K),
+            "mth_i2s_gemv_act: K=%lld not supported (K %% 64 == 0, K <= 12288, 16-byte aligned packed)",
+            (long long)K);
+    return check_launch(mth::launch_i2s_act(act, amax, packed, w_scale, y, M, K, mth::ResidOut{}, nullptr,
+                                            S(stream)),
+                        "mth_i2s_gemv_act");
+}
+
 int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream) {
     REQUIRE(a && b && c, "mth_add: null pointer");
     REQUIRE(n > 0 && n < kMaxDim, "mth_add: bad size");

@@ -223,6 +223,23 @@ hipError_t enqueue_step_split_norm(const mth_decoder* d, hipStream_t s) {
         ro.gamma = L.ffn_norm;
         ro.ssp = d->ssp2;
         TRY(mth::launch_oil8_gemv_resid(mth::Oil8Seg{L.wo, L.cbo, nullptr, H}, d->att, QD, ro, &ns_ffn.nparts, s));
+        if (gate_up_fused(d, L) && mth::oil4_swiglu_supported(L.wgate, L.cbgate, d->h, F, H) &&
+            d->c.cb_block == 128 && mth::i2s_swiglu_supported(L.wdown, H, F)) {
+            // the SwiGLU in the gate/up epilogue (act in gu[0, F), the
+            // maxima of |act| per 8 in gu[F, F + F / 8)), the quantisation
+            // inside the down projection
+            TRY(mth::launch_oil4_swiglu(L.wgate, L.cbgate, d->h, ns_ffn, d->gu, d->gu + F, F, H, s));
+            ro.ssp = d->ssp;
+            if (!last) {
+                ro.gamma = d->layers[(size_t)l + 1].attn_norm;
+                TRY(mth::launch_i2s_act(d->gu, d->gu + F, L.wdown, L.down_scale, nullptr, H, F, ro,
+                                        &ns_attn.nparts, s));
+            } else {
+                TRY(mth::launch_i2s_act(d->gu, d->gu + F, L.wdown, L.down_scale, d->t, H, F, mth::ResidOut{},
+                                        nullptr, s));
+            }
+            continue;
+        }
         if (gate_up_fused(d, L)) {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
         } else {

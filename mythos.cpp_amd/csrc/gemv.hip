@@ -384,22 +384,48 @@ struct Oil4V2Lds {
     static constexpr int bytes = part + NW * 16 * 4;
 };
 
-template <int NW, int NPH, bool SHARED>
-__global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, const uint16_t* cbs,
+// PAIR: the SwiGLU epilogue of the fused gate/up projection (decode batch
+// 1).  Weight rows [0, F) are the gate, [F, 2F) the up projection (M = 2F,
+// F % 8 == 0, grid F / 8); workgroup t computes gate rows 8t..8t+7 as tile
+// rows 0-7 and the matching up rows as tile rows 8-15, then writes
+//   act[i] = silu(g_i * ni) * (u_i * ni),  amax[t] = max over its 8 |act|,
+// ni: the RMSNorm's 1 / rms (NormScale) with norm_scale<16>'s summation
+// order (16 waves of 64 threads, partials i = thread, thread + 1024, ...,
+// wave sums, waves in order), g_i and u_i summed as the plain output is:
+// act is bit-identical to silu_mul_quant_k's SwiGLU of that output.
+struct SwigluTile {
+    NormScale ns;
+    float* act;
+    float* amax;
+    int F;
+};
+
+template <int NW, int NPH, bool SHARED, bool PAIR = false>
+__global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2(const uint8_t* nib, const uint16_t* cbs,
                                                         const float* __restrict__ x, float* __restrict__ y,
-                                                        int M, int K) {
+                                                        int M, int K, SwigluTile sw = SwigluTile{}) {
     using L = Oil4V2Lds<NW, NPH, SHARED>;
     constexpr int KW = L::KW;
     __shared__ __align__(16) uint8_t lds[L::bytes];
+    __shared__ double nred[PAIR ? 16 : 1];
     float* part = (float*)(lds + L::part);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
     const int row0 = blockIdx.x * 16;
     const int k0 = wave * KW;
 
-    // x first, then (once every wave of the workgroup has issued it) the
-    // weight streams: the CU returns loads in issue order.
+    // x first (and the norm's partial sums), then (once every wave of the
+    // workgroup has issued them) the weight streams: the CU returns loads in
+    // issue order.
     const bool xl = lane * 16 < KW;
+    constexpr int VW = PAIR ? (16 + NW - 1) / NW : 1;  // norm_scale<16> waves taken by this wave
+    double np1[VW];
+    if (PAIR && sw.ns.ssp) {
+        const int last = sw.ns.nparts - 1;
+#pragma unroll
+        for (int i = 0; i < VW; ++i)
+            np1[i] = last >= 0 ? sw.ns.ssp[min((wave + i * NW) * 64 + lane, last)] : 0.0;
+    }
     float4 xq[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) xq[i] = ldf4(x + k0 + (xl ? lane * 16 : 0) + 4 * i);
@@ -408,9 +434,24 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
     __builtin_amdgcn_sched_barrier(0);
 
     Oil4TileLoads<NPH, SHARED> w;
-    w.issue(nib, cbs, row0, M, K, k0, lane);
+    if (PAIR)
+        w.issue_rows(nib, cbs, blockIdx.x * 8, sw.F + blockIdx.x * 8, M, K, k0, lane);
+    else
+        w.issue(nib, cbs, row0, M, K, k0, lane);
     CbPlanes shared_planes;
     if (SHARED) shared_planes = cb_planes(ld16(cbs), ld16(cbs + 8));
+    // (PAIR) norm_scale<16>'s wave sums of this wave's virtual waves, before
+    // the x conversion, so that the partials' registers are free at its peak
+    if (PAIR && sw.ns.ssp) {
+#pragma unroll
+        for (int i = 0; i < VW; ++i) {
+            const int vw = wave + i * NW, vt = vw * 64 + lane;
+            double t = vt < sw.ns.nparts ? np1[i] : 0.0;
+            for (int k = vt + 1024; k < sw.ns.nparts; k += 1024) t += sw.ns.ssp[k];
+            t = wave_sum_dbl(t);
+            if (lane == 0 && vw < 16) nred[vw] = t;
+        }
+    }
 
     // ---- x slice -> power-of-two scale -> FP16 hi/lo B fragments --------
     // lane l holds columns 16l .. 16l+15 = phase l/16, group (l%16)/4,
@@ -476,6 +517,32 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_v2(const uint8_t* nib, cons
         if (j == 0) part[wave * 16 + 4 * q + i] = ldexpf(s, -sh);
     }
     __syncthreads();
+    if (PAIR) {
+        if (tid < 8) {
+            float g = part[tid], u = part[8 + tid];
+#pragma unroll
+            for (int w2 = 1; w2 < NW; ++w2) {
+                g += part[w2 * 16 + tid];
+                u += part[w2 * 16 + 8 + tid];
+            }
+            if (sw.ns.ssp) {
+                double t = 0.0;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) t += nred[v];
+                const float ni = (float)(1.0 / sqrt(t / (double)sw.ns.dim + (double)sw.ns.eps));
+                g *= ni;
+                u *= ni;
+            }
+            const float a = silu1(g) * u;
+            sw.act[blockIdx.x * 8 + tid] = a;
+            float m = fabsf(a);
+            m = fmaxf(m, __shfl_xor(m, 4, 8));
+            m = fmaxf(m, __shfl_xor(m, 2, 8));
+            m = fmaxf(m, __shfl_xor(m, 1, 8));
+            if (tid == 0) sw.amax[blockIdx.x] = m;
+        }
+        return;
+    }
     if (tid < 16 && row0 + tid < M) {
         float sum = part[tid];
 #pragma unroll
@@ -673,6 +740,30 @@ void run_oil4_mfma(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, co
 }
 
 }  // namespace
+
+bool oil4_swiglu_supported(const uint8_t* nib, const uint16_t* cbs, const float* x, int64_t F, int64_t K) {
+    // the K range where launch_oil4_gemv runs oil4_gemv_v2 with 4 phases
+    return F > 0 && F % 8 == 0 && 2 * F < (1ll << 31) && K % 1024 == 0 && K >= 1024 && K <= 4096 &&
+           aligned16(nib) && aligned16(cbs) && aligned16(x);
+}
+
+hipError_t launch_oil4_swiglu(const uint8_t* nib, const uint16_t* cbs, const float* x, const NormScale& ns,
+                              float* act, float* amax, int64_t F, int64_t K, hipStream_t s) {
+    if (!oil4_swiglu_supported(nib, cbs, x, F, K)) return hipErrorInvalidValue;
+    const SwigluTile sw{ns, act, amax, (int)F};
+    const int grid = (int)(F / 8);
+    switch (K / 1024) {
+#define MTH_SW_CASE(NW)                                                                                     \
+    case NW:                                                                                                \
+        oil4_gemv_v2<NW, 4, false, true><<<grid, NW * 64, 0, s>>>(nib, cbs, x, nullptr, (int)(2 * F),        \
+                                                                  (int)K, sw);                              \
+        break;
+        MTH_SW_CASE(1) MTH_SW_CASE(2) MTH_SW_CASE(3) MTH_SW_CASE(4)
+#undef MTH_SW_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x, float* y,
                             int64_t M, int64_t K, int64_t batch, hipStream_t s) {

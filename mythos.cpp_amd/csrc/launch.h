@@ -41,6 +41,13 @@ hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float*
 // ---- OIL4 (gemv.hip) ----------------------------------------------------
 // cb_block > 0: codebooks[(m*(K/cb_block) + k/cb_block)*16 + i] (fp16 bits);
 // cb_block == 0: one shared 16-entry codebook.
+// Batch 1, per-128 codebooks: the fused gate/up projection (rows [0, F) the
+// gate, [F, 2F) the up projection of one weight) with the SwiGLU in its
+// epilogue: act[F] = silu(g * ni) * (u * ni) (ni from ns; ns.ssp null: 1)
+// and amax[F / 8] = max |act| over rows 8t..8t+7.  K % 1024 == 0, K <= 4096.
+bool oil4_swiglu_supported(const uint8_t* nib, const uint16_t* cbs, const float* x, int64_t F, int64_t K);
+hipError_t launch_oil4_swiglu(const uint8_t* nib, const uint16_t* cbs, const float* x, const NormScale& ns,
+                              float* act, float* amax, int64_t F, int64_t K, hipStream_t s);
 hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block,
                             const float* x, float* y, int64_t M, int64_t K, int64_t batch,
                             hipStream_t s);
@@ -104,6 +111,11 @@ hipError_t launch_i2s_gemv_resid(const uint8_t* packed, float w_scale, const int
 bool i2s_swiglu_supported(const uint8_t* packed, int64_t M, int64_t K);
 hipError_t launch_i2s_swiglu(const float* g, const float* u, const NormScale& ns, const uint8_t* packed, float w_scale,
                              float* y, int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s);
+// Batch 1: as launch_i2s_swiglu with the SwiGLU already applied: act[K] =
+// silu(g * ni) * (u * ni) and amax[K / 8] the maxima of |act| over groups of
+// 8 (launch_oil4_swiglu's outputs); quantisation and product as there.
+hipError_t launch_i2s_act(const float* act, const float* amax, const uint8_t* packed, float w_scale, float* y,
+                          int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s);
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 // ws: null (one wave per output) or i2s_gemm_workspace_bytes(M, N, K) bytes of

@@ -182,15 +182,20 @@ struct Oil4TileLoads {
 
     __device__ __forceinline__ void issue(const uint8_t* nib, const uint16_t* cbs, int row0, int M, int K, int k0,
                                           int lane) {
+        issue_rows(nib, cbs, row0, row0 + 8, M, K, k0, lane);
+    }
+    // Tile rows 0-7 are weight rows rowA.., tile rows 8-15 rows rowB.. (rows
+    // past M - 1 read row M - 1).
+    __device__ __forceinline__ void issue_rows(const uint8_t* nib, const uint16_t* cbs, int rowA, int rowB, int M,
+                                               int K, int k0, int lane) {
         const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
         const int nbr = K >> 7;  // codebook blocks per row
-        const uint8_t* nx = nib + (int64_t)min(row0 + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
-        const uint8_t* ny = nib + (int64_t)min(row0 + 8 + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
+        const uint8_t* nx = nib + (int64_t)min(rowA + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
+        const uint8_t* ny = nib + (int64_t)min(rowB + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
         // codebook loads: lane l -> row 8u + l/8, 16-byte piece l % 8 of the
         // 4 blocks of a phase pair
-        const uint16_t* cl0 = cbs + ((int64_t)min(row0 + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
-        const uint16_t* cl1 =
-            cbs + ((int64_t)min(row0 + 8 + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
+        const uint16_t* cl0 = cbs + ((int64_t)min(rowA + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
+        const uint16_t* cl1 = cbs + ((int64_t)min(rowB + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
 #pragma unroll
         for (int p = 0; p < NPH; ++p) {
             if (!SHARED && p % 2 == 0) {

@@ -250,7 +250,10 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
 // to res.ssp, which must not be ns.ssp (other workgroups may still read it).
 constexpr int kSwT = 1024, kSwQ = 12;  // as silu_mul_quant_k (kSQT, kSQ)
 
-template <int NSEG>
+// PRE: g holds the SwiGLU output a itself and u the maxima of |a| over
+// groups of 8 columns (K / 8 of them, oil4_gemv_v2's SwiGLU epilogue); the
+// norm and the SwiGLU are skipped and max|a| is the maximum of those maxima.
+template <int NSEG, bool PRE = false>
 __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g, const float* __restrict__ u,
                                                      NormScale ns, const uint8_t* packed, float w_scale,
                                                      float* __restrict__ y, int M, int K, ResidOut res) {
@@ -264,13 +267,20 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
     const int bpr = K >> 2, nseg = bpr >> 4;
 
     double npart[kNormBatch];
-    if (ns.ssp) norm_issue(ns, 0, tid, kSwT, npart);
+    float mp[2];  // PRE: maxima of groups tid, tid + 1024 (K / 8 <= 2 * kSwT)
+    if (PRE) {
+        const int last = (K >> 3) - 1;
+        mp[0] = u[min(tid, last)];
+        mp[1] = u[min(tid + kSwT, last)];
+    } else if (ns.ssp) {
+        norm_issue(ns, 0, tid, kSwT, npart);
+    }
     float gv[kSwQ], uv[kSwQ];
 #pragma unroll
     for (int j = 0; j < kSwQ; ++j) {
         const int i = tid + j * kSwT;
         gv[j] = i < K ? g[i] : 0.0f;
-        uv[j] = i < K ? u[i] : 0.0f;
+        if (!PRE) uv[j] = i < K ? u[i] : 0.0f;
     }
     uint4 w[NSEG];
     __builtin_amdgcn_sched_barrier(0);
@@ -279,7 +289,7 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
         w[s] = ld_stream(packed + (int64_t)min(row, M - 1) * bpr + (int64_t)min(lane + 64 * s, nseg - 1) * 16);
     __builtin_amdgcn_sched_barrier(0);
 
-    if (ns.ssp) {  // norm_scale<16>: per-thread sums, wave sums, waves in order
+    if (!PRE && ns.ssp) {  // norm_scale<16>: per-thread sums, wave sums, waves in order
         double sum = wave_sum_dbl(norm_finish(ns, 0, tid, kSwT, npart));
         if (lane == 0) nred[wave] = sum;
         __syncthreads();
@@ -294,10 +304,15 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
         }
     }
     float m = 0.0f;
+    if (PRE) {
+        if (tid < (K >> 3)) m = fmaxf(m, mp[0]);
+        if (tid + kSwT < (K >> 3)) m = fmaxf(m, mp[1]);
+    } else {
 #pragma unroll
-    for (int j = 0; j < kSwQ; ++j) {
-        gv[j] = silu1(gv[j]) * uv[j];
-        m = fmaxf(m, fabsf(gv[j]));
+        for (int j = 0; j < kSwQ; ++j) {
+            gv[j] = silu1(gv[j]) * uv[j];
+            m = fmaxf(m, fabsf(gv[j]));
+        }
     }
     m = wave_max(m);
     if (lane == 0) red[wave] = m;
@@ -1046,6 +1061,23 @@ hipError_t launch_i2s_swiglu(const float* g, const float* u, const NormScale& ns
         i2s_swiglu_k<2><<<grid, kSwT, lds, s>>>(g, u, ns, packed, w_scale, y, (int)M, (int)K, ro);
     else
         i2s_swiglu_k<3><<<grid, kSwT, lds, s>>>(g, u, ns, packed, w_scale, y, (int)M, (int)K, ro);
+    if (nparts) *nparts = grid;
+    return hipGetLastError();
+}
+
+hipError_t launch_i2s_act(const float* act, const float* amax, const uint8_t* packed, float w_scale, float* y,
+                          int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s) {
+    if (!i2s_swiglu_supported(packed, M, K)) return hipErrorInvalidValue;
+    const int64_t nseg = K / 64;
+    const int grid = ceil_div(M, kSwT / 64);
+    const size_t lds = (size_t)K;
+    const NormScale none{};
+    if (nseg <= 64)
+        i2s_swiglu_k<1, true><<<grid, kSwT, lds, s>>>(act, amax, none, packed, w_scale, y, (int)M, (int)K, ro);
+    else if (nseg <= 128)
+        i2s_swiglu_k<2, true><<<grid, kSwT, lds, s>>>(act, amax, none, packed, w_scale, y, (int)M, (int)K, ro);
+    else
+        i2s_swiglu_k<3, true><<<grid, kSwT, lds, s>>>(act, amax, none, packed, w_scale, y, (int)M, (int)K, ro);
     if (nparts) *nparts = grid;
     return hipGetLastError();
 }

@@ -27,7 +27,8 @@ EXPORTS = (
     "mth_quantize_per_token", "mth_dequantize_per_tensor",
     "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
     "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
-    "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_silu_mul_quant", "mth_add", "mth_mul",
+    "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_silu_mul_quant",
+    "mth_oil4_gemv_swiglu", "mth_i2s_gemv_act", "mth_add", "mth_mul",
     "mth_softmax", "mth_softmax_axis", "mth_axpby", "mth_gemv_f32", "mth_relu", "mth_gelu", "mth_scale",
     "mth_layer_norm",
     "mth_rope_tables", "mth_rope_kv", "mth_attention_decode", "mth_argmax",
@@ -82,6 +83,8 @@ _SIG = {
     "mth_silu": [VP, VP, I64, VP],
     "mth_silu_mul": [VP, VP, VP, I64, I64, I64, I64, VP],
     "mth_silu_mul_quant": [VP, VP, VP, VP, I64, I64, I64, I64, VP],
+    "mth_oil4_gemv_swiglu": [VP, VP, VP, VP, VP, I64, I64, VP],
+    "mth_i2s_gemv_act": [VP, F32, VP, VP, VP, I64, I64, VP],
     "mth_add": [VP, VP, VP, I64, VP],
     "mth_mul": [VP, VP, VP, I64, VP],
     "mth_softmax": [VP, VP, I64, I64, VP],
@@ -301,6 +304,24 @@ def silu_mul_quant(g, u, q, inv_scale, rows, n, gstride=None, ustride=None, stre
     _check(_lib.mth_silu_mul_quant(_ptr(g, t.float32, (rows - 1) * gs + n, "g"),
                                    _ptr(u, t.float32, (rows - 1) * us + n, "u"), _ptr(q, t.int8, rows * n, "q"),
                                    _ptr(inv_scale, t.float32, rows, "inv_scale"), rows, n, gs, us, _stream(stream)))
+
+
+def oil4_gemv_swiglu(packed, codebooks, x, act, amax, F, K, stream=None):
+    """Gate/up projections of one OIL4 weight of 2F rows (per-128 codebooks)
+    and the SwiGLU: act[F] = silu(g) * u, amax[F // 8] = max |act| per 8."""
+    t = _torch()
+    _check(_lib.mth_oil4_gemv_swiglu(_ptr(packed, t.uint8, 2 * F * K // 2, "packed"),
+                                     _ptr(codebooks, t.int16, 2 * F * (K // 128) * 16, "codebooks"),
+                                     _ptr(x, t.float32, K, "x"), _ptr(act, t.float32, F, "act"),
+                                     _ptr(amax, t.float32, F // 8, "amax"), F, K, _stream(stream)))
+
+
+def i2s_gemv_act(packed, w_scale, act, amax, y, M, K, stream=None):
+    """I2_S GEMV of quantize_per_token(act), amax as from oil4_gemv_swiglu."""
+    t = _torch()
+    _check(_lib.mth_i2s_gemv_act(_ptr(packed, t.uint8, M * K // 4, "packed"), float(w_scale),
+                                 _ptr(act, t.float32, K, "act"), _ptr(amax, t.float32, K // 8, "amax"),
+                                 _ptr(y, t.float32, M, "y"), M, K, _stream(stream)))
 
 
 def add(a, b, c, n, stream=None):

@@ -32,6 +32,11 @@ SMALL = dict(vocab=1000, hidden=256, layers=2, heads=2, kv_heads=2, head_dim=128
 # batches >= 2 (OIL4 needs K >= 512), gate and up as one launch over 2*ffn rows
 MID = dict(vocab=1000, hidden=512, layers=2, heads=4, kv_heads=4, head_dim=128, ffn=1024, max_seq=20,
            cb_block=128, eps=1e-5, theta=10000.0)
+# hidden 1024 / ffn 2048: at batch 1 the gate/up projection runs with the
+# SwiGLU in its epilogue (hidden % 1024 == 0) and the down projection
+# quantises the activations it reads
+WIDE = dict(vocab=1000, hidden=1024, layers=2, heads=8, kv_heads=8, head_dim=128, ffn=2048, max_seq=12,
+            cb_block=128, eps=1e-5, theta=10000.0)
 TOL = 1e-4
 THREADS = max(1, min(16, os.cpu_count() or 1))
 
@@ -339,6 +344,29 @@ def test_mid_b1_split_norm(kv, mid, oracle):
     cfg, model = mid
     P = 6
     prompts = synth.decoder_prompts(cfg, 1, P, config=79)
+    dec = make(cfg, model, 1, kv)
+    dec.start(prompts)
+    orc = oracle.decoder(oracle_cfg(cfg, kv), model)
+    kc, vc = orc.new_cache()
+    for pos in range(P):
+        dec.step(1)
+        err = rel(dec.logits()[0], orc.step(kc, vc, pos, int(prompts[0, pos]), threads=THREADS))
+        assert err < TOL, (pos, err)
+    dec.close()
+
+
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_wide_b1_swiglu_epilogue(kv, oracle):
+    """Batch 1 with real ternary weights: the SwiGLU computed in the gate/up
+    projection's epilogue (rows paired gate/up per workgroup) and quantised
+    inside the down projection, against the oracle's teacher-forced logits,
+    graph-replayed steps.  (Both kernels are bit-exact against the unfused
+    chain in test_gpu_gemv.py, at config 5's shapes too.)"""
+    print(f"decoder wide b=1 kv={kv}", flush=True)
+    cfg = synth.decoder_config(**WIDE)
+    model = synth.decoder_model(cfg, config=81, random_gamma=True)
+    P = 6
+    prompts = synth.decoder_prompts(cfg, 1, P, config=82)
     dec = make(cfg, model, 1, kv)
     dec.start(prompts)
     orc = oracle.decoder(oracle_cfg(cfg, kv), model)

@@ -262,6 +262,74 @@ def test_oil4_gemm_reference_indexing(M, N, K, oracle, mth, dev):
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * scale), np.abs(got - ref).max()
 
 
+# ------------------------------------------ FFN in two launches (batch 1) --
+@pytest.mark.parametrize("F,K", [
+    (11008, 4096),   # config 5's gate/up (four-wave workgroups)
+    (2048, 1024),    # one wave per workgroup
+    (64, 3072),      # three waves: norm-sum waves not a multiple of them
+    (8, 4096),       # one workgroup
+])
+def test_oil4_gemv_swiglu_bit_exact(F, K, oracle, mth, dev):
+    """Gate/up GEMV with the SwiGLU in its epilogue: act bit-identical to
+    mth_oil4_gemv over the 2F rows followed by mth_silu_mul; amax the exact
+    maxima of |act| over groups of 8; the GEMV itself against the oracle."""
+    import torch
+    print(f"oil4_gemv_swiglu F={F} K={K}", flush=True)
+    packed, cbs, x = synth.oil4(2 * F, K, 1, 128)
+    p, c, xd = to_dev(packed, dev), to_dev(cbs, dev), to_dev(x, dev)
+    act, amax = empty(F, torch.float32, dev), empty(F // 8, torch.float32, dev)
+    mth.oil4_gemv_swiglu(p, c, xd, act, amax, F, K)
+    y, ref_act = empty(2 * F, torch.float32, dev), empty(F, torch.float32, dev)
+    mth.oil4_gemv(p, c, 128, xd, y, 2 * F, K)
+    mth.silu_mul(y[:F], y[F:], ref_act, 1, F)
+    torch.cuda.synchronize()
+    got, want = act.cpu().numpy(), ref_act.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(amax.cpu().numpy(), np.abs(want).reshape(-1, 8).max(1))
+    ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, 2 * F, K, 1, 128, threads=8)
+    W = synth.dequant_oil4(packed, cbs, 2 * F, K, 128)
+    absw = np.abs(W).astype(np.float64) @ np.abs(x.astype(np.float64)).T
+    fp32_close(y.cpu().numpy().reshape(1, 2 * F), ref, absw.T, 1e-5, "oil4_gemv (2F rows)")
+
+
+@pytest.mark.parametrize("M,K", [
+    (4096, 11008),   # config 5's down projection
+    (4096, 512),
+    (100, 64),       # one segment
+    (33, 12288),     # the largest K, rows not a multiple of 16
+])
+def test_i2s_gemv_act_bit_exact(M, K, oracle, mth, dev):
+    """The I2_S GEMV of quantize_per_token(act) with the quantisation inside
+    the launch (max|act| from the per-8 maxima): bit-exact against the
+    oracle's quantize_per_token + i2s_gemv; an all-zero act gives 0."""
+    import torch
+    print(f"i2s_gemv_act M={M} K={K}", flush=True)
+    g = np.random.default_rng(M + K)
+    packed = g.integers(0, 256, (M, K // 4), dtype=np.uint8)  # all four codes
+    for act in (g.normal(0, 1, K).astype(np.float32), np.zeros(K, np.float32)):
+        amax = np.abs(act).reshape(-1, 8).max(1)
+        y = empty(M, torch.float32, dev)
+        mth.i2s_gemv_act(to_dev(packed, dev), 0.0159577, to_dev(act, dev), to_dev(amax, dev), y, M, K)
+        torch.cuda.synchronize()
+        ref = oracle.i2s_gemv_f32(packed.ravel(), 0.0159577, act.reshape(1, K), M, K, 1, threads=8)
+        assert np.array_equal(y.cpu().numpy().reshape(1, M), ref)
+
+
+def test_ffn_building_blocks_reject_shapes(mth, dev):
+    import torch
+    p = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    c = torch.zeros(1 << 14, dtype=torch.int16, device=dev)
+    f = torch.zeros(1 << 14, dtype=torch.float32, device=dev)
+    with pytest.raises(mth.MythosError):
+        mth.oil4_gemv_swiglu(p, c, f, f, f, 12, 1024)      # F % 8 != 0
+    with pytest.raises(mth.MythosError):
+        mth.oil4_gemv_swiglu(p, c, f, f, f, 8, 1536)      # K % 1024 != 0
+    with pytest.raises(mth.MythosError):
+        mth.oil4_gemv_swiglu(p, c, f, f, f, 8, 8192)      # K > 4096
+    with pytest.raises(mth.MythosError):
+        mth.i2s_gemv_act(p, 1.0, f, f, f, 8, 1000)         # K % 64 != 0
+
+
 # ------------------------------------------------------------- int8/I2_S --
 @pytest.mark.parametrize("rows,cols", [(1, 4096), (16, 11008), (3, 5), (2, 1)])
 def test_quantize_per_token_bit_exact(rows, cols, oracle, mth, dev):
