@@ -230,10 +230,11 @@ __device__ __forceinline__ double norm_finish(const NormScale& ns, int t, int i0
 }
 // 1 / sqrt(sum / dim + eps) of token t, computed by a whole workgroup of
 // NW waves (red: NW doubles of LDS); every thread gets it.
+// norm_scale_issued: the same from partials this thread loaded with
+// norm_issue(ns, t, threadIdx.x, NW * 64, v) earlier (ahead of other loads).
 template <int NW>
-__device__ __forceinline__ float norm_scale(const NormScale& ns, int t, double* red) {
-    double v[kNormBatch];
-    norm_issue(ns, t, threadIdx.x, NW * 64, v);
+__device__ __forceinline__ float norm_scale_issued(const NormScale& ns, int t, const double (&v)[kNormBatch],
+                                                   double* red) {
     double s = wave_sum_dbl(norm_finish(ns, t, threadIdx.x, NW * 64, v));
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -242,6 +243,12 @@ __device__ __forceinline__ float norm_scale(const NormScale& ns, int t, double* 
 #pragma unroll
     for (int w = 0; w < NW; ++w) s += red[w];
     return (float)(1.0 / sqrt(s / (double)ns.dim + (double)ns.eps));
+}
+template <int NW>
+__device__ __forceinline__ float norm_scale(const NormScale& ns, int t, double* red) {
+    double v[kNormBatch];
+    norm_issue(ns, t, threadIdx.x, NW * 64, v);
+    return norm_scale_issued<NW>(ns, t, v, red);
 }
 
 // silu(g) = g / (1 + e^-g), in FP32 with expf and an IEEE division (the

@@ -306,11 +306,29 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
     }
     if (fold1) return enqueue_step_split_norm(d, s);
     const Slices none{nullptr, 0, 0, 0, 1.0f, nullptr};
+    // Batches split the RMSNorms too, but the O and down projections leave
+    // split-K partial sums, so the residual add runs as its own wide launch
+    // (resid_split: x += partials, x * gamma, partial sums of squares); the
+    // Q/K/V and gate/up GEMVs take x * gamma and the attention and the SwiGLU
+    // apply 1 / rms.  The embedding writes the first layer's.
+    bool splitb = fold && mth::resid_split_parts(H) * B <= H / 4 + 2 &&
+                  ((((uintptr_t)d->x | (uintptr_t)d->h) & 15u) == 0);
+    for (int64_t l = 0; splitb && l < c.layers; l++) {
+        const mth_decoder_layer& L = d->layers[(size_t)l];
+        splitb = ((((uintptr_t)L.attn_norm | (uintptr_t)L.ffn_norm) & 15u) == 0) &&
+                 mth::resid_split_supported(d->x, none, L.attn_norm, d->h, B, H);
+    }
+    mth::NormScale ns_attn{}, ns_ffn{};
+    if (splitb) {
+        ns_attn = mth::NormScale{d->ssp, 1, (float)H, c.eps};
+        ns_ffn = mth::NormScale{d->ssp2, 0, (float)H, c.eps};
+    }
     const int64_t tap_floats = mth_decoder_tap_floats(d);
     auto tap_copy = [&](float* dst, const void* src, size_t bytes) {
         return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
     };
-    TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, B, (int)H, (int)c.vocab, s));
+    TRY(mth::launch_embed(d->g.emb, d->hist, d->step, (int)d->hist_stride, d->x, B, (int)H, (int)c.vocab, s,
+                          splitb ? mth::ResidOut{d->x, d->layers[0].attn_norm, d->h, d->ssp} : mth::ResidOut{}));
     Slices resid = none;  // the previous layer's FFN output, added by the next norm
     for (int64_t l = 0; l < c.layers; l++) {
         const mth_decoder_layer& L = d->layers[(size_t)l];
@@ -324,7 +342,10 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         float* tp_inv = tp ? tp_aq + B * F / 4 : nullptr;
         float* tp_down = tp ? tp_inv + B : nullptr;
         // residual of the previous layer's FFN folded into this norm
-        TRY(mth::launch_rms_norm_slices(d->x, resid, L.attn_norm, d->h, B, H, c.eps, s));
+        if (!splitb)
+            TRY(mth::launch_rms_norm_slices(d->x, resid, L.attn_norm, d->h, B, H, c.eps, s));
+        else if (l > 0)
+            TRY(mth::launch_resid_split(d->x, resid, L.attn_norm, d->h, d->ssp, B, H, &ns_attn.nparts, s));
         // Q, K, V, then RoPE + KV append + attention
         Slices sq = plain_slices(d->q, QD), sk = plain_slices(d->k, KD), sv = plain_slices(d->v, KD);
         const mth::Oil8Seg qkv_seg[3] = {{L.wq, L.cbq, d->q, QD}, {L.wk, L.cbk, d->k, KD}, {L.wv, L.cbv, d->v, KD}};
@@ -335,7 +356,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         } else {
             TRY(qkv(d, L, d->h, d->q, d->k, d->v, B, s));
         }
-        TRY(mth::launch_rope_attention_slices(sq, sk, sv, mth::NormScale{}, d->rope_cos, d->rope_sin, kc, vc,
+        TRY(mth::launch_rope_attention_slices(sq, sk, sv, ns_attn, d->rope_cos, d->rope_sin, kc, vc,
                                               c.kv_dtype == 1, d->att,
                                               d->step, B, (int)c.heads, (int)c.kv_heads, (int)c.head_dim,
                                               (int)c.max_seq, s));
@@ -348,7 +369,10 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
         } else {
             TRY(oil8(d, L.wo, L.cbo, d->att, d->t, H, QD, s));
         }
-        TRY(mth::launch_rms_norm_slices(d->x, so, L.ffn_norm, d->h, B, H, c.eps, s));
+        if (splitb)
+            TRY(mth::launch_resid_split(d->x, so, L.ffn_norm, d->h, d->ssp2, B, H, &ns_ffn.nparts, s));
+        else
+            TRY(mth::launch_rms_norm_slices(d->x, so, L.ffn_norm, d->h, B, H, c.eps, s));
         if (tp) TRY(tap_copy(tp, d->x, (size_t)(B * H) * 4));
         const bool fused = gate_up_fused(d, L);
         // gate/up, then silu(gate)*up quantised to int8 per token (once, not
@@ -360,7 +384,7 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
             // to read the gate/up slices as fast as the reduction kernel)
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, 2 * F, H, s));
             if (tp) TRY(tap_copy(tp_gu, d->gu, (size_t)(B * 2 * F) * 4));
-            TRY(mth::launch_silu_mul_quant_slices(sg, su, mth::NormScale{}, d->aq, d->a_inv, tp_act, B, F, s));
+            TRY(mth::launch_silu_mul_quant_slices(sg, su, ns_ffn, d->aq, d->a_inv, tp_act, B, F, s));
         } else {
             TRY(oil4(d, L.wgate, L.cbgate, d->h, d->gu, F, H, s));
             TRY(oil4(d, L.wup, L.cbup, d->h, d->gu + B * F, F, H, s));
@@ -370,7 +394,11 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
                 TRY(hipMemcpy2DAsync(tp_gu + F, (size_t)(2 * F) * 4, d->gu + B * F, (size_t)F * 4, (size_t)F * 4,
                                      (size_t)B, hipMemcpyDeviceToDevice, s));
             }
-            TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, tp_act, B, F, F, F, s));
+            if (splitb)
+                TRY(mth::launch_silu_mul_quant_slices(plain_slices(d->gu, F), plain_slices(d->gu + B * F, F), ns_ffn,
+                                                      d->aq, d->a_inv, tp_act, B, F, s));
+            else
+                TRY(mth::launch_silu_mul_quant(d->gu, d->gu + B * F, d->aq, d->a_inv, tp_act, B, F, F, F, s));
         }
         resid = plain_slices(d->t, H);
         if ((((uintptr_t)L.wdown | (uintptr_t)d->aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, B)) {

@@ -110,6 +110,41 @@ __global__ __launch_bounds__(kRN) void rms_norm_k(float* x, Slices t, const floa
     }
 }
 
+// The residual add of the split RMSNorm for a batch of rows (ResidOut,
+// common.h), as a launch of its own since the producers of t leave split-K
+// partial sums: x <- t + x (the sum of rms_norm_k), xg = x * gamma, and per
+// workgroup the sum of x^2 over its 4 * kRS columns (double, in rms_norm_k's
+// per-element order) in ssp[row][blockIdx.x].  The consumers apply the
+// 1 / rms (NormScale).  grid (ceil(dim / (4 kRS)), rows); dim % 4 == 0.
+constexpr int kRS = 64;
+__global__ __launch_bounds__(kRS) void resid_split_k(float* x, Slices t, const float* __restrict__ gamma, float* xg,
+                                                     double* ssp, int dim) {
+    __shared__ double red[kRS / 64];
+    const int r = blockIdx.y, i = (blockIdx.x * kRS + threadIdx.x) * 4;
+    double ss = 0.0;
+    if (i < dim) {
+        float* xr = x + (int64_t)r * dim + i;
+        float4 v = ldf4(xr);
+        const float4 g = ldf4(gamma + i);
+        if (t.n) {
+            const float4 a = slice_value4(t, r, i);
+            v = make_float4((a.x + v.x), (a.y + v.y), (a.z + v.z), (a.w + v.w));
+            *(float4*)xr = v;
+        }
+        *(float4*)(xg + (int64_t)r * dim + i) = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
+        ss = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+    ss = wave_sum_dbl(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < kRS / 64; ++w) tot += red[w];
+        ssp[(int64_t)r * gridDim.x + blockIdx.x] = tot;
+    }
+}
+
 // Generic-width variant (dim % 4 != 0 or unaligned rows).
 __global__ __launch_bounds__(kT) void rms_norm_any_k(float* x, Slices t, const float* __restrict__ gamma, float* y,
                                                      int64_t dim, float eps) {
@@ -590,6 +625,8 @@ __global__ __launch_bounds__(kSQT) void silu_mul_quant_k(Slices g, Slices u, Nor
     __shared__ float red[kSQT / 64];
     __shared__ double nred[kSQT / 64];
     const int r = blockIdx.x, tid = threadIdx.x;
+    double npart[kNormBatch];  // the norm's partial sums, loaded first
+    if (ns.ssp) norm_issue(ns, r, tid, kSQT, npart);
     float gv[kSQ], uv[kSQ];
     if (g.n == 1 && u.n == 1) {
         const float* gr = g.p + r * g.ts;
@@ -609,7 +646,7 @@ __global__ __launch_bounds__(kSQT) void silu_mul_quant_k(Slices g, Slices u, Nor
         }
     }
     if (ns.ssp) {
-        const float ni = norm_scale<kSQT / 64>(ns, r, nred);
+        const float ni = norm_scale_issued<kSQT / 64>(ns, r, npart, nred);
 #pragma unroll
         for (int j = 0; j < kSQ; ++j) {
             gv[j] *= ni;
@@ -816,6 +853,24 @@ hipError_t launch_rms_norm_slices(float* x, const Slices& t, const float* gamma,
         rms_norm_k<<<(unsigned)rows, kRN, 0, s>>>(x, t, gamma, y, (int)dim, eps);
     else
         rms_norm_any_k<<<(unsigned)rows, kT, 0, s>>>(x, t, gamma, y, dim, eps);
+    return hipGetLastError();
+}
+
+bool resid_split_supported(const float* x, const Slices& t, const float* gamma, const float* xg, int64_t rows,
+                           int64_t dim) {
+    const bool t_al = t.n == 0 || (al16(t.p) && t.ts % 4 == 0 && t.zs % 4 == 0);
+    return dim % 4 == 0 && dim < (1ll << 31) && rows >= 1 && rows <= 65535 && al16(x) && al16(gamma) && al16(xg) &&
+           t_al && t.n <= kMaxSlices;
+}
+
+int resid_split_parts(int64_t dim) { return (int)((dim + 4 * kRS - 1) / (4 * kRS)); }
+
+hipError_t launch_resid_split(float* x, const Slices& t, const float* gamma, float* xg, double* ssp, int64_t rows,
+                              int64_t dim, int* nparts, hipStream_t s) {
+    if (!resid_split_supported(x, t, gamma, xg, rows, dim)) return hipErrorInvalidValue;
+    const int np = resid_split_parts(dim);
+    resid_split_k<<<dim3((unsigned)np, (unsigned)rows), kRS, 0, s>>>(x, t, gamma, xg, ssp, (int)dim);
+    if (nparts) *nparts = np;
     return hipGetLastError();
 }
 

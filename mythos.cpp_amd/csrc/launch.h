@@ -145,7 +145,15 @@ hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* n
 // x <- t + x (when t), then y = rms_norm(x) * gamma per row of dim.
 hipError_t launch_rms_norm(float* x, const float* t, const float* gamma, float* y, int64_t rows, int64_t dim,
                            float eps, hipStream_t s);
-// The same with t read as Slices (t.n == 0: no residual add).
+// The residual add of the split RMSNorm for a batch (resid_split_k): x <-
+// t + x, xg = x * gamma, partial sums of x^2 in ssp[row][*nparts]
+// (resid_split_parts(dim) per row); the consumers apply 1 / rms (NormScale).
+bool resid_split_supported(const float* x, const Slices& t, const float* gamma, const float* xg, int64_t rows,
+                           int64_t dim);
+int resid_split_parts(int64_t dim);
+hipError_t launch_resid_split(float* x, const Slices& t, const float* gamma, float* xg, double* ssp, int64_t rows,
+                              int64_t dim, int* nparts, hipStream_t s);
+// launch_rms_norm with t read as Slices (t.n == 0: no residual add).
 hipError_t launch_rms_norm_slices(float* x, const Slices& t, const float* gamma, float* y, int64_t rows, int64_t dim,
                                   float eps, hipStream_t s);
 // y[r][i] = silu(g[r*gstride + i]) * u[r*ustride + i], i < n
