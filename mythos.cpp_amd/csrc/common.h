@@ -25,6 +25,31 @@ __device__ __forceinline__ int group_sum_i(int v) {
     for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
     return v;
 }
+// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of
+// a group gets its sum.  Within 16 lanes by DPP row rotations (VALU only,
+// no LDS round trip; the empty asm keeps each read out of partial-exec
+// code), beyond that by shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_ror_f(float v) {
+    int r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false);
+    asm volatile("" : "+v"(r));
+    return __int_as_float(r);
+}
+template <int N>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (N >= 16) {
+        v += dpp_ror_f<0x128>(v);  // row_ror:8
+        v += dpp_ror_f<0x124>(v);  // row_ror:4
+        v += dpp_ror_f<0x122>(v);  // row_ror:2
+        v += dpp_ror_f<0x121>(v);  // row_ror:1
+#pragma unroll
+        for (int o = 16; o < N; o <<= 1) v += __shfl_xor(v, o, MTH_WAVE);
+    } else {
+#pragma unroll
+        for (int o = N / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, N);
+    }
+    return v;
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MTH_WAVE));

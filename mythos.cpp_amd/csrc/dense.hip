@@ -456,14 +456,26 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         else
             slice_issue_all(q, row, h * D + tid, raw[0]);
     }
-    // cache rows: this thread's K row of the first tile, then its V rows
-    Raw kr0[D / 4];
-    const bool has0 = tid < nmem;
-    {
-        const KV* kr = kc + (crow + (has0 ? tid : 0)) * D;
+    // cache rows: K of the first KPRE rounds, then this thread's V rows.  A
+    // K row is read by KL lanes, 16 bytes each (row kr of a round of KRR
+    // rows, chunk kl), so that a load instruction covers whole rows.
+    constexpr int KE = 16 / (int)sizeof(KV);  // cache elements per 16-byte chunk
+    constexpr int KL = D / KE;                // lanes per K row
+    constexpr int KRR = kT / KL;              // K rows per round
+    constexpr int KPRE = 192 / KRR < 12 ? 192 / KRR : 12;  // rounds loaded up front (<= 192 rows)
+    const int kl = tid % KL, kr = tid / KL;
+    const KV* kchunk = kc + crow * D + kl * KE;
+    uint4 kpre[KPRE];
 #pragma unroll
-        for (int d = 0; d < D / 4; ++d) kr0[d] = kv_raw4(kr + 4 * d);
+    for (int i = 0; i < KPRE; ++i) {
+        const int t = i * KRR + kr;
+        kpre[i] = *(const uint4*)(kchunk + (int64_t)(t < nmem ? t : 0) * D);
     }
+    // every wave's K ahead of any wave's V (the CU returns loads in issue
+    // order): the scores wait for half the stream, not all of it
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     const KV* vcol = vc + crow * D + 4 * g;
     Raw vpre[VP];
 #pragma unroll
@@ -514,32 +526,47 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         kc[(crow + pos) * D + tid] = kv_store_value(ks[tid], KV{});
         vc[(crow + pos) * D + tid] = kv_store_value(vs[tid], KV{});
     }
-    auto dot_raw = [&](const Raw* kr) {
-        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    // scores: each lane's chunk against the same columns of q, summed over
+    // the row's KL lanes (butterfly: every lane of the group gets the sum)
+    float qv[KE];
 #pragma unroll
-        for (int d = 0; d < D / 4; ++d) {
-            const float4 k4 = kv_widen(kr[d]);
-            const float4 q4 = *(const float4*)(qs + 4 * d);
-            s0 = s0 + q4.x * k4.x;
-            s1 = s1 + q4.y * k4.y;
-            s2 = s2 + q4.z * k4.z;
-            s3 = s3 + q4.w * k4.w;
+    for (int e = 0; e < KE; ++e) qv[e] = qs[kl * KE + e];
+    auto score = [&](const uint4& w) {
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < KE; e += 2) {
+            float k0, k1;
+            if (sizeof(KV) == 2) {
+                k0 = __uint_as_float(u[e / 2] << 16);
+                k1 = __uint_as_float(u[e / 2] & 0xffff0000u);
+            } else {
+                k0 = __uint_as_float(u[e]);
+                k1 = __uint_as_float(u[e + 1]);
+            }
+            s0 = s0 + qv[e] * k0;
+            s1 = s1 + qv[e + 1] * k1;
         }
-        return ((s0 + s1) + (s2 + s3)) * scale;
+        return lanes_sum<KL>(s0 + s1) * scale;
     };
     float mx = -INFINITY;
-    if (has0) {
-        const float s = dot_raw(kr0);
-        sc[tid] = s;
-        mx = s;
-    }
-    for (int t = tid + kT; t < nmem; t += kT) {
-        Raw kr[D / 4];
 #pragma unroll
-        for (int d = 0; d < D / 4; ++d) kr[d] = kv_raw4(kc + (crow + t) * D + 4 * d);
-        const float s = dot_raw(kr);
-        sc[t] = s;
-        mx = fmaxf(mx, s);
+    for (int i = 0; i < KPRE; ++i) {
+        if (i * KRR >= nmem) break;  // uniform: rounds past the context
+        const int t = i * KRR + kr;
+        const float s = score(kpre[i]);
+        if (t < nmem) {
+            if (kl == 0) sc[t] = s;
+            mx = fmaxf(mx, s);
+        }
+    }
+    for (int t0 = KPRE * KRR; t0 < nmem; t0 += KRR) {
+        const int t = t0 + kr;
+        const float s = score(*(const uint4*)(kchunk + (int64_t)(t < nmem ? t : 0) * D));
+        if (t < nmem) {
+            if (kl == 0) sc[t] = s;
+            mx = fmaxf(mx, s);
+        }
     }
     if (ROPE && tid == (pos % kT)) {  // the current position, from LDS
         float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
