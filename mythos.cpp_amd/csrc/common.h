@@ -11,50 +11,99 @@
 
 namespace mth {
 
-// ---- cross-lane sums over groups of G consecutive lanes (G | 64) --------
-// Butterfly over xor-partners; every lane of a group ends with the group sum.
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
-    return v;
-}
-template <int G>
-__device__ __forceinline__ int group_sum_i(int v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
-    return v;
-}
-// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of
-// a group gets its sum.  Within 16 lanes by DPP row rotations (VALU only,
-// no LDS round trip; the empty asm keeps each read out of partial-exec
-// code), beyond that by shuffles.
-template <int CTRL>
-__device__ __forceinline__ float dpp_ror_f(float v) {
-    int r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false);
+// ---- cross-lane reductions over aligned groups of G lanes (G | 64) -------
+// In VALU only, with no LDS round trip: lanes l and l ^ 32 by
+// v_permlane32_swap and l and l ^ 16 by v_permlane16_swap (each swaps one
+// half of its two operands, so with both operands v its two results are v
+// and the partner in every lane), 16-lane rows by DPP row rotations, groups
+// of 8 / 4 / 2 by DPP half-mirror and quad permutations.  Every lane of a
+// group ends with the group's reduction (each step combines two equal-rank
+// values, so all lanes add the same operands).  The empty asm keeps each
+// cross-lane read out of partial-exec code.
+__device__ __forceinline__ uint32_t lane_pin(uint32_t r) {
     asm volatile("" : "+v"(r));
-    return __int_as_float(r);
+    return r;
 }
-template <int N>
-__device__ __forceinline__ float lanes_sum(float v) {
-    if constexpr (N >= 16) {
-        v += dpp_ror_f<0x128>(v);  // row_ror:8
-        v += dpp_ror_f<0x124>(v);  // row_ror:4
-        v += dpp_ror_f<0x122>(v);  // row_ror:2
-        v += dpp_ror_f<0x121>(v);  // row_ror:1
-#pragma unroll
-        for (int o = 16; o < N; o <<= 1) v += __shfl_xor(v, o, MTH_WAVE);
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return lane_pin((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false));
+}
+template <typename T>
+__device__ __forceinline__ uint32_t lane_bits(T v) { return __builtin_bit_cast(uint32_t, v); }
+template <typename T>
+__device__ __forceinline__ T lane_val(uint32_t b) { return __builtin_bit_cast(T, b); }
+
+template <int G, typename T, typename Op>
+__device__ __forceinline__ T group_reduce(T v, Op op) {
+    static_assert(sizeof(T) == 4 && G >= 1 && G <= 64 && (G & (G - 1)) == 0, "32-bit lanes, G a power of two");
+    if constexpr (G >= 64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(lane_bits(v), lane_bits(v), false, false);
+        v = op(lane_val<T>(lane_pin(r[0])), lane_val<T>(lane_pin(r[1])));
+    }
+    if constexpr (G >= 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(lane_bits(v), lane_bits(v), false, false);
+        v = op(lane_val<T>(lane_pin(r[0])), lane_val<T>(lane_pin(r[1])));
+    }
+    if constexpr (G >= 16) {
+        v = op(v, lane_val<T>(dpp_u<0x128>(lane_bits(v))));  // row_ror:8
+        v = op(v, lane_val<T>(dpp_u<0x124>(lane_bits(v))));  // row_ror:4
+        v = op(v, lane_val<T>(dpp_u<0x122>(lane_bits(v))));  // row_ror:2
+        v = op(v, lane_val<T>(dpp_u<0x121>(lane_bits(v))));  // row_ror:1
     } else {
-#pragma unroll
-        for (int o = N / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, N);
+        if constexpr (G >= 8) v = op(v, lane_val<T>(dpp_u<0x141>(lane_bits(v))));  // row_half_mirror
+        if constexpr (G >= 4) v = op(v, lane_val<T>(dpp_u<0x4E>(lane_bits(v))));   // quad_perm [2,3,0,1]
+        if constexpr (G >= 2) v = op(v, lane_val<T>(dpp_u<0xB1>(lane_bits(v))));   // quad_perm [1,0,3,2]
     }
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
+// The value of lane l ^ 1 (DPP quad_perm [1,0,3,2]).
+__device__ __forceinline__ float lane_xor1(float v) { return lane_val<float>(dpp_u<0xB1>(lane_bits(v))); }
+struct AddOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct MaxOp {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Transposed reduction of R per-lane values over the 64 lanes: halving
+// exchanges (lanes l ^ 32, l ^ 16, l ^ 8: each lane keeps the rows of its
+// half and adds its partner's values of them) and then a sum over groups of
+// 64 / R lanes.  After it every lane holds the wave total of row lane /
+// (64 / R).  R <= 8.
+template <int R, typename T>
+__device__ __forceinline__ T transposed_reduce(T (&v)[R], int lane) {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "R in 1, 2, 4, 8");
+    if constexpr (R >= 2) {  // lanes l ^ 32: lanes < 32 keep v[j], the rest v[j + R/2]
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MTH_WAVE));
-    return v;
+        for (int j = 0; j < R / 2; ++j) {
+            const auto r = __builtin_amdgcn_permlane32_swap(lane_bits(v[j]), lane_bits(v[j + R / 2]), false, false);
+            v[j] = lane_val<T>(lane_pin(r[0])) + lane_val<T>(lane_pin(r[1]));
+        }
+    }
+    if constexpr (R >= 4) {  // lanes l ^ 16
+#pragma unroll
+        for (int j = 0; j < R / 4; ++j) {
+            const auto r = __builtin_amdgcn_permlane16_swap(lane_bits(v[j]), lane_bits(v[j + R / 4]), false, false);
+            v[j] = lane_val<T>(lane_pin(r[0])) + lane_val<T>(lane_pin(r[1]));
+        }
+    }
+    if constexpr (R >= 8) {  // lanes l ^ 8 (row_ror:8)
+        const bool hi = (lane & 8) != 0;
+        const T send = hi ? v[0] : v[1], keep = hi ? v[1] : v[0];
+        v[0] = keep + lane_val<T>(dpp_u<0x128>(lane_bits(send)));
+    }
+    return group_reduce<64 / R>(v[0], AddOp{});
 }
+
+// Sums over groups of G consecutive lanes; every lane of a group gets it.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) { return group_reduce<G>(v, AddOp{}); }
+template <int G>
+__device__ __forceinline__ int group_sum_i(int v) { return group_reduce<G>(v, AddOp{}); }
+template <int N>
+__device__ __forceinline__ float lanes_sum(float v) { return group_reduce<N>(v, AddOp{}); }
+__device__ __forceinline__ float wave_max(float v) { return group_reduce<64>(v, MaxOp{}); }
 
 // ---- fp16 bits -> f32 (hardware v_cvt_f32_f16: exact for normals and
 // subnormals, the same values as src/kernel_oil4.cpp:15-29; NaNs stay NaN) ----
@@ -227,9 +276,32 @@ struct NormScale {
     int nparts;
     float dim, eps;
 };
+// Sum over the 64 lanes in FP64, the same steps as group_reduce<64> on both
+// halves of each value.
 __device__ __forceinline__ double wave_sum_dbl(double v) {
+    auto part = [](double x, int step) -> double {
+        const uint64_t b = __builtin_bit_cast(uint64_t, x);
+        const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+        uint32_t l2, h2;
+        if (step == 0 || step == 1) {
+            const auto rl = step == 0 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                                      : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+            const auto rh = step == 0 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                                      : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+            const double a = __builtin_bit_cast(double, (uint64_t)lane_pin(rl[0]) | ((uint64_t)lane_pin(rh[0]) << 32));
+            const double c = __builtin_bit_cast(double, (uint64_t)lane_pin(rl[1]) | ((uint64_t)lane_pin(rh[1]) << 32));
+            return a + c;
+        }
+        switch (step) {
+            case 2: l2 = dpp_u<0x128>(lo), h2 = dpp_u<0x128>(hi); break;
+            case 3: l2 = dpp_u<0x124>(lo), h2 = dpp_u<0x124>(hi); break;
+            case 4: l2 = dpp_u<0x122>(lo), h2 = dpp_u<0x122>(hi); break;
+            default: l2 = dpp_u<0x121>(lo), h2 = dpp_u<0x121>(hi); break;
+        }
+        return x + __builtin_bit_cast(double, (uint64_t)l2 | ((uint64_t)h2 << 32));
+    };
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int step = 0; step < 6; ++step) v = part(v, step);
     return v;
 }
 // This thread's share of token t's NormScale sum: partials i = i0, i0 +

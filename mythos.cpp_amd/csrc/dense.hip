@@ -35,16 +35,8 @@ namespace {
 constexpr int kT = 256;  // threads per workgroup (4 waves)
 constexpr int kArgChunk = 2048;  // argmax columns per stage-1 workgroup
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
-    return v;
-}
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, MTH_WAVE);
-    return v;
-}
+__device__ __forceinline__ double wave_sum_d(double v) { return wave_sum_dbl(v); }
+__device__ __forceinline__ float wave_sum_f(float v) { return group_sum<64>(v); }
 
 // Sum over the workgroup; every thread gets the total.
 template <typename T>

@@ -54,25 +54,10 @@ __device__ __forceinline__ uint32_t perm_addr(uint32_t packed, uint32_t lane4, i
     return __builtin_amdgcn_perm(packed, lane4, 0x0c0c0000u | ((uint32_t)(4 + b) << 8));
 }
 
-// Transposed reduction of R per-lane values over the 64 lanes.  After it,
-// every lane holds the wave total of row (lane / (64/R)).
+// Transposed reduction of R per-lane values over the 64 lanes (common.h):
+// every lane then holds the wave total of row lane / (64/R).
 template <int R>
-__device__ __forceinline__ float transposed_sum(float (&v)[R], int lane) {
-#pragma unroll
-    for (int n = R, mask = 32; n > 1; n >>= 1, mask >>= 1) {
-        const bool hi = (lane & mask) != 0;
-#pragma unroll
-        for (int j = 0; j < n / 2; ++j) {
-            const float send = hi ? v[j] : v[j + n / 2];
-            const float keep = hi ? v[j + n / 2] : v[j];
-            v[j] = keep + __shfl_xor(send, mask, MTH_WAVE);
-        }
-    }
-    float s = v[0];
-#pragma unroll
-    for (int mask = 32 / R; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask, MTH_WAVE);
-    return s;
-}
+__device__ __forceinline__ float transposed_sum(float (&v)[R], int lane) { return transposed_reduce<R>(v, lane); }
 
 // ===================================================================
 // OIL8
@@ -353,7 +338,7 @@ __global__ __launch_bounds__(NW * 64) void oil4_gemv_mfma(const uint8_t* nib, co
     // D[4g+i][n]: rows' hi (n = 0) + lo (n = 1) parts (oil4_hi_lo)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float s = oil4_hi_lo(acc[i], __shfl_xor(acc[i], 1, MTH_WAVE));
+        const float s = oil4_hi_lo(acc[i], lane_xor1(acc[i]));
         if (n == 0) part[wave * 16 + 4 * g + i] = ldexpf(s, -sh);
     }
     __syncthreads();
@@ -513,7 +498,7 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
     // D[4q+i][n]: rows' hi (n = 0) + lo (n = 1) parts (oil4_hi_lo)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float s = oil4_hi_lo(acc[i], __shfl_xor(acc[i], 1, MTH_WAVE));
+        const float s = oil4_hi_lo(acc[i], lane_xor1(acc[i]));
         if (j == 0) part[wave * 16 + 4 * q + i] = ldexpf(s, -sh);
     }
     __syncthreads();
@@ -535,10 +520,7 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
             }
             const float a = silu1(g) * u;
             sw.act[blockIdx.x * 8 + tid] = a;
-            float m = fabsf(a);
-            m = fmaxf(m, __shfl_xor(m, 4, 8));
-            m = fmaxf(m, __shfl_xor(m, 2, 8));
-            m = fmaxf(m, __shfl_xor(m, 1, 8));
+            const float m = group_reduce<8>(fabsf(a), MaxOp{});  // lanes 0-7, all active
             if (tid == 0) sw.amax[blockIdx.x] = m;
         }
         return;

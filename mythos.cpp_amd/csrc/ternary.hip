@@ -399,22 +399,7 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
 // across the wave by a transposed butterfly.  K % 64 == 0, K <= 4096 NSEG,
 // K <= 1024 XQ (FUSED).  Dynamic LDS: K bytes.
 template <int R>
-__device__ __forceinline__ int transposed_sum_i(int (&v)[R], int lane) {
-#pragma unroll
-    for (int n = R, mask = 32; n > 1; n >>= 1, mask >>= 1) {
-        const bool hi = (lane & mask) != 0;
-#pragma unroll
-        for (int j = 0; j < n / 2; ++j) {
-            const int send = hi ? v[j] : v[j + n / 2];
-            const int keep = hi ? v[j + n / 2] : v[j];
-            v[j] = keep + __shfl_xor(send, mask, MTH_WAVE);
-        }
-    }
-    int s = v[0];
-#pragma unroll
-    for (int mask = 32 / R; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask, MTH_WAVE);
-    return s;
-}
+__device__ __forceinline__ int transposed_sum_i(int (&v)[R], int lane) { return transposed_reduce<R>(v, lane); }
 
 template <int R, int NSEG, int XQ, bool FUSED>
 __global__ __launch_bounds__(kWG) void i2s_gemv_rows(const uint8_t* packed, float w_scale,
