@@ -504,6 +504,76 @@ __global__ __launch_bounds__(kWG) void i2s_gemv_rows(const uint8_t* packed, floa
     if ((lane % Lr) == 0 && row < M) y[row] = __fmul_rn(__fmul_rn((float)tot, w_scale), inv);
 }
 
+// I2_S GEMV, batch 1, K = 4096 exactly (i2s_gemv_k4096): i2s_gemv_rows with
+// every lane holding one full 16-byte segment of each of its 4 rows and no
+// bounds guard at all (the guarded kernel measured ~10% slower at this
+// shape: its branches changed the compiler's wait placement).  Same loads in
+// the same order, same quantisation and the same integer products, so the
+// outputs are those of i2s_gemv_rows bit for bit.  Dynamic LDS: 4096 bytes.
+constexpr int kK4096 = 4096;
+__global__ __launch_bounds__(kWG) void i2s_gemv_k4096(const uint8_t* packed, float w_scale,
+                                                      const float* __restrict__ x, float* __restrict__ y, int M) {
+    constexpr int R = 4, XQ = kK4096 / (4 * kWG), bpr = kK4096 / 4;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    int8_t* q = (int8_t*)lds_raw;
+    __shared__ float red[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = (blockIdx.x * kWaves + wave) * R;
+    float4 xr[XQ];
+#pragma unroll
+    for (int j = 0; j < XQ; ++j) xr[j] = ldf4(x + (tid + j * kWG) * 4);
+    uint4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = ld_stream(packed + (int64_t)min(row0 + r, M - 1) * bpr + (int64_t)lane * 16);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < XQ; ++j)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xr[j].x), fabsf(xr[j].y)), fmaxf(fabsf(xr[j].z), fabsf(xr[j].w))));
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    float mx = red[0];
+#pragma unroll
+    for (int w2 = 1; w2 < kWaves; ++w2) mx = fmaxf(mx, red[w2]);
+    if (mx < 1e-10f) mx = 1e-10f;
+    const float sc = __fdiv_rn(127.0f, mx), inv = __fdiv_rn(mx, 127.0f);
+#pragma unroll
+    for (int j = 0; j < XQ; ++j) {
+        const uint32_t b0 = (uint32_t)quant_i8(xr[j].x, sc) & 0xffu, b1 = (uint32_t)quant_i8(xr[j].y, sc) & 0xffu;
+        const uint32_t b2 = (uint32_t)quant_i8(xr[j].z, sc) & 0xffu, b3 = (uint32_t)quant_i8(xr[j].w, sc) & 0xffu;
+        *(uint32_t*)(q + (tid + j * kWG) * 4) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+    __syncthreads();
+    // lane's activations: A[d][j] byte b = a[lane*64 + 16d + 4b + j]
+    uint32_t A[4][4];
+    int asum = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint4 n = *(const uint4*)(q + lane * 64 + 16 * d);
+        const uint32_t N[4] = {n.x, n.y, n.z, n.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            A[d][j] = ((N[0] >> (8 * j)) & 0xffu) | (((N[1] >> (8 * j)) & 0xffu) << 8) |
+                      (((N[2] >> (8 * j)) & 0xffu) << 16) | (((N[3] >> (8 * j)) & 0xffu) << 24);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asum = dot4(N[j], 0x01010101u, asum);
+    }
+    int acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int a = 0;
+        a = tdot16(w[r].x, A[0], a);
+        a = tdot16(w[r].y, A[1], a);
+        a = tdot16(w[r].z, A[2], a);
+        a = tdot16(w[r].w, A[3], a);
+        acc[r] = a - asum;
+    }
+    const int tot = transposed_sum_i<R>(acc, lane);
+    constexpr int Lr = MTH_WAVE / R;
+    const int row = row0 + lane / Lr;
+    if ((lane % Lr) == 0 && row < M) y[row] = __fmul_rn(__fmul_rn((float)tot, w_scale), inv);
+}
+
 // Generic I2_S GEMV: one wave per (row, token); any K % 4 == 0.
 template <bool FUSED>
 __global__ __launch_bounds__(kWG) void i2s_gemv_generic(
@@ -1077,7 +1147,11 @@ hipError_t launch_i2s_gemv(const uint8_t* packed, float w_scale, const float* x,
         // batch 1, f32 activations: all loads up front, 16 rows per workgroup
         const int grid = ceil_div(M, 4 * kWaves);
         const size_t lds = (size_t)K;
-        i2s_gemv_rows<4, 1, 4, true><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M, (int)K);
+        if (K == kK4096)
+            i2s_gemv_k4096<<<grid, kWG, lds, s>>>(packed, w_scale, x, y, (int)M);
+        else
+            i2s_gemv_rows<4, 1, 4, true><<<grid, kWG, lds, s>>>(packed, w_scale, x, act, act_scale, y, (int)M,
+                                                                (int)K);
         return hipGetLastError();
     }
     if (fast) {
