@@ -223,8 +223,8 @@ int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_sca
  * 2F rows (gate rows first, then up; per-128 codebooks as mth_oil4_gemv with
  * cb_block 128) and the SwiGLU in the same launch: act[F] = silu(g) * u,
  * bit-identical to mth_oil4_gemv over the 2F rows followed by mth_silu_mul,
- * and amax[F / 8] = max |act| over rows 8t..8t+7.  F % 8 == 0, K % 1024 ==
- * 0, K <= 4096, 16-byte aligned packed / codebooks / x.
+ * and amax[F / 8] = max |act| over rows 8t..8t+7.  F % 8 == 0, K % 512 ==
+ * 0, 512 <= K <= 4096, 16-byte aligned packed / codebooks / x.
  *
  * mth_i2s_gemv_act: y = the I2_S GEMV of quantize_per_token(act) (the
  * quantisation done inside the launch), bit-identical to

@@ -409,7 +409,7 @@ int mth_oil4_gemv_swiglu(const uint8_t* packed, const uint16_t* codebooks, const
                          float* amax, int64_t F, int64_t K, mth_stream_t stream) {
     REQUIRE(packed && codebooks && x && act && amax, "mth_oil4_gemv_swiglu: null pointer");
     REQUIRE(mth::oil4_swiglu_supported(packed, codebooks, x, F, K),
-            "mth_oil4_gemv_swiglu: F=%lld K=%lld not supported (F %% 8 == 0, K %% 1024 == 0, K <= 4096, "
+            "mth_oil4_gemv_swiglu: F=%lld K=%lld not supported (F %% 8 == 0, K %% 512 == 0, 512 <= K <= 4096, "
             "16-byte aligned packed/codebooks/x)",
             (long long)F, (long long)K);
     return check_launch(mth::launch_oil4_swiglu(packed, codebooks, x, mth::NormScale{}, act, amax, F, K, S(stream)),

@@ -688,7 +688,7 @@ inline int pick_rows_per_wave(int64_t M, int rg) {
 #define MTH_OIL4_PD 2
 #endif
 #ifndef MTH_OIL4_V2_NPH
-#define MTH_OIL4_V2_NPH 4
+#define MTH_OIL4_V2_NPH 2
 #endif
 // oil4_gemv_v2 with NPH phases of 256 columns per wave, K / (256 NPH) waves
 template <int NPH, bool SHARED>
@@ -724,8 +724,9 @@ void run_oil4_mfma(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, co
 }  // namespace
 
 bool oil4_swiglu_supported(const uint8_t* nib, const uint16_t* cbs, const float* x, int64_t F, int64_t K) {
-    // the K range where launch_oil4_gemv runs oil4_gemv_v2 with 4 phases
-    return F > 0 && F % 8 == 0 && 2 * F < (1ll << 31) && K % 1024 == 0 && K >= 1024 && K <= 4096 &&
+    // the K range where launch_oil4_gemv runs oil4_gemv_v2 with MTH_OIL4_V2_NPH phases
+    constexpr int KP = 256 * MTH_OIL4_V2_NPH;
+    return F > 0 && F % 8 == 0 && 2 * F < (1ll << 31) && K % KP == 0 && K >= 512 && K <= 4096 &&
            aligned16(nib) && aligned16(cbs) && aligned16(x);
 }
 
@@ -734,13 +735,15 @@ hipError_t launch_oil4_swiglu(const uint8_t* nib, const uint16_t* cbs, const flo
     if (!oil4_swiglu_supported(nib, cbs, x, F, K)) return hipErrorInvalidValue;
     const SwigluTile sw{ns, act, amax, (int)F};
     const int grid = (int)(F / 8);
-    switch (K / 1024) {
+    constexpr int NPH = MTH_OIL4_V2_NPH;
+    switch (K / (256 * NPH)) {
 #define MTH_SW_CASE(NW)                                                                                     \
     case NW:                                                                                                \
-        oil4_gemv_v2<NW, 4, false, true><<<grid, NW * 64, 0, s>>>(nib, cbs, x, nullptr, (int)(2 * F),        \
-                                                                  (int)K, sw);                              \
+        oil4_gemv_v2<NW, NPH, false, true><<<grid, NW * 64, 0, s>>>(nib, cbs, x, nullptr, (int)(2 * F),      \
+                                                                    (int)K, sw);                            \
         break;
         MTH_SW_CASE(1) MTH_SW_CASE(2) MTH_SW_CASE(3) MTH_SW_CASE(4)
+        MTH_SW_CASE(5) MTH_SW_CASE(6) MTH_SW_CASE(7) MTH_SW_CASE(8)
 #undef MTH_SW_CASE
         default: return hipErrorInvalidValue;
     }

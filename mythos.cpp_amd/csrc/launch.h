@@ -44,7 +44,8 @@ hipError_t launch_oil8_gemm_mn(const uint8_t* idx, const float* cb, const float*
 // Batch 1, per-128 codebooks: the fused gate/up projection (rows [0, F) the
 // gate, [F, 2F) the up projection of one weight) with the SwiGLU in its
 // epilogue: act[F] = silu(g * ni) * (u * ni) (ni from ns; ns.ssp null: 1)
-// and amax[F / 8] = max |act| over rows 8t..8t+7.  K % 1024 == 0, K <= 4096.
+// and amax[F / 8] = max |act| over rows 8t..8t+7.  K % 512 == 0, 512 <= K <=
+// 4096 (the shapes launch_oil4_gemv runs on oil4_gemv_v2).
 bool oil4_swiglu_supported(const uint8_t* nib, const uint16_t* cbs, const float* x, int64_t F, int64_t K);
 hipError_t launch_oil4_swiglu(const uint8_t* nib, const uint16_t* cbs, const float* x, const NormScale& ns,
                               float* act, float* amax, int64_t F, int64_t K, hipStream_t s);

@@ -265,8 +265,9 @@ def test_oil4_gemm_reference_indexing(M, N, K, oracle, mth, dev):
 # ------------------------------------------ FFN in two launches (batch 1) --
 @pytest.mark.parametrize("F,K", [
     (11008, 4096),   # config 5's gate/up (four-wave workgroups)
-    (2048, 1024),    # one wave per workgroup
-    (64, 3072),      # three waves: norm-sum waves not a multiple of them
+    (2048, 1024),    # two waves per workgroup
+    (64, 3072),      # six waves: norm-sum waves not a multiple of them
+    (40, 512),       # one wave
     (8, 4096),       # one workgroup
 ])
 def test_oil4_gemv_swiglu_bit_exact(F, K, oracle, mth, dev):
@@ -323,7 +324,7 @@ def test_ffn_building_blocks_reject_shapes(mth, dev):
     with pytest.raises(mth.MythosError):
         mth.oil4_gemv_swiglu(p, c, f, f, f, 12, 1024)      # F % 8 != 0
     with pytest.raises(mth.MythosError):
-        mth.oil4_gemv_swiglu(p, c, f, f, f, 8, 1536)      # K % 1024 != 0
+        mth.oil4_gemv_swiglu(p, c, f, f, f, 8, 1280)      # K % 512 != 0
     with pytest.raises(mth.MythosError):
         mth.oil4_gemv_swiglu(p, c, f, f, f, 8, 8192)      # K > 4096
     with pytest.raises(mth.MythosError):
