@@ -51,6 +51,39 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
     __syncthreads();
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
+// The same over NW waves (pairwise over the waves in order: for NW == 4 the
+// sums of block_sum and the maximum of block_max).
+template <int NW, typename T>
+__device__ __forceinline__ T block_sum_w(T v, T* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if constexpr (sizeof(T) == 8)
+        v = wave_sum_d(v);
+    else
+        v = wave_sum_f(v);
+    __syncthreads();  // red may still be read by a previous reduction
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    T t[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t[w] = red[w];
+#pragma unroll
+    for (int st = 1; st < NW; st *= 2)
+#pragma unroll
+        for (int i = 0; i + st < NW; i += 2 * st) t[i] = t[i] + t[i + st];
+    return t[0];
+}
+template <int NW>
+__device__ __forceinline__ float block_max_w(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w]);
+    return m;
+}
 __device__ __forceinline__ float block_max(float v, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     v = wave_max(v);
@@ -387,20 +420,24 @@ __device__ __forceinline__ uint2 kv_raw4(const uint16_t* p) { return *(const uin
 // > 1: the prompt rows of a prefill chunk, each attending causally).
 // ns (ROPE, NormScale in common.h): q/k/v are projections of x * gamma and
 // get the RMSNorm's 1 / rms here.
-template <int D, bool ROPE, typename KV>
-__global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices vin, NormScale ns,
+// NT: threads per workgroup (256, or 1024 for a decode step of few heads:
+// the same work in 16 waves, each phase a quarter as long).
+template <int D, bool ROPE, typename KV, int NT = kT>
+__global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices vin, NormScale ns,
                                                   const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                                                   KV* kc, KV* vc, float* __restrict__ out, const int* __restrict__ step,
                                                   int ctx0, int np, int heads, int kv_heads, int max_seq,
                                                   float scale) {
     typedef typename KvRaw4<KV>::type Raw;
     constexpr int G = D / 4;        // float4 column groups
-    constexpr int SL = kT / G;      // position slices in P*V
-    constexpr int VP = (sizeof(KV) == 2 ? 16 : 8) * 128 / D;  // V rows per thread held in registers
+    constexpr int NW = NT / 64;
+    constexpr int SL = NT / G;      // position slices in P*V
+    constexpr int VP = (sizeof(KV) == 2 ? 16 : 8) * 128 / D * kT / NT;  // V rows per thread held in registers
+    static_assert(VP >= 1, "V rows per thread");
     extern __shared__ float sc[];   // [max_seq] scores, then probabilities
     __shared__ __align__(16) float qs[D], ks[D], vs[D];
     __shared__ float4 part[SL][G];
-    __shared__ float redf[4];
+    __shared__ float redf[NW];
     const int h = blockIdx.x, row = blockIdx.y, b = row / np, tid = threadIdx.x;
     const int pos = (step ? *step : 0) + ctx0 + row % np;  // the last position attended to
     const int ctx = pos + 1;
@@ -417,21 +454,30 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     // are six loads; split-K partials are loaded without branches
     // (slice_issue_all) and added after the cache loads are issued.
     double npart[kNormBatch];
-    if (ROPE && ns.ssp) norm_issue(ns, row, tid, kT, npart);
+    if (ROPE && ns.ssp) norm_issue(ns, row, tid, NT, npart);
     const bool plain = q.n == 1 && !q.tscale && (!ROPE || (kin.n == 1 && vin.n == 1 && !kin.tscale && !vin.tscale));
-    float raw[ROPE ? 6 : 1][kMaxSlices];
+    // (16 waves: split-K q/k/v summed on the spot, the registers are short)
+    constexpr bool RAW = NT <= kT;
+    float raw[RAW ? (ROPE ? 6 : 1) : 1][kMaxSlices];
     float q1 = 0.0f, q2 = 0.0f, k1 = 0.0f, k2 = 0.0f, v1 = 0.0f, v2 = 0.0f, c = 0.0f, sn = 0.0f;
     if (ROPE) {
         if (tid < D / 2) {
             const int64_t qm = h * D + tid, km = kh * D + tid;
-            if (plain) {
+            if (!RAW && !plain) {
+                q1 = slice_value(q, row, qm);
+                q2 = slice_value(q, row, qm + D / 2);
+                k1 = slice_value(kin, row, km);
+                k2 = slice_value(kin, row, km + D / 2);
+                v1 = slice_value(vin, row, km);
+                v2 = slice_value(vin, row, km + D / 2);
+            } else if (plain) {
                 q1 = q.p[row * q.ts + qm];
                 q2 = q.p[row * q.ts + qm + D / 2];
                 k1 = kin.p[row * kin.ts + km];
                 k2 = kin.p[row * kin.ts + km + D / 2];
                 v1 = vin.p[row * vin.ts + km];
                 v2 = vin.p[row * vin.ts + km + D / 2];
-            } else {
+            } else if constexpr (RAW) {
                 slice_issue_all(q, row, qm, raw[0]);
                 slice_issue_all(q, row, qm + D / 2, raw[1]);
                 slice_issue_all(kin, row, km, raw[2]);
@@ -445,15 +491,17 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
     } else if (tid < D) {
         if (plain)
             q1 = q.p[row * q.ts + h * D + tid];
-        else
+        else if constexpr (RAW)
             slice_issue_all(q, row, h * D + tid, raw[0]);
+        else
+            q1 = slice_value(q, row, h * D + tid);
     }
     // cache rows: K of the first KPRE rounds, then this thread's V rows.  A
     // K row is read by KL lanes, 16 bytes each (row kr of a round of KRR
     // rows, chunk kl), so that a load instruction covers whole rows.
     constexpr int KE = 16 / (int)sizeof(KV);  // cache elements per 16-byte chunk
     constexpr int KL = D / KE;                // lanes per K row
-    constexpr int KRR = kT / KL;              // K rows per round
+    constexpr int KRR = NT / KL;              // K rows per round
     constexpr int KPRE = 192 / KRR < 12 ? 192 / KRR : 12;  // rounds loaded up front (<= 192 rows)
     const int kl = tid % KL, kr = tid / KL;
     const KV* kchunk = kc + crow * D + kl * KE;
@@ -475,7 +523,7 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         const int t = sl + SL * j;
         vpre[j] = kv_raw4(vcol + (int64_t)(t < nmem ? t : 0) * D);
     }
-    if (!plain) {
+    if (RAW && !plain) {
         if (ROPE) {
             if (tid < D / 2) {
                 q1 = slice_sum(q, row, raw[0]);
@@ -490,15 +538,15 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         }
     }
     if (ROPE) {
-        __shared__ double nred[kT / 64];
+        __shared__ double nred[NW];
         float ni = 1.0f;
         if (ns.ssp) {  // the RMSNorm's 1 / rms (NormScale): same sum as norm_scale
-            const double sum = wave_sum_dbl(norm_finish(ns, row, tid, kT, npart));
+            const double sum = wave_sum_dbl(norm_finish(ns, row, tid, NT, npart));
             if ((tid & 63) == 0) nred[tid >> 6] = sum;
             __syncthreads();
             double t = 0.0;
 #pragma unroll
-            for (int w = 0; w < kT / 64; ++w) t += nred[w];
+            for (int w = 0; w < NW; ++w) t += nred[w];
             ni = (float)(1.0 / sqrt(t / (double)ns.dim + (double)ns.eps));
             q1 *= ni, q2 *= ni, k1 *= ni, k2 *= ni, v1 *= ni, v2 *= ni;
         }
@@ -560,7 +608,7 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
             mx = fmaxf(mx, s);
         }
     }
-    if (ROPE && tid == (pos % kT)) {  // the current position, from LDS
+    if (ROPE && tid == (pos % NT)) {  // the current position, from LDS
         float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
         for (int d = 0; d < D; d += 4) {
@@ -575,14 +623,14 @@ __global__ __launch_bounds__(kT) void attention_k(Slices q, Slices kin, Slices v
         sc[pos] = s;
         mx = fmaxf(mx, s);
     }
-    mx = block_max(mx, redf);
+    mx = block_max_w<NW>(mx, redf);
     float sum = 0.0f;
-    for (int t = tid; t < ctx; t += kT) {
+    for (int t = tid; t < ctx; t += NT) {
         const float e = expf(sc[t] - mx);
         sc[t] = e;
         sum += e;
     }
-    sum = block_sum(sum, redf);   // its barriers also publish sc[]
+    sum = block_sum_w<NW>(sum, redf);   // its barriers also publish sc[]
     const float inv = 1.0f / sum;
     float4 acc[4];
 #pragma unroll
@@ -986,15 +1034,30 @@ static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& 
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
     const dim3 grid((unsigned)heads, (unsigned)rows);
-    if (head_dim == 64)
-        attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
-                                                        heads, kv_heads, max_seq, scale);
-    else if (head_dim == 128)
-        attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
-                                                         heads, kv_heads, max_seq, scale);
-    else
-        attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
-                                                         heads, kv_heads, max_seq, scale);
+    // few workgroups (a decode step of a handful of sequences): 16 waves each
+    const bool wide = ROPE && np == 1 && rows * heads <= 128;
+    if (head_dim == 64) {
+        if (wide)
+            attention_k<64, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+                                                                    ctx0, np, heads, kv_heads, max_seq, scale);
+        else
+            attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
+                                                            heads, kv_heads, max_seq, scale);
+    } else if (head_dim == 128) {
+        if (wide)
+            attention_k<128, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+                                                                     ctx0, np, heads, kv_heads, max_seq, scale);
+        else
+            attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0,
+                                                             np, heads, kv_heads, max_seq, scale);
+    } else {
+        if (wide)
+            attention_k<256, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+                                                                     ctx0, np, heads, kv_heads, max_seq, scale);
+        else
+            attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0,
+                                                             np, heads, kv_heads, max_seq, scale);
+    }
     return hipGetLastError();
 }
 
