@@ -23,6 +23,10 @@
 #include "launch.h"
 #include "../../include/mythos_decoder.h"
 
+// Block maxima of the batched SwiGLU per token (one per 256 columns of ffn):
+// the fused batch path covers ffn <= 64 * 256.
+constexpr int kAmxParts = 64;
+
 struct mth_decoder {
     mth_decoder_config c{};
     int device = 0;
@@ -40,6 +44,7 @@ struct mth_decoder {
     float *rope_cos = nullptr, *rope_sin = nullptr, *bt_partial = nullptr, *arg_v = nullptr;
     double* ssp = nullptr;  // per-workgroup sums of squares of the split RMSNorm (ResidOut): attention norm
     double* ssp2 = nullptr;  // the same for the FFN norm (batch 1)
+    float* amx = nullptr;    // the SwiGLU's block maxima of |act| per token (batches: kAmxParts per token)
     int8_t* aq = nullptr;
     int *hist = nullptr, *step = nullptr, *ids = nullptr, *arg_i = nullptr;
     int64_t hist_stride = 0, layer_kv = 0;
@@ -375,6 +380,19 @@ hipError_t enqueue_step(const mth_decoder* d, hipStream_t s) {
             TRY(mth::launch_rms_norm_slices(d->x, so, L.ffn_norm, d->h, B, H, c.eps, s));
         if (tp) TRY(tap_copy(tp, d->x, (size_t)(B * H) * 4));
         const bool fused = gate_up_fused(d, L);
+        // Split norm: the SwiGLU in the gate/up projection's K-slice
+        // reduction (act over gu's gate half, block maxima in amx) and the
+        // per-token int8 quantisation inside the ternary GEMV: no SwiGLU launch
+        if (fused && splitb && mth::oil4_bt_swiglu_parts(F) <= kAmxParts &&
+            mth::oil4_bt_swiglu_supported(F, H, c.cb_block, B) && mth::i2s_bt_supported(H, F, B) &&
+            ((((uintptr_t)L.wgate | (uintptr_t)L.cbgate | (uintptr_t)d->h | (uintptr_t)L.wdown) & 15u) == 0)) {
+            TRY(mth::launch_oil4_gemv_bt_swiglu(L.wgate, L.cbgate, c.cb_block, d->h, ns_ffn, d->gu, d->amx, F, H, B,
+                                                d->bt_partial, s));
+            TRY(mth::launch_i2s_gemv_bt_f32act(L.wdown, L.down_scale, d->gu, 2 * F, d->amx,
+                                               mth::oil4_bt_swiglu_parts(F), d->a_inv, d->t, H, F, B, d->bt_partial,
+                                               &resid, s));
+            continue;
+        }
         // gate/up, then silu(gate)*up quantised to int8 per token (once, not
         // per workgroup of the down projection), then the ternary GEMV on the
         // int8 activations
@@ -495,6 +513,7 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->pf_att, (size_t)(PR * QD) * 4}, {(void**)&d->pf_gu, (size_t)(PR * 2 * F) * 4},
         {(void**)&d->pf_aq, (size_t)(PR * F)},      {(void**)&d->pf_inv, (size_t)PR * 4},
         {(void**)&d->ssp, (size_t)(H / 4 + 2) * 8},  {(void**)&d->ssp2, (size_t)(H / 4 + 2) * 8},
+        {(void**)&d->amx, (size_t)(B * kAmxParts) * 4},
     };
     size_t total = 0;
     for (const Slot& sl : slots) total += round_up(sl.bytes);

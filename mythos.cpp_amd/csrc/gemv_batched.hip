@@ -172,6 +172,70 @@ __global__ __launch_bounds__(256) void oil4_bt_reduce(const float* __restrict__ 
     y[i] = s;
 }
 
+// oil4_bt_reduce of a gate/up projection (rows [0, F) the gate, [F, 2F) the
+// up) with the SwiGLU after it (the decode step of a batch): the same sums,
+// then act[t * lda + i] = silu(g * ni) * (u * ni) (ni: the RMSNorm's 1 / rms
+// from ns, in norm_scale<16>'s order; ns.ssp null: 1) -- the activations of
+// silu_mul_quant_k bit for bit -- and per workgroup the maximum of |act|
+// over its 256 columns in amax[t][blockIdx.x] for the down projection's
+// quantisation.  act may be the gate half of the input itself (partial ==
+// act, lda == 2F, one slice): each thread writes only the element it alone
+// has read.  grid (ceil(F / 256), batch).
+__global__ __launch_bounds__(256) void oil4_bt_swiglu_reduce(const float* partial, NormScale ns, float* act,
+                                                             int64_t lda, float* __restrict__ amax, int F,
+                                                             int nslice) {
+    __shared__ double nred[16];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.y, i = blockIdx.x * 256 + tid, M = 2 * F;
+    const int ic = i < F ? i : F - 1;
+    // the norm's partial sums (four of norm_scale<16>'s waves per wave)
+    double np4[4];
+    if (ns.ssp) {
+        const int last = ns.nparts - 1;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) np4[v] = last >= 0 ? ns.ssp[(int64_t)t * ns.nparts + min((wave + 4 * v) * 64 + lane, last)] : 0.0;
+    }
+    const float* pg = partial + (int64_t)t * M + ic;
+    const int64_t zs = (int64_t)kBtTok * M;
+    float vg[16], vu[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) {
+        vg[z] = z < nslice ? pg[z * zs] : 0.0f;
+        vu[z] = z < nslice ? pg[z * zs + F] : 0.0f;
+    }
+    float g = vg[0], u = vu[0];
+#pragma unroll
+    for (int z = 1; z < 16; ++z)
+        if (z < nslice) {
+            g += vg[z];
+            u += vu[z];
+        }
+    if (ns.ssp) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int vt = (wave + 4 * v) * 64 + lane;
+            double a = vt < ns.nparts ? np4[v] : 0.0;
+            for (int k = vt + 1024; k < ns.nparts; k += 1024) a += ns.ssp[(int64_t)t * ns.nparts + k];
+            a = wave_sum_dbl(a);
+            if (lane == 0) nred[wave + 4 * v] = a;
+        }
+        __syncthreads();
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) sum += nred[w];
+        const float ni = (float)(1.0 / sqrt(sum / (double)ns.dim + (double)ns.eps));
+        g *= ni;
+        u *= ni;
+    }
+    const float a = silu1(g) * u;
+    if (i < F) act[(int64_t)t * lda + i] = a;
+    float m = i < F ? fabsf(a) : 0.0f;
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (tid == 0) amax[(int64_t)t * gridDim.x + blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
 
 inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
@@ -748,6 +812,26 @@ void bt_dispatch(const uint8_t* nib, const uint16_t* cbs, bool sh, const float* 
 }
 
 }  // namespace
+
+bool oil4_bt_swiglu_supported(int64_t F, int64_t K, int64_t cb_block, int64_t batch) {
+    return batch <= kBtTok && F % 4 == 0 && oil4_bt_supported(2 * F, K, cb_block, batch);
+}
+
+int oil4_bt_swiglu_parts(int64_t F) { return ceil_div_i(F, 256); }
+
+hipError_t launch_oil4_gemv_bt_swiglu(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x,
+                                      const NormScale& ns, float* gu, float* amax, int64_t F, int64_t K,
+                                      int64_t batch, float* partial, hipStream_t s) {
+    if (!oil4_bt_swiglu_supported(F, K, cb_block, batch)) return hipErrorInvalidValue;
+    const int64_t M = 2 * F;
+    const int S = (int)(K / (256 * bt_nph(K)));
+    bt_dispatch(nib, cbs, cb_block == 0, x, gu, partial, M, K, (int)batch, false, s);
+    // one slice: the GEMV wrote gu itself, [token][2F] like a slice of
+    // partial; act goes over gu's gate half either way
+    oil4_bt_swiglu_reduce<<<dim3((unsigned)oil4_bt_swiglu_parts(F), (unsigned)batch), 256, 0, s>>>(
+        S > 1 ? partial : gu, ns, gu, 2 * F, amax, (int)F, S);
+    return hipGetLastError();
+}
 
 bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch) {
     // K <= 8192 keeps the slice count <= 16 (the reduction kernel's limit)

@@ -56,6 +56,16 @@ hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_
 // partial: oil4_bt_partial_bytes(M, K) bytes of device scratch (null when
 // that is 0); calls that share it must be stream-ordered.
 bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch);
+// Batches of 2..16: the gate/up projection of one OIL4 weight of 2F rows
+// (gate first) and the SwiGLU after its K-slice reduction: gu[t][i] (i < F,
+// row stride 2F) = silu(g * ni) * (u * ni) (ni from ns; ns.ssp null: 1) and
+// amax[t][parts] the maxima of |act| over blocks of 256 columns
+// (oil4_bt_swiglu_parts(F) per token).  gu: 2F floats per token.
+bool oil4_bt_swiglu_supported(int64_t F, int64_t K, int64_t cb_block, int64_t batch);
+int oil4_bt_swiglu_parts(int64_t F);
+hipError_t launch_oil4_gemv_bt_swiglu(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x,
+                                      const NormScale& ns, float* gu, float* amax, int64_t F, int64_t K,
+                                      int64_t batch, float* partial, hipStream_t s);
 size_t oil4_bt_partial_bytes(int64_t M, int64_t K);
 hipError_t launch_oil4_gemv_bt(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, const float* x, float* y,
                                int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
@@ -98,6 +108,14 @@ hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t
                               int64_t M, int64_t K, int64_t batch, float* partial, hipStream_t s);
 // Batches of at most 16 without the slice reduction (Slices with the I2_S
 // epilogue, common.h).
+// Batches of 2..16 with FP32 activations quantised inside the launch (the
+// decode step): act[t * lda + k] and amax[t][nmx] as
+// launch_oil4_gemv_bt_swiglu writes them; inv[t] = max|act| / 127 is
+// written (the output's act scale).  out: the output as Slices (split-K
+// partials or y itself).
+hipError_t launch_i2s_gemv_bt_f32act(const uint8_t* packed, float w_scale, const float* act, int64_t lda,
+                                     const float* amax, int nmx, float* inv, float* y, int64_t M, int64_t K,
+                                     int64_t batch, float* partial, Slices* out, hipStream_t s);
 hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
                                     float* y, int64_t M, int64_t K, int64_t batch, float* partial, Slices* out,
                                     hipStream_t s);

@@ -758,17 +758,46 @@ __device__ __forceinline__ uint32_t byte_t4x4(uint32_t a, uint32_t b, uint32_t c
            (((d >> (8 * s)) & 0xffu) << 24);
 }
 
+// FP32 activations (the decode step of a batch, FA): act[t * lda + k] =
+// silu(g * ni) * (u * ni) with amax[t][nmx] the maxima of |act| over blocks
+// of it (oil4_gemv_bt_swiglu); the kernel quantises per token as
+// quantize_per_token (src/int8_quant.cpp:8-31) -- max |act| (the maximum of
+// the block maxima, floor 1e-10), q = round(act * (127 / max)) -- while
+// staging, and workgroup (0, 0) writes inv[t] = max / 127 (the consumer's
+// act scale).  nmx <= 16 kIbFaMx.
+struct I2sF32Act {
+    const float* act;  // row stride lda
+    int64_t lda;
+    const float* amax;
+    int nmx;
+    float* inv;
+};
+constexpr int kIbFaMx = 4, kIbFaChunks = 4;  // FA: block maxima per thread, chunks per round
+
 // One round of NC chunks (NC is the exact count, so every load below is
 // unconditional straight-line code and the waits before the staging and the
-// MFMAs count only what they need).
-template <int NC>
+// MFMAs count only what they need).  FA: the activations are FP32 (arowf)
+// and quantised with the token's scale sc while staging; in the first round
+// sc is derived from the block maxima mxv (loaded at the kernel's start)
+// after the weights are issued.
+template <int NC, bool FA = false>
 __device__ __forceinline__ void ib_round(const uint8_t* wrow, const int8_t* arow, bool sv, bool stager, int c0,
                                          bool first, uint32_t (*qs)[kIbTok * kIbTokStride], int st, int sg, int r,
-                                         int g, int& asum, i32x4& acc) {
-    uint4 an[NC], wv[NC];
+                                         int g, int& asum, i32x4& acc, const float* arowf = nullptr,
+                                         float* sc = nullptr, const float* mxv = nullptr,
+                                         const I2sF32Act* fa = nullptr, float* tinv = nullptr) {
+    uint4 an[FA ? 1 : NC], wv[NC];
+    float4 af[FA ? NC : 1][4];
     if (stager) {
+        if constexpr (FA) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) an[c] = ld16(arow + (int64_t)(c0 + c) * 256);  // a clamped row if !sv
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) af[c][e] = ldf4(arowf + (int64_t)(c0 + c) * 256 + 4 * e);
+        } else {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) an[c] = ld16(arow + (int64_t)(c0 + c) * 256);  // a clamped row if !sv
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();  // every wave's activations are issued before any weights
@@ -776,11 +805,40 @@ __device__ __forceinline__ void ib_round(const uint8_t* wrow, const int8_t* arow
 #pragma unroll
     for (int c = 0; c < NC; ++c) wv[c] = ld_stream(wrow + (int64_t)(c0 + c) * 64);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FA) {
+        if (first && stager) {  // the token's scale: 16 threads (sg) per token
+            float m = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kIbFaMx; ++k)
+                if (sg + 16 * k < fa->nmx) m = fmaxf(m, mxv[k]);
+            m = group_reduce<16>(m, MaxOp{});
+            if (m < 1e-10f) m = 1e-10f;
+            *sc = __fdiv_rn(127.0f, m);
+            const float inv = __fdiv_rn(m, 127.0f);
+            if (sg == 0) {
+                tinv[st] = inv;
+                if (blockIdx.x == 0 && blockIdx.y == 0 && sv) fa->inv[st] = inv;
+            }
+        }
+    }
     if (!first) __syncthreads();  // the previous round's chunks have been read
     if (stager) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const uint32_t a4[4] = {sv ? an[c].x : 0u, sv ? an[c].y : 0u, sv ? an[c].z : 0u, sv ? an[c].w : 0u};
+            uint32_t a4[4];
+            if constexpr (FA) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 v = af[c][i];
+                    a4[i] = sv ? ((uint32_t)quant_i8(v.x, *sc) & 0xffu) | (((uint32_t)quant_i8(v.y, *sc) & 0xffu) << 8) |
+                                     (((uint32_t)quant_i8(v.z, *sc) & 0xffu) << 16) |
+                                     (((uint32_t)quant_i8(v.w, *sc) & 0xffu) << 24)
+                               : 0u;
+                }
+            } else {
+                a4[0] = sv ? an[c].x : 0u, a4[1] = sv ? an[c].y : 0u, a4[2] = sv ? an[c].z : 0u;
+                a4[3] = sv ? an[c].w : 0u;
+            }
             // col 16sg + 4i + s at byte s of a4[i]
             uint4 o;
             o.x = byte_t4x4(a4[0], a4[1], a4[2], a4[3], 0);
@@ -807,15 +865,17 @@ __device__ __forceinline__ void ib_round(const uint8_t* wrow, const int8_t* arow
     }
 }
 
-template <int MAXC, int WV>
+template <int MAXC, int WV, bool FA = false>
 __global__ __launch_bounds__(WV * 64) void i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t* act,
                                                        const float* __restrict__ act_scale, float* __restrict__ y,
-                                                       float* __restrict__ partial, int M, int K, int batch) {
+                                                       float* __restrict__ partial, int M, int K, int batch,
+                                                       I2sF32Act fa = I2sF32Act{}) {
     static_assert(MAXC >= 1 && MAXC <= 8, "ib_round is dispatched for 1..8 chunks");
     // [chunk][token][16-col group][4 dwords], token stride kIbTokStride (64 + 4 dwords: the 16 tokens of an
     // MFMA operand read land on distinct banks)
     __shared__ __align__(16) uint32_t qs[MAXC][kIbTok * kIbTokStride];
     __shared__ int asum_p[kIbTok][16];
+    __shared__ float tinv[kIbTok];  // FA: max / 127 per token
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int m0 = blockIdx.x * (WV * 16) + wave * 16;
@@ -828,20 +888,28 @@ __global__ __launch_bounds__(WV * 64) void i2s_gemv_bt(const uint8_t* packed, fl
     const bool stager = __builtin_amdgcn_readfirstlane(wave) < 4;
     const bool sv = st < batch;
     const int8_t* arow = act + (int64_t)(sv ? st : 0) * K + 16 * sg;
+    // FA: the token's block maxima first (16 threads per token, clamped)
+    const float* arowf = FA ? fa.act + (int64_t)(sv ? st : 0) * fa.lda + 16 * sg : nullptr;
+    float mxv[kIbFaMx], sc = 0.0f;
+    if (FA && stager) {
+        const float* am = fa.amax + (int64_t)(sv ? st : 0) * fa.nmx;
+#pragma unroll
+        for (int k = 0; k < kIbFaMx; ++k) mxv[k] = am[min(sg + 16 * k, fa.nmx - 1)];
+    }
     int asum = 0;
     i32x4 acc = {0, 0, 0, 0};
     for (int c0 = sc0; c0 < sc1; c0 += MAXC) {
         const int nc = min(MAXC, sc1 - c0);
         const bool first = c0 == sc0;
         switch (nc) {
-            case 1: ib_round<1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            case 2: ib_round<2>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            case 3: ib_round<3>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            case 4: ib_round<4>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            case 5: ib_round<5 <= MAXC ? 5 : 1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            case 6: ib_round<6 <= MAXC ? 6 : 1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            case 7: ib_round<7 <= MAXC ? 7 : 1>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
-            default: ib_round<MAXC>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc); break;
+            case 1: ib_round<1, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            case 2: ib_round<2, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            case 3: ib_round<3, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            case 4: ib_round<4, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            case 5: ib_round<5 <= MAXC ? 5 : 1, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            case 6: ib_round<6 <= MAXC ? 6 : 1, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            case 7: ib_round<7 <= MAXC ? 7 : 1, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
+            default: ib_round<MAXC, FA>(wrow, arow, sv, stager, c0, first, qs, st, sg, r, g, asum, acc, arowf, &sc, mxv, &fa, tinv); break;
         }
     }
     if (stager) asum_p[st][sg] = asum;
@@ -858,7 +926,7 @@ __global__ __launch_bounds__(WV * 64) void i2s_gemv_bt(const uint8_t* packed, fl
         if (m >= M) continue;
         const int v = acc[i] - as;
         if (S == 1)
-            y[(int64_t)t * M + m] = __fmul_rn(__fmul_rn((float)v, w_scale), act_scale[t]);
+            y[(int64_t)t * M + m] = __fmul_rn(__fmul_rn((float)v, w_scale), FA ? tinv[t] : act_scale[t]);
         else
             partial[((int64_t)blockIdx.y * kIbTok + t) * M + m] = (float)v;
     }
@@ -1202,6 +1270,19 @@ hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const
     i2s_gemv_bt<kIbChunks, kIbWaves><<<dim3(ceil_div(M, kIbRows), (unsigned)S), kIbWaves * 64, 0, s>>>(packed, w_scale, act, act_scale, y, partial,
                                                                         (int)M, (int)K, (int)batch);
     *out = S == 1 ? plain_slices(y, M) : Slices{partial, M, kIbTok * M, S, w_scale, act_scale};
+    return hipGetLastError();
+}
+
+hipError_t launch_i2s_gemv_bt_f32act(const uint8_t* packed, float w_scale, const float* act, int64_t lda,
+                                     const float* amax, int nmx, float* inv, float* y, int64_t M, int64_t K,
+                                     int64_t batch, float* partial, Slices* out, hipStream_t s) {
+    if (!i2s_bt_supported(M, K, batch) || batch > kIbTok || nmx < 1 || nmx > 16 * kIbFaMx)
+        return hipErrorInvalidValue;
+    const int S = ib_slices(M, K);
+    const I2sF32Act fa{act, lda, amax, nmx, inv};
+    i2s_gemv_bt<kIbFaChunks, kIbWaves, true><<<dim3(ceil_div(M, kIbRows), (unsigned)S), kIbWaves * 64, 0, s>>>(
+        packed, w_scale, nullptr, nullptr, y, partial, (int)M, (int)K, (int)batch, fa);
+    *out = S == 1 ? plain_slices(y, M) : Slices{partial, M, kIbTok * M, S, w_scale, inv};
     return hipGetLastError();
 }
 
