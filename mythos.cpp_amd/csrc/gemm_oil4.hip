@@ -14,6 +14,8 @@
 #include "launch.h"
 #include "oil4_common.h"
 
+#include <type_traits>
+
 namespace mth {
 namespace {
 
@@ -292,55 +294,66 @@ __global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __re
 }
 
 // ===================================================================
-// Prefill with FP16 A (oil4_prefill_a16 + oil4_prefill_ws)
+// Prefill with FP16 A in MFMA fragment order (oil4_prefill_a16 + oil4_prefill_ws)
 // ===================================================================
-// With both operands staged in LDS (oil4_prefill_mfma) the LDS (128 B/clk per
-// CU, measured) carries ~1060 clk of traffic per K step of 64 against 896 clk
-// of MFMA work per SIMD.  Here only the dequantised W tile goes through LDS
-// (written once, read by four waves: ~560 clk); A is read from L2 straight
-// into the MFMA fragment registers, as FP16 converted once per call by
-// oil4_prefill_a16 (a per-workgroup conversion would cost ~96 VALU per wave
-// and step).  Workgroups on one XCD share an M tile (WG id i runs on XCD
-// i % 8), so each XCD's L2 holds one M tile's rows of A; C is staged through
-// LDS as bf16 and written in 16-byte pieces.
-template <int BN>
-struct Pf2Lds {
-    static constexpr int w = BN * 128;
-    static constexpr int stage = 256 * BN * 2;          // C tile (bf16), after the main loop
-    static constexpr int bytes = (2 * w > stage) ? 2 * w : stage;
-};
-
+// oil4_prefill_a16 converts A (bf16, exact in FP16 inside its range) once per
+// call and writes it in the order the MFMA reads it: for 16-row group g and
+// 32-column chunk kc, the 64 lanes' 16-byte A fragments (lane l: row 16g + l %
+// 16, columns 32kc + 8(l / 16) .. + 7) are 1 KB contiguous.  Each fragment
+// load of the GEMM is then one 1 KB run (8 full 128-byte lines); read in the
+// natural row-major order, a fragment load touches 16 rows x 64 bytes (16
+// half-used lines at an 8 KB stride), which measured 96 -> 83 us at config 4.
+// Rows past M repeat row M - 1 (their outputs are never stored); the
+// workspace holds ceil(M / 16) * 16 rows.
 __global__ __launch_bounds__(256) void oil4_prefill_a16(const uint16_t* __restrict__ a, uint16_t* __restrict__ a16,
-                                                        int64_t n8) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n8) return;
-    const uint4 v = ld16(a + 8 * i);
-    const half8 h = bf16x8_to_f16(v);
-    *(half8*)(a16 + 8 * i) = h;
+                                                        int M, int K, int64_t n16) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= n16) return;
+    const int l = (int)(o & 63);
+    const int64_t q = o >> 6;
+    const int kc32 = K / 32;
+    const int kc = (int)(q % kc32);
+    const int64_t g = q / kc32;
+    const int64_t r = min((int64_t)(16 * g + (l & 15)), (int64_t)M - 1);
+    *(half8*)(a16 + 8 * o) = bf16x8_to_f16(ld16(a + r * K + 32 * kc + 8 * (l >> 4)));
 }
 
 // ===================================================================
 // Prefill kernel, producer / consumer waves (oil4_prefill_ws)
 // ===================================================================
-// With one wave per SIMD, the W dequantisation (~110 VALU per step) and the
-// step's 56 MFMAs of the same wave are issued one after the other (measured:
-// MFMA busy 28% of the time).  Here a workgroup has 8 waves, two per SIMD:
-// waves 0-3 (consumers) hold the accumulators and run the MFMAs of their 64
-// rows, with A fragments loaded from L2 into registers one step ahead; waves
-// 4-7 (producers) stream the W nibbles and codebooks (PW - 1 steps ahead) and
-// dequantise the next step's tile into LDS.  The SIMD interleaves the two
-// waves' instructions, so the dequantisation runs under the MFMAs.  One
-// barrier per step hands the tile over (double-buffered).  Tile 256 x BN per
-// workgroup, one workgroup per CU.  At config 4 (512 x 14336 x 4096) it runs
-// at ~90% of the throughput hipBLASLt reaches on a dense FP16 GEMM of the same
-// shape on this GPU (torch.mm, measured in the same session).
-template <int BN, int PW = 2, int PA = 2>
+// A workgroup has 8 waves, two per SIMD, and computes a 256 x BN tile of C:
+// waves 0-3 (consumers) hold the accumulators of 64 rows each and run
+// v_mfma_f32_16x16x32_f16 with A fragments loaded from L2 into a ring of PA
+// registers sets (PA - 1 K steps ahead); waves 4-7 (producers) dequantise W
+// (v_perm lookups, oil4_common.h) into a ring of 2 BS FP16 tiles in LDS, one
+// tile per K step of 64, BS steps ahead of the consumers; one barrier per BS
+// steps hands the tiles over.  The SIMD interleaves the two waves, so the
+// dequantisation runs under the MFMAs.  A CU returns vector loads in issue
+// order across its waves, so the consumers' A loads (L2 hits) come back
+// behind the producers' weight stream (HBM): the A ring runs 3 steps ahead
+// where the registers allow it (BN <= 112; measured 79 -> 74 us at config 4
+// with BS = 2).  Producer thread pairs stream 32 nibbles per K step of one
+// row (4 steps ahead); a row's codebook block (32 bytes) covers two K steps
+// (cb_block % 128 == 0) and is loaded once per pair of steps, half by each
+// thread of the pair, the halves exchanged with a DPP lane swap.  Workgroups
+// on one XCD share an M tile (WG i runs on XCD i % 8), so an XCD's L2 holds
+// one M tile's rows of A.  C is staged through LDS as bf16 and written in
+// 16-byte pieces.
+template <int BN, int BS>
+struct Pf2Lds {
+    static constexpr int w = BN * 128;                   // one K step's dequantised W tile
+    static constexpr int stage = 256 * BN * 2;           // C tile (bf16), after the main loop
+    static constexpr int bytes = (2 * BS * w > stage) ? 2 * BS * w : stage;
+};
+
+template <int BN, int PA, int BS>
 __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restrict__ A16, const uint8_t* nib,
                                                        const uint16_t* cbs, int cb_block, uint16_t* __restrict__ C,
                                                        int M, int N, int K) {
-    using L = Pf2Lds<BN>;
-    constexpr int NT = BN / 16;
-    static_assert(PW == 2 || PW == 4, "ring index");
+    using L = Pf2Lds<BN, BS>;
+    constexpr int NT = BN / 16, PW = 4;
+    static_assert(PA == 2 || PA == 4, "A ring index");
+    static_assert(BS == 1 || BS == 2 || BS == 4, "barrier interval");
     __shared__ __align__(16) uint8_t lds[L::bytes];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tm = (M + PBM - 1) / PBM, tn = N / BN;
@@ -364,54 +377,72 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
         const int t = tid - 256;
         const bool wt = t < 2 * BN;
         const int wn = t >> 1, wh = t & 1;
-        const int nb = K / cb_block;
         const int wrow = n0 + (wt ? wn : 0);
         const uint8_t* wnib = nib + (int64_t)wrow * (K >> 1) + 16 * wh;
-        const uint16_t* wcb = cbs + (int64_t)wrow * nb * 16;
-        uint4 nv[PW], ca[PW], cc[PW];
-        auto load_w = [&](int step, int slot) {
-            const int k0 = step * PBK;
-            nv[slot] = ld_stream(wnib + (k0 >> 1));
-            const uint16_t* cp = wcb + (k0 / cb_block) * 16;
-            ca[slot] = ld16(cp);
-            cc[slot] = ld16(cp + 8);
-        };
-        auto dequant = [&](int slot, uint8_t* wb) {
+        const uint16_t* wcb = cbs + (int64_t)wrow * (K / cb_block) * 16 + 8 * wh;
+        const int pairs = steps >> 1;
+        uint4 nv[PW], cbh[2];
+        auto load_n = [&](int step, int slot) { nv[slot] = ld_stream(wnib + ((step * PBK) >> 1)); };
+        auto load_c = [&](int pair, int slot) { cbh[slot] = ld16(wcb + ((pair * 2 * PBK) / cb_block) * 16); };
+        // Dequantise K step x (x % 4 == XM) into its ring tile, then refill x's nibble slot with step x + 4 and,
+        // after the second step of a pair, the pair's codebook slot with the pair after next.
+        auto produce = [&](int x, auto xm) {
+            constexpr int XM = decltype(xm)::value;
+            const uint4 mine = cbh[(XM >> 1) & 1];
+            uint4 oth;
+            oth.x = dpp_u<0xB1>(mine.x);  // quad_perm [1,0,3,2]: the pair partner's half
+            oth.y = dpp_u<0xB1>(mine.y);
+            oth.z = dpp_u<0xB1>(mine.z);
+            oth.w = dpp_u<0xB1>(mine.w);
             if (wt) {
-                const CbPlanes pl = cb_planes(ca[slot], cc[slot]);
+                uint8_t* wb = lds + (x % (2 * BS)) * L::w;
+                const CbPlanes pl = wh ? cb_planes(oth, mine) : cb_planes(mine, oth);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    *(half8*)(wb + pf_off(wn, 4 * wh + i)) = lookup8_natural(u4get(nv[slot], i), pl);
+                    *(half8*)(wb + pf_off(wn, 4 * wh + i)) = lookup8_natural(u4get(nv[XM], i), pl);
             }
+            load_n(min(x + PW, steps - 1), XM);
+            if (XM & 1) load_c(min((x >> 1) + 2, pairs - 1), (XM >> 1) & 1);
         };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
 #pragma unroll
-        for (int u = 0; u < PW; ++u) load_w(u < steps ? u : steps - 1, u);
-        dequant(0, lds);
+        for (int u = 0; u < PW; ++u) load_n(min(u, steps - 1), u);
+        load_c(0, 0);
+        load_c(min(1, pairs - 1), 1);
+        produce(0, I0{});
+        if constexpr (BS >= 2) produce(1, I1{});
+        if constexpr (BS >= 4) {
+            produce(2, I2{});
+            produce(3, I3{});
+        }
         __syncthreads();
         for (int s0 = 0; s0 < steps; s0 += 4) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int step = s0 + u;
-                // W(step + 1) (loaded PW - 1 steps ago), then refill the slot of W(step)
-                dequant((u + 1) % PW, lds + ((u + 1) & 1) * L::w);
-                load_w(min(step + PW, steps - 1), u % PW);
-                __syncthreads();
-            }
+            // steps s0 + BS .. s0 + 3 + BS while the consumers run s0 .. s0 + 3 (tiles of steps >= steps are unused)
+            produce(s0 + BS, std::integral_constant<int, BS % 4>{});
+            if constexpr (BS == 1) __syncthreads();
+            produce(s0 + 1 + BS, std::integral_constant<int, (1 + BS) % 4>{});
+            if constexpr (BS <= 2) __syncthreads();
+            produce(s0 + 2 + BS, std::integral_constant<int, (2 + BS) % 4>{});
+            if constexpr (BS == 1) __syncthreads();
+            produce(s0 + 3 + BS, std::integral_constant<int, (3 + BS) % 4>{});
+            __syncthreads();
         }
         __syncthreads();  // consumers stage C
     } else {
         // ---------------- consumers ----------------
-        const int arow = min(m0 + 64 * wave + (lane & 15), M - 1);
-        const uint16_t* abase = A16 + (int64_t)arow * K + 8 * (lane >> 4);
-        static_assert(PA == 2 || PA == 4, "buffer index");
+        const int kc32 = K / 32;
+        const int g0 = (m0 >> 4) + 4 * wave, gmax = ((M + 15) >> 4) - 1;
+        const half8* af16 = (const half8*)A16 + lane;
         half8 af[PA][4][2];
         auto load_a = [&](int step, int b) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int r = min(m0 + 64 * wave + 16 * i + (lane & 15), M - 1) - arow;
+                const int g = min(g0 + i, gmax);
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk)
-                    af[b][i][kk] = *(const half8*)(abase + (int64_t)r * K + step * PBK + 32 * kk);
+                for (int kk = 0; kk < 2; ++kk) af[b][i][kk] = af16[((int64_t)g * kc32 + 2 * step + kk) * 64];
             }
         };
         floatx4 acc[4][NT];
@@ -420,14 +451,14 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
 #pragma unroll
             for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < PA - 1; ++u) load_a(u < steps ? u : steps - 1, u);
+        for (int u = 0; u < PA - 1; ++u) load_a(min(u, steps - 1), u);
         __syncthreads();
         for (int s0 = 0; s0 < steps; s0 += 4) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int step = s0 + u;
-                const uint8_t* cur = lds + (u & 1) * L::w;
-                load_a(min(step + PA - 1, steps - 1), (u + PA - 1) % PA);  // into the buffer of A(step - 1)
+                const uint8_t* cur = lds + (step % (2 * BS)) * L::w;
+                load_a(min(step + PA - 1, steps - 1), (u + PA - 1) % PA);  // into the set of A(step - 1)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     half8 bfr[NT];
@@ -441,9 +472,10 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
                             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u % PA][i][kk], bfr[j], acc[i][j], 0,
                                                                                0, 0);
                 }
-                __syncthreads();
+                if ((u + 1) % BS == 0) __syncthreads();
             }
         }
+        __syncthreads();
         uint16_t* st = (uint16_t*)lds;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -453,7 +485,6 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
                 for (int r = 0; r < 4; ++r)
                     st[(64 * wave + 16 * i + 4 * (lane >> 4) + r) * BN + 16 * j + (lane & 15)] =
                         f32_to_bf16_rne(acc[i][j][r]);
-        __syncthreads();
     }
     __syncthreads();
     const uint16_t* st = (const uint16_t*)lds;
@@ -500,25 +531,27 @@ inline int pick_bn(int64_t M, int64_t N) {
 
 }  // namespace
 
+// oil4_prefill_ws serves K % 256 == 0, codebook blocks of a multiple of 128 and an N that one of the tile widths
+// divides; the workspace is A in FP16 fragment order (ceil(M / 16) * 16 rows)
 size_t oil4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t cb_block) {
-    const bool v2 = K % (4 * PBK) == 0 && cb_block % PBK == 0 && pick_bn_v2(M, N) != 0 && M < (1ll << 31) &&
+    const bool v2 = K % (4 * PBK) == 0 && cb_block % (2 * PBK) == 0 && pick_bn_v2(M, N) != 0 && M < (1ll << 31) &&
                     ((M + PBM - 1) / PBM) * (N / 64) < (1ll << 31) && M * K < (1ll << 40);
-    return v2 ? (size_t)(M * K * 2) : 0;
+    return v2 ? (size_t)(((M + 15) / 16) * 16 * K * 2) : 0;
 }
 
 hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                         int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
                                         uint16_t* a16, hipStream_t s) {
-    const int64_t n8 = M * K / 8;
-    oil4_prefill_a16<<<(unsigned)((n8 + 255) / 256), 256, 0, s>>>(a_bf16, a16, n8);
+    const int64_t n16 = ((M + 15) / 16) * 16 * K / 8;
+    oil4_prefill_a16<<<(unsigned)((n16 + 255) / 256), 256, 0, s>>>(a_bf16, a16, (int)M, (int)K, n16);
     const int bn = pick_bn_v2(M, N);
     const unsigned grid = (unsigned)(((M + PBM - 1) / PBM) * (N / bn));
     const int cbk = (int)cb_block, m = (int)M, n = (int)N, k = (int)K;
     switch (bn) {
-        case 128: oil4_prefill_ws<128><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
-        case 112: oil4_prefill_ws<112><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
-        case 96: oil4_prefill_ws<96><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
-        default: oil4_prefill_ws<64><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
+        case 128: oil4_prefill_ws<128, 2, 1><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
+        case 112: oil4_prefill_ws<112, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
+        case 96: oil4_prefill_ws<96, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
+        default: oil4_prefill_ws<64, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
     }
     return hipGetLastError();
 }

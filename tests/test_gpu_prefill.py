@@ -3,9 +3,10 @@ oracle (small shapes, every element) and against a float64 contraction of the
 dequantised weights (config 4 shape, sampled rows and all columns).
 
 Tolerance: 2e-3 relative for the OIL4/bf16 path.  The
-production kernel (K and the codebook block multiples of 64) uses the FP16
-codebook entries exactly and converts A bf16 -> FP16 (exact in range), sums in
-FP32; the output is rounded to bf16 (<= 2^-8 relative).  Asserted norm-wise
+production kernel (K a multiple of 256, the codebook block a multiple of 128,
+N a multiple of 128, 112, 96 or 64) uses the FP16 codebook entries exactly and
+converts A bf16 -> FP16 (exact in range), sums in FP32; the output is rounded
+to bf16 (<= 2^-8 relative).  Asserted norm-wise
 <= 2e-3 and per element |d| <= 2^-8*|ref| + 1e-3*sum|a*w|.  Other shapes run
 the first FP16 kernel (same arithmetic, smaller tiles).
 """
@@ -28,8 +29,11 @@ def check(got_bits, ref_f64, absw, what):
     return nrm
 
 
-@pytest.mark.parametrize("M,N,K,block", [(128, 256, 256, 128), (200, 130, 512, 64), (16, 64, 4096, 128),
-                                         (300, 250, 1024, 128), (32, 48, 96, 32)])
+# producer/consumer kernel: tile widths 128 (256, 128), 112 (224; ragged M, block 256), 96 (288; two M tiles,
+# M % 16 != 0), 64 (64); block 64 and N = 130 / 250 take the one-wave kernel, K = 96 the first kernel
+@pytest.mark.parametrize("M,N,K,block", [(128, 256, 256, 128), (64, 128, 1024, 128), (40, 224, 512, 256),
+                                         (270, 288, 1024, 128), (96, 256, 512, 64), (200, 130, 512, 64),
+                                         (16, 64, 4096, 128), (300, 250, 1024, 128), (32, 48, 96, 32)])
 def test_prefill_small_vs_oracle(M, N, K, block, oracle, mth, dev):
     import torch
     print(f"prefill M={M} N={N} K={K} block={block}", flush=True)
