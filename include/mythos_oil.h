@@ -230,7 +230,7 @@ int mth_silu_mul_quant(const float* g, const float* u, int8_t* q, float* inv_sca
  * quantisation done inside the launch), bit-identical to
  * mth_quantize_per_token followed by mth_i2s_gemv; amax as written by
  * mth_oil4_gemv_swiglu (the maxima of |act| over groups of 8).  K % 64 ==
- * 0, K <= 12288, 16-byte aligned packed. */
+ * 0, K <= 12288, 16-byte aligned packed and act. */
 int mth_oil4_gemv_swiglu(const uint8_t* packed, const uint16_t* codebooks, const float* x, float* act,
                          float* amax, int64_t F, int64_t K, mth_stream_t stream);
 int mth_i2s_gemv_act(const uint8_t* packed, float w_scale, const float* act, const float* amax, float* y,

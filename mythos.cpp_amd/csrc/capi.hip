@@ -421,8 +421,8 @@ int mth_i2s_gemv_act(const uint8_t* packed, float w_scale, const float* act, con
     REQUIRE(packed && act && amax && y, "mth_i2s_gemv_act: null pointer");
     REQUIRE(M > 0 && K > 0 && M < kMaxDim, "mth_i2s_gemv_act: bad sizes M=%lld K=%lld", (long long)M,
             (long long)K);
-    REQUIRE(mth::i2s_swiglu_supported(packed, M, K),
-            "mth_i2s_gemv_act: K=%lld not supported (K %% 64 == 0, K <= 12288, 16-byte aligned packed)",
+    REQUIRE(mth::i2s_swiglu_supported(packed, M, K) && (((uintptr_t)act & 15u) == 0),
+            "mth_i2s_gemv_act: K=%lld not supported (K %% 64 == 0, K <= 12288, 16-byte aligned packed and act)",
             (long long)K);
     return check_launch(mth::launch_i2s_act(act, amax, packed, w_scale, y, M, K, mth::ResidOut{}, nullptr,
                                             S(stream)),

@@ -11,6 +11,17 @@
 
 namespace mth {
 
+// ---- rounded FP32 products ---------------------------------------------------
+// x * y rounded to FP32 on its own.  hipcc's __fmul_rn is a plain multiply,
+// which the compiler may fuse with a following add into one FMA (one rounding
+// instead of two) depending on the surrounding code; the reference rounds the
+// product first (e.g. an I2_S row's (sum * w_scale) * act_scale, then the
+// residual add), so these products are kept out of contraction.
+__device__ __forceinline__ float fmul_rn(float x, float y) {
+#pragma clang fp contract(off)
+    return x * y;
+}
+
 // ---- cross-lane reductions over aligned groups of G lanes (G | 64) -------
 // In VALU only, with no LDS round trip: lanes l and l ^ 32 by
 // v_permlane32_swap and l and l ^ 16 by v_permlane16_swap (each swaps one
@@ -225,7 +236,7 @@ __device__ __forceinline__ float slice_sum(const Slices& s, int t, const float (
 #pragma unroll
     for (int z = 1; z < kMaxSlices; ++z)
         if (z < s.n) sum += v[z];
-    if (s.tscale) sum = __fmul_rn(__fmul_rn(sum, s.scale), s.tscale[t]);
+    if (s.tscale) sum = fmul_rn(fmul_rn(sum, s.scale), s.tscale[t]);
     return sum;
 }
 __device__ __forceinline__ float slice_value(const Slices& s, int t, int64_t m) {
@@ -251,8 +262,8 @@ __device__ __forceinline__ float4 slice_value4(const Slices& s, int t, int64_t m
         }
     if (s.tscale) {
         const float ts = s.tscale[t];
-        sum = make_float4(__fmul_rn(__fmul_rn(sum.x, s.scale), ts), __fmul_rn(__fmul_rn(sum.y, s.scale), ts),
-                          __fmul_rn(__fmul_rn(sum.z, s.scale), ts), __fmul_rn(__fmul_rn(sum.w, s.scale), ts));
+        sum = make_float4(fmul_rn(fmul_rn(sum.x, s.scale), ts), fmul_rn(fmul_rn(sum.y, s.scale), ts),
+                          fmul_rn(fmul_rn(sum.z, s.scale), ts), fmul_rn(fmul_rn(sum.w, s.scale), ts));
     }
     return sum;
 }
@@ -361,7 +372,7 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 // Reference int8 quantisation of one value (src/int8_quant.cpp:19):
 // (int8_t)std::round(v * scale) — round half away from zero, then truncate.
 __device__ __forceinline__ int quant_i8(float v, float scale) {
-    return (int)(int8_t)(int)__builtin_roundf(__fmul_rn(v, scale));
+    return (int)(int8_t)(int)__builtin_roundf(fmul_rn(v, scale));
 }
 
 }  // namespace mth

@@ -208,7 +208,7 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
                 acc = tdot16(sv ? w[s].w : pad, A[s][3], acc);
             }
             acc = group_sum_i<LPR>(acc - asum);
-            const float v = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
+            const float v = fmul_rn(fmul_rn((float)acc, w_scale), inv);
             const int64_t i = (int64_t)t * M + row;
             if (!res.x) {
                 if (li == 0 && rv) y[i] = v;
@@ -250,10 +250,7 @@ __global__ __launch_bounds__(kWG, 2) void i2s_gemv_fast(
 // to res.ssp, which must not be ns.ssp (other workgroups may still read it).
 constexpr int kSwT = 1024, kSwQ = 12;  // as silu_mul_quant_k (kSQT, kSQ)
 
-// PRE: g holds the SwiGLU output a itself and u the maxima of |a| over
-// groups of 8 columns (K / 8 of them, oil4_gemv_v2's SwiGLU epilogue); the
-// norm and the SwiGLU are skipped and max|a| is the maximum of those maxima.
-template <int NSEG, bool PRE = false>
+template <int NSEG>
 __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g, const float* __restrict__ u,
                                                      NormScale ns, const uint8_t* packed, float w_scale,
                                                      float* __restrict__ y, int M, int K, ResidOut res) {
@@ -267,20 +264,13 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
     const int bpr = K >> 2, nseg = bpr >> 4;
 
     double npart[kNormBatch];
-    float mp[2];  // PRE: maxima of groups tid, tid + 1024 (K / 8 <= 2 * kSwT)
-    if (PRE) {
-        const int last = (K >> 3) - 1;
-        mp[0] = u[min(tid, last)];
-        mp[1] = u[min(tid + kSwT, last)];
-    } else if (ns.ssp) {
-        norm_issue(ns, 0, tid, kSwT, npart);
-    }
+    if (ns.ssp) norm_issue(ns, 0, tid, kSwT, npart);
     float gv[kSwQ], uv[kSwQ];
 #pragma unroll
     for (int j = 0; j < kSwQ; ++j) {
         const int i = tid + j * kSwT;
         gv[j] = i < K ? g[i] : 0.0f;
-        if (!PRE) uv[j] = i < K ? u[i] : 0.0f;
+        uv[j] = i < K ? u[i] : 0.0f;
     }
     uint4 w[NSEG];
     __builtin_amdgcn_sched_barrier(0);
@@ -289,7 +279,7 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
         w[s] = ld_stream(packed + (int64_t)min(row, M - 1) * bpr + (int64_t)min(lane + 64 * s, nseg - 1) * 16);
     __builtin_amdgcn_sched_barrier(0);
 
-    if (!PRE && ns.ssp) {  // norm_scale<16>: per-thread sums, wave sums, waves in order
+    if (ns.ssp) {  // norm_scale<16>: per-thread sums, wave sums, waves in order
         double sum = wave_sum_dbl(norm_finish(ns, 0, tid, kSwT, npart));
         if (lane == 0) nred[wave] = sum;
         __syncthreads();
@@ -304,15 +294,10 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
         }
     }
     float m = 0.0f;
-    if (PRE) {
-        if (tid < (K >> 3)) m = fmaxf(m, mp[0]);
-        if (tid + kSwT < (K >> 3)) m = fmaxf(m, mp[1]);
-    } else {
 #pragma unroll
-        for (int j = 0; j < kSwQ; ++j) {
-            gv[j] = silu1(gv[j]) * uv[j];
-            m = fmaxf(m, fabsf(gv[j]));
-        }
+    for (int j = 0; j < kSwQ; ++j) {
+        gv[j] = silu1(gv[j]) * uv[j];
+        m = fmaxf(m, fabsf(gv[j]));
     }
     m = wave_max(m);
     if (lane == 0) red[wave] = m;
@@ -364,7 +349,7 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
         acc = tdot16(sv ? w[s].w : pad, A[s][3], acc);
     }
     acc = group_sum_i<64>(acc - asum);
-    const float v = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
+    const float v = fmul_rn(fmul_rn((float)acc, w_scale), inv);
     const bool rv = row < M;
     if (!res.x) {
         if (lane == 0 && rv) y[row] = v;
@@ -383,6 +368,140 @@ __global__ __launch_bounds__(kSwT) void i2s_swiglu_k(const float* __restrict__ g
         double t = 0.0;
 #pragma unroll
         for (int w2 = 0; w2 < kSwT / 64; ++w2) t += rsq[w2];
+        res.ssp[blockIdx.x] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// I2_S down projection from a SwiGLU output computed elsewhere (decode batch 1)
+// ---------------------------------------------------------------------------
+// act = a (K floats) and amax = the maxima of |a| over groups of 8 columns
+// (K / 8 of them, oil4_gemv_v2's SwiGLU epilogue): max|a| is the maximum of
+// the maxima, q = quantize_per_token(a) (src/int8_quant.cpp:8-31) and
+// y[m] = ((float)sum_k t(m, k) q[k] * w_scale) * (max|a| / 127), the values
+// i2s_swiglu_k computes.  Workgroup = 8 waves, two rows per wave (16 rows):
+// every wave holds the whole token's int8 operands in registers, so two rows
+// per wave halve the LDS reads and the activation sums per row (16 waves of
+// one row measured 8.0 us at 4096 x 11008, 8 waves of two 6.4 us, 4 of four
+// 6.8 us).  Loads in order of use: maxima, activations (float4), the rows'
+// weights.  The residual epilogue sums the 16 rows' squares in row order,
+// as i2s_swiglu_k does.
+constexpr int kIaR = 2, kIaT = 1024 / kIaR;
+
+template <int NSEG>
+__global__ __launch_bounds__(kIaT) void i2s_act_k(const float* __restrict__ act, const float* __restrict__ amax,
+                                                  const uint8_t* packed, float w_scale, float* __restrict__ y, int M,
+                                                  int K, ResidOut res) {
+    constexpr int R = kIaR, T = kIaT, NW = T / 64;
+    constexpr int NM = (kSwT * kSwQ / 8 + T - 1) / T, NA = (kSwT * kSwQ / 4 + T - 1) / T;  // K <= kSwT * kSwQ
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    int8_t* q = (int8_t*)lds_raw;  // K bytes
+    __shared__ float red[NW];
+    __shared__ double rsq[NW * R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * (NW * R) + wave * R;
+    const int bpr = K >> 2, nseg = bpr >> 4, nm = K >> 3, n4 = K >> 2;
+    float mp[NM];
+#pragma unroll
+    for (int j = 0; j < NM; ++j) mp[j] = amax[min(tid + j * T, nm - 1)];
+    float4 av[NA];
+#pragma unroll
+    for (int j = 0; j < NA; ++j) av[j] = ((const float4*)act)[min(tid + j * T, n4 - 1)];
+    uint4 w[R][NSEG];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int s = 0; s < NSEG; ++s)
+            w[r][s] = ld_stream(packed + (int64_t)min(row0 + r, M - 1) * bpr +
+                                (int64_t)min(lane + 64 * s, nseg - 1) * 16);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+        if (tid + j * T < nm) m = fmaxf(m, mp[j]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) m = fmaxf(m, red[w2]);
+    if (m < 1e-10f) m = 1e-10f;
+    const float sc = __fdiv_rn(127.0f, m), inv = __fdiv_rn(m, 127.0f);
+    // q transposed within each 16-column group (column 4b + j at byte 4j + b), the operand order of tdot16
+#pragma unroll
+    for (int j = 0; j < NA; ++j) {
+        const int i4 = tid + j * T;
+        if (i4 < n4) {
+            const float vv[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int i = 4 * i4 + b;
+                q[(i & ~15) | ((i & 3) << 2) | ((i >> 2) & 3)] = (int8_t)quant_i8(vv[b], sc);
+            }
+        }
+    }
+    __syncthreads();
+
+    // lane's activations: A[s][d][j] byte b = a[seg*64 + 16d + 4b + j]
+    uint32_t A[NSEG][4][4];
+    int asum = 0;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        const int seg = lane + 64 * s;
+        if (seg < nseg) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint4 n = *(const uint4*)(q + seg * 64 + 16 * d);
+                A[s][d][0] = n.x, A[s][d][1] = n.y, A[s][d][2] = n.z, A[s][d][3] = n.w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asum = dot4(A[s][d][j], 0x01010101u, asum);
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) A[s][d][j] = 0;
+        }
+    }
+    float vr = 0.0f;  // lane r: row row0 + r
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int acc = 0;
+#pragma unroll
+        for (int s = 0; s < NSEG; ++s) {
+            const bool sv = lane + 64 * s < nseg;
+            const uint32_t pad = 0x55555555u;  // t = 0 codes past the row (they meet A = 0)
+            acc = tdot16(sv ? w[r][s].x : pad, A[s][0], acc);
+            acc = tdot16(sv ? w[r][s].y : pad, A[s][1], acc);
+            acc = tdot16(sv ? w[r][s].z : pad, A[s][2], acc);
+            acc = tdot16(sv ? w[r][s].w : pad, A[s][3], acc);
+        }
+        acc = group_sum_i<64>(acc - asum);
+        const float v = fmul_rn(fmul_rn((float)acc, w_scale), inv);
+        if (lane == r) vr = v;
+    }
+    const int row = row0 + lane;
+    if (!res.x) {
+        if (lane < R && row < M) y[row] = vr;
+        return;
+    }
+    if (lane < R) {
+        double sq = 0.0;
+        if (row < M) {
+            const float r = vr + res.x[row];
+            res.x[row] = r;
+            res.xg[row] = r * res.gamma[row];
+            sq = (double)r * r;
+        }
+        rsq[wave * R + lane] = sq;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double t = 0.0;
+#pragma unroll
+        for (int i = 0; i < NW * R; ++i) t += rsq[i];
         res.ssp[blockIdx.x] = t;
     }
 }
@@ -501,7 +620,7 @@ __global__ __launch_bounds__(kWG) void i2s_gemv_rows(const uint8_t* packed, floa
     const int tot = transposed_sum_i<R>(acc, lane);
     constexpr int Lr = MTH_WAVE / R;
     const int row = row0 + lane / Lr;
-    if ((lane % Lr) == 0 && row < M) y[row] = __fmul_rn(__fmul_rn((float)tot, w_scale), inv);
+    if ((lane % Lr) == 0 && row < M) y[row] = fmul_rn(fmul_rn((float)tot, w_scale), inv);
 }
 
 // I2_S GEMV, batch 1, K = 4096 exactly (i2s_gemv_k4096): i2s_gemv_rows with
@@ -571,7 +690,7 @@ __global__ __launch_bounds__(kWG) void i2s_gemv_k4096(const uint8_t* packed, flo
     const int tot = transposed_sum_i<R>(acc, lane);
     constexpr int Lr = MTH_WAVE / R;
     const int row = row0 + lane / Lr;
-    if ((lane % Lr) == 0 && row < M) y[row] = __fmul_rn(__fmul_rn((float)tot, w_scale), inv);
+    if ((lane % Lr) == 0 && row < M) y[row] = fmul_rn(fmul_rn((float)tot, w_scale), inv);
 }
 
 // Generic I2_S GEMV: one wave per (row, token); any K % 4 == 0.
@@ -605,7 +724,7 @@ __global__ __launch_bounds__(kWG) void i2s_gemv_generic(
             acc += tv * a;
         }
         acc = group_sum_i<64>(acc);
-        if (lane == 0) y[t * M + row] = __fmul_rn(__fmul_rn((float)acc, w_scale), inv);
+        if (lane == 0) y[t * M + row] = fmul_rn(fmul_rn((float)acc, w_scale), inv);
     }
 }
 
@@ -706,7 +825,7 @@ __global__ __launch_bounds__(kWG) void tl2_gemm_k(const uint8_t* __restrict__ w,
 __global__ __launch_bounds__(kWG) void dequantize_k(const int8_t* __restrict__ src, float* __restrict__ dst,
                                                     int64_t n, float inv) {
     const int64_t i = (int64_t)blockIdx.x * kWG + threadIdx.x;
-    if (i < n) dst[i] = __fmul_rn((float)src[i], inv);
+    if (i < n) dst[i] = fmul_rn((float)src[i], inv);
 }
 
 // Pair / triple LUTs of src/kernel_tl.cpp:13-31 and :88-107; one thread per
@@ -926,7 +1045,7 @@ __global__ __launch_bounds__(WV * 64) void i2s_gemv_bt(const uint8_t* packed, fl
         if (m >= M) continue;
         const int v = acc[i] - as;
         if (S == 1)
-            y[(int64_t)t * M + m] = __fmul_rn(__fmul_rn((float)v, w_scale), FA ? tinv[t] : act_scale[t]);
+            y[(int64_t)t * M + m] = fmul_rn(fmul_rn((float)v, w_scale), FA ? tinv[t] : act_scale[t]);
         else
             partial[((int64_t)blockIdx.y * kIbTok + t) * M + m] = (float)v;
     }
@@ -947,7 +1066,7 @@ __global__ __launch_bounds__(kWG) void i2s_bt_reduce(const float* __restrict__ p
 #pragma unroll
     for (int z = 1; z < kMaxSlices; ++z)
         if (z < nslice) s += v[z];
-    y[i] = __fmul_rn(__fmul_rn(s, w_scale), act_scale[t]);
+    y[i] = fmul_rn(fmul_rn(s, w_scale), act_scale[t]);
 }
 
 // K slices of the batched I2_S GEMV: about one workgroup per CU (256), at
@@ -1190,17 +1309,16 @@ hipError_t launch_i2s_swiglu(const float* g, const float* u, const NormScale& ns
 
 hipError_t launch_i2s_act(const float* act, const float* amax, const uint8_t* packed, float w_scale, float* y,
                           int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s) {
-    if (!i2s_swiglu_supported(packed, M, K)) return hipErrorInvalidValue;
+    if (!i2s_swiglu_supported(packed, M, K) || !aligned16(act)) return hipErrorInvalidValue;
     const int64_t nseg = K / 64;
-    const int grid = ceil_div(M, kSwT / 64);
+    const int grid = ceil_div(M, kIaT / 64 * kIaR);
     const size_t lds = (size_t)K;
-    const NormScale none{};
     if (nseg <= 64)
-        i2s_swiglu_k<1, true><<<grid, kSwT, lds, s>>>(act, amax, none, packed, w_scale, y, (int)M, (int)K, ro);
+        i2s_act_k<1><<<grid, kIaT, lds, s>>>(act, amax, packed, w_scale, y, (int)M, (int)K, ro);
     else if (nseg <= 128)
-        i2s_swiglu_k<2, true><<<grid, kSwT, lds, s>>>(act, amax, none, packed, w_scale, y, (int)M, (int)K, ro);
+        i2s_act_k<2><<<grid, kIaT, lds, s>>>(act, amax, packed, w_scale, y, (int)M, (int)K, ro);
     else
-        i2s_swiglu_k<3, true><<<grid, kSwT, lds, s>>>(act, amax, none, packed, w_scale, y, (int)M, (int)K, ro);
+        i2s_act_k<3><<<grid, kIaT, lds, s>>>(act, amax, packed, w_scale, y, (int)M, (int)K, ro);
     if (nparts) *nparts = grid;
     return hipGetLastError();
 }

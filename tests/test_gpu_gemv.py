@@ -298,6 +298,7 @@ def test_oil4_gemv_swiglu_bit_exact(F, K, oracle, mth, dev):
     (4096, 512),
     (100, 64),       # one segment
     (33, 12288),     # the largest K, rows not a multiple of 16
+    (17, 8256),      # three segments per lane, the last partial; one row past a workgroup
 ])
 def test_i2s_gemv_act_bit_exact(M, K, oracle, mth, dev):
     """The I2_S GEMV of quantize_per_token(act) with the quantisation inside
@@ -329,6 +330,8 @@ def test_ffn_building_blocks_reject_shapes(mth, dev):
         mth.oil4_gemv_swiglu(p, c, f, f, f, 8, 8192)      # K > 4096
     with pytest.raises(mth.MythosError):
         mth.i2s_gemv_act(p, 1.0, f, f, f, 8, 1000)         # K % 64 != 0
+    with pytest.raises(mth.MythosError):
+        mth.i2s_gemv_act(p, 1.0, f[1:], f, f, 8, 64)       # act not 16-byte aligned
 
 
 # ------------------------------------------------------------- int8/I2_S --
