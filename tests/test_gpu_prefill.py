@@ -29,9 +29,11 @@ def check(got_bits, ref_f64, absw, what):
     return nrm
 
 
-# producer/consumer kernel: tile widths 128 (256, 128), 112 (224; ragged M, block 256), 96 (288; two M tiles,
-# M % 16 != 0), 64 (64); block 64 and N = 130 / 250 take the one-wave kernel, K = 96 the first kernel
+# producer/consumer kernel (the tile width with the best fill of 256 CUs): 128 (N = 32768), 112 (224; ragged M,
+# block 256), 96 (288: two M tiles, M % 16 != 0; 96: three M tiles, the last of one row), 64 (N = 256, 128, 64;
+# one row); block 64 and N = 130 / 250 take the one-wave kernel, K = 96 the first kernel
 @pytest.mark.parametrize("M,N,K,block", [(128, 256, 256, 128), (64, 128, 1024, 128), (40, 224, 512, 256),
+                                         (1, 128, 256, 128), (513, 96, 512, 128), (16, 32768, 256, 128),
                                          (270, 288, 1024, 128), (96, 256, 512, 64), (200, 130, 512, 64),
                                          (16, 64, 4096, 128), (300, 250, 1024, 128), (32, 48, 96, 32)])
 def test_prefill_small_vs_oracle(M, N, K, block, oracle, mth, dev):
