@@ -10,12 +10,14 @@ per second.  Method, per workload:
     timing; the weight operand is replicated into >= 1 GiB of distinct copies
     and consecutive steps rotate over them, so every step streams its weights
     from HBM rather than the 256 MB MALL;
-  * the launches of one rotation are captured in a HIP graph and replayed
-    back to back; W warm-up steps, then exactly K timed steps bracketed by
-    device synchronisation, timed with HIP events on the launch stream;
+  * the launches of one rotation are captured in a HIP graph (the K mod
+    copies launches after it in a second one) and replayed back to back; at
+    least W warm-up steps, then exactly K timed steps bracketed by device
+    synchronisation, timed with HIP events on the launch stream;
   * value = algorithmic bytes per launch / average launch time.
 cpu_baseline: the CPU restatement of the reference kernel (oracle, "port"),
-single thread, timed on a bounded sample of the same workload on this host.
+on the host's cores (up to 16 OpenMP threads; the one-thread figure in
+extra), timed on a bounded sample of the same workload on this host.
 
 Prints ONE JSON line.
 """
@@ -59,9 +61,13 @@ def replicate(t, nbytes_each):
 
 def time_graph(launch, n_copies, steps, warmup):
     """launch(i) enqueues step i (rotating copy i % n_copies) on the current
-    stream.  Captures one rotation in a graph, replays it; returns
-    (avg seconds per step, steps actually timed)."""
+    stream.  Captures one rotation in a graph (and the steps % n_copies
+    launches that follow it in a second one), replays at least `warmup`
+    untimed launches, then times exactly `steps` launches: steps // n_copies
+    replays of the rotation and one of the remainder.  Returns (avg seconds
+    per step, steps timed)."""
     import torch
+    steps = max(1, int(steps))
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         for i in range(n_copies):  # eager pass: first-touch, JIT-free check
@@ -71,9 +77,15 @@ def time_graph(launch, n_copies, steps, warmup):
     with torch.cuda.graph(g, stream=s):
         for i in range(n_copies):
             launch(i)
+    full, rem = divmod(steps, n_copies)
+    gr = None
+    if rem:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            for i in range(rem):
+                launch(i)
     torch.cuda.synchronize()
     reps_w = max(1, -(-warmup // n_copies))
-    reps = max(1, -(-steps // n_copies))
     with torch.cuda.stream(s):
         for _ in range(reps_w):
             g.replay()
@@ -81,12 +93,14 @@ def time_graph(launch, n_copies, steps, warmup):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(s):
         e0.record(s)
-        for _ in range(reps):
+        for _ in range(full):
             g.replay()
+        if gr is not None:
+            gr.replay()
         e1.record(s)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
-    return ms / 1e3 / (reps * n_copies), reps * n_copies
+    return ms / 1e3 / steps, steps
 
 
 def bench_oil4_gemv(mth, dev, M, K, batch, steps, warmup, block=128):
