@@ -317,6 +317,14 @@ def test_i2s_gemv_act_bit_exact(M, K, oracle, mth, dev):
         assert np.array_equal(y.cpu().numpy().reshape(1, M), ref)
 
 
+@pytest.mark.parametrize("M,K", [(int(m), 64 * int(k)) for m, k in
+                                 zip(np.random.default_rng(5).integers(1, 300, 6),
+                                     np.random.default_rng(6).integers(1, 193, 6))])
+def test_i2s_gemv_act_random_shapes(M, K, oracle, mth, dev):
+    """Seeded random (M, K): K % 64 == 0 up to 12288 (one to three segments per lane), ragged M."""
+    test_i2s_gemv_act_bit_exact(M, K, oracle, mth, dev)
+
+
 def test_ffn_building_blocks_reject_shapes(mth, dev):
     import torch
     p = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)

@@ -52,6 +52,25 @@ def test_prefill_small_vs_oracle(M, N, K, block, oracle, mth, dev):
     check(got, ref32.astype(np.float64), absw, "prefill vs oracle")
 
 
+def _random_prefill_shapes(n, seed=11):
+    """Seeded shapes for the producer/consumer kernel: N a multiple of one of its tile widths, K % 256 == 0,
+    codebook blocks of 128 or 256, ragged M."""
+    g = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        bn = int(g.choice([64, 96, 112, 128]))
+        out.append((int(g.integers(1, 600)), bn * int(g.integers(1, 5)), 256 * int(g.integers(1, 5)),
+                    int(g.choice([128, 256]))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,block", _random_prefill_shapes(8))
+def test_prefill_random_shapes_vs_oracle(M, N, K, block, oracle, mth, dev):
+    if K % block:
+        block = 128
+    test_prefill_small_vs_oracle(M, N, K, block, oracle, mth, dev)
+
+
 def test_prefill_config4_sampled(mth, dev):
     import torch
     M, N, K, block = 512, 14336, 4096, 128
