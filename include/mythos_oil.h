@@ -9,8 +9,10 @@
  * never accumulated.
  *
  * Workspace.  The batched GEMVs (mth_oil8_gemv, mth_oil4_gemv, mth_i2s_gemv
- * with batch >= 2), mth_argmax, mth_oil4_gemm_prefill (an FP16 copy of A,
- * M*K*2 bytes, for K % 256 == 0) and mth_i2s_gemm_vnni (permuted activations,
+ * with batch >= 2), mth_argmax, mth_oil4_gemm_prefill (an FP16 copy of A in
+ * MFMA fragment order, ceil(M/16)*16*K*2 bytes, for K % 256 == 0, codebook
+ * blocks of a multiple of 128 and N a multiple of 64, 96 or 112) and
+ * mth_i2s_gemm_vnni (permuted activations,
  * for its MFMA shapes) keep intermediate data in a device workspace
  * the library owns, one per (device, stream).  The first call that needs more
  * than the stream's workspace holds allocates a larger one (hipMalloc, at
