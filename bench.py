@@ -85,13 +85,17 @@ def time_graph(launch, n_copies, steps, warmup):
             for i in range(rem):
                 launch(i)
     torch.cuda.synchronize()
+    # warm-up: every graph the timed region replays is replayed first, and
+    # the timed replays are queued behind the last warm-up replay (no
+    # synchronisation in between), so the timed launches start on a busy
+    # queue as in steady state
     reps_w = max(1, -(-warmup // n_copies))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(s):
         for _ in range(reps_w):
             g.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):
+        if gr is not None:
+            gr.replay()
         e0.record(s)
         for _ in range(full):
             g.replay()
@@ -157,6 +161,53 @@ def bench_i2s_gemv_i8(mth, dev, M, K, batch, steps, warmup):
                         warmup)
     alg = packed.nbytes + 4 + q.nbytes + inv.nbytes + 4 * M * batch
     return dict(sec=sec, steps=n, bytes=alg, copies=len(ps))
+
+
+def stream_floor(dev, nbytes, steps, warmup):
+    """The measured streaming floor for one launch that reads `nbytes` once:
+    the fastest of a plain 16-byte streaming-read kernel
+    (csrc/stream_probe.hip) over a few grid shapes, rotated over >= 1 GiB
+    of copies and timed like the GEMVs.  Returns (seconds per launch, grid,
+    unroll)."""
+    import ctypes as C
+    import torch
+    lib = C.CDLL(os.path.join(ROOT, "mythos.cpp_amd", "libmythos_probe.so"))
+    lib.mth_probe_stream_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.mth_probe_stream_read.restype = C.c_int
+    nb = -(-nbytes // 4096) * 4096
+    n = max(2, -(-ROTATE_BYTES // nb))
+    buf = torch.ones(n * nb, dtype=torch.uint8, device=dev)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    base, optr = buf.data_ptr(), out.data_ptr()
+    best = None
+    for grid in (512, 1024, 2048, 4096):
+        for unroll in (1, 4):
+            def launch(i, grid=grid, unroll=unroll):
+                rc = lib.mth_probe_stream_read(base + i * nb, nbytes, grid, unroll, optr,
+                                               torch.cuda.current_stream().cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"stream probe failed ({rc})")
+            sec, _ = time_graph(launch, n, steps, warmup)
+            if best is None or sec < best[0]:
+                best = (sec, grid, unroll)
+    del buf
+    torch.cuda.empty_cache()
+    return best
+
+
+def cpu_time(fn, budget_s):
+    """Median seconds of fn() over repetitions filling ~budget_s (3 warm-ups
+    and at least 10 timed calls, as bench/bench_oil_quant.cpp:23-32 of the
+    reference times its kernels)."""
+    for _ in range(3):
+        fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < 10 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts)
 
 
 def bench_prefill(mth, dev, M, N, K, steps, warmup, block=128):
@@ -283,6 +334,18 @@ def cpu_threads():
     return max(1, min(16, n))
 
 
+def cpu_model():
+    """The host CPU's model name (lscpu's), for the CPU baselines."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_reference_oil8(idx, cb, x, M, K, budget_s):
     """The reference's own oil8_gemm (AVX2 build, oracle/_ref) when present."""
     sys.path.insert(0, ROOT)
@@ -322,7 +385,8 @@ def main():
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,i2sb16,prefill,ternary_gemm,decode (default all)")
+    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,i2sb16,floor,prefill,"
+                                               "ternary_gemm,decode (default all); floor: each GEMV's streaming floor")
     ap.add_argument("--decode-batches", default="1,16", help="comma list of decode batch sizes (config 5)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -341,43 +405,57 @@ def main():
 
     extra = {}
     head = None
+    floors = {}
+
+    def floor_of(name, nbytes):
+        """Streaming floor for nbytes, measured once per size (want("floor"))."""
+        if not want("floor"):
+            return None
+        if nbytes not in floors:
+            sec, grid, unroll = stream_floor(dev, nbytes, args.steps, args.warmup)
+            floors[nbytes] = dict(us=sec * 1e6, GBps=nbytes / sec / 1e9, frac=nbytes / sec / 1e9 / HBM_PEAK_GBS,
+                                  grid=grid, unroll=unroll)
+            log(f"stream floor {nbytes} B: {sec*1e6:.2f} us ({nbytes / sec / 1e9:.0f} GB/s, grid {grid} x{unroll})")
+        extra.setdefault("stream_floor", {})[name] = dict(bytes=nbytes, **floors[nbytes])
+        return floors[nbytes]["us"]
+
+    def gemv_entry(name, r):
+        gbs = r["bytes"] / r["sec"] / 1e9
+        e = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS, bytes=r["bytes"], copies=r["copies"],
+                 traffic=load_traffic(name))
+        fl = floor_of(name, r["bytes"])
+        if fl is not None:
+            e.update(floor_us=fl, frac_of_floor=fl / e["us"])
+        return e
+
     if want("oil4"):
         M, K = 11008, 4096
         r, data = bench_oil4_gemv(mth, dev, M, K, 1, args.steps, args.warmup)
         gbs = r["bytes"] / r["sec"] / 1e9
         head = dict(r=r, gbs=gbs, data=data, M=M, K=K)
         log(f"oil4 b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s ({gbs/HBM_PEAK_GBS:.1%})")
+        head["floor_us"] = floor_of("oil4_gemv_11008x4096_b1", r["bytes"])
     if want("oil4b16"):
         r, _ = bench_oil4_gemv(mth, dev, 11008, 4096, 16, args.steps, args.warmup)
-        gbs = r["bytes"] / r["sec"] / 1e9
-        extra["oil4_gemv_11008x4096_b16"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                                 bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("oil4_gemv_11008x4096_b16"))
-        log(f"oil4 b=16: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
-    oil8_data = None
+        extra["oil4_gemv_11008x4096_b16"] = e = gemv_entry("oil4_gemv_11008x4096_b16", r)
+        log(f"oil4 b=16: {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
+    oil8_data = i2s_data = None
     if want("oil8"):
         r, oil8_data = bench_oil8_gemv(mth, dev, 4096, 4096, 1, args.steps, args.warmup)
-        gbs = r["bytes"] / r["sec"] / 1e9
-        extra["oil8_gemv_4096x4096_b1"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                               bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("oil8_gemv_4096x4096_b1"))
-        log(f"oil8 b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
+        extra["oil8_gemv_4096x4096_b1"] = e = gemv_entry("oil8_gemv_4096x4096_b1", r)
+        log(f"oil8 b=1: {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
     if want("oil8b16"):
         r, _ = bench_oil8_gemv(mth, dev, 4096, 4096, 16, args.steps, args.warmup)
-        gbs = r["bytes"] / r["sec"] / 1e9
-        extra["oil8_gemv_4096x4096_b16"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                                bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("oil8_gemv_4096x4096_b16"))
-        log(f"oil8 b=16: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
+        extra["oil8_gemv_4096x4096_b16"] = e = gemv_entry("oil8_gemv_4096x4096_b16", r)
+        log(f"oil8 b=16: {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
     if want("i2s"):
-        r, _ = bench_i2s_gemv(mth, dev, 4096, 4096, 1, args.steps, args.warmup)
-        gbs = r["bytes"] / r["sec"] / 1e9
-        extra["i2s_gemv_4096x4096_b1"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                              bytes=r["bytes"], copies=r["copies"], traffic=load_traffic("i2s_gemv_4096x4096_b1"))
-        log(f"i2s b=1: {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
+        r, i2s_data = bench_i2s_gemv(mth, dev, 4096, 4096, 1, args.steps, args.warmup)
+        extra["i2s_gemv_4096x4096_b1"] = e = gemv_entry("i2s_gemv_4096x4096_b1", r)
+        log(f"i2s b=1: {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
     if want("i2sb16"):
         r = bench_i2s_gemv_i8(mth, dev, 4096, 11008, 16, args.steps, args.warmup)
-        gbs = r["bytes"] / r["sec"] / 1e9
-        extra["i2s_gemv_4096x11008_b16_int8"] = dict(us=r["sec"] * 1e6, GBps=gbs, frac=gbs / HBM_PEAK_GBS,
-                                                     bytes=r["bytes"], copies=r["copies"])
-        log(f"i2s b=16 (int8 acts, 4096x11008): {r['sec']*1e6:.2f} us/launch, {gbs:.0f} GB/s")
+        extra["i2s_gemv_4096x11008_b16_int8"] = e = gemv_entry("i2s_gemv_4096x11008_b16_int8", r)
+        log(f"i2s b=16 (int8 acts, 4096x11008): {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
     if want("prefill"):
         r = bench_prefill(mth, dev, 512, 14336, 4096, args.steps, args.warmup)
         tf = r["flop"] / r["sec"] / 1e12
@@ -415,6 +493,35 @@ def main():
         if ref:
             extra["cpu_reference_oil8_gemm_avx2"] = dict(ms=ref[0] * 1e3, GBps=16811008 / ref[0] / 1e9, calls=ref[1],
                                                          cores=1)
+    # configs 1 and 3 on the host: the oracle's OIL8 GEMV (AVX2 lane order
+    # of src/kernel_oil8.cpp:30-60) and its I2_S GEMV with the per-token
+    # quantisation (src/kernel_i2s.cpp:32-40, src/int8_quant.cpp:24-31), one
+    # thread and all cores, median of >= 10 calls
+    if oil8_data is not None or i2s_data is not None:
+        sys.path.insert(0, ROOT)
+        from oracle import Oracle
+        o = Oracle()
+        nt = cpu_threads()
+        budget = min(3.0, args.cpu_seconds / 4)
+        jobs = []
+        if oil8_data is not None:
+            idx, cb, x = oil8_data
+            ib, xb = np.ascontiguousarray(idx.ravel()), np.ascontiguousarray(x[:1])
+            jobs.append(("cpu_oil8_gemv_4096x4096_b1", 16811008,
+                         lambda th: o.oil8_gemv(ib, cb, xb, 4096, 4096, 1, threads=th)))
+        if i2s_data is not None:
+            packed, w_scale, x = i2s_data
+            pb, xb3 = np.ascontiguousarray(packed.ravel()), np.ascontiguousarray(x[:1])
+            jobs.append(("cpu_i2s_gemv_4096x4096_b1", 4227076,
+                         lambda th: o.i2s_gemv_f32(pb, float(w_scale), xb3, 4096, 4096, 1, threads=th)))
+        for name, nbytes, fn in jobs:
+            e = {}
+            for th in (1, nt):
+                sec, n = cpu_time(lambda: fn(th), budget)
+                e[f"threads_{th}"] = dict(ms=sec * 1e3, GBps=nbytes / sec / 1e9, calls=n)
+                log(f"{name}, {th} thread(s): {sec*1e3:.2f} ms")
+            e.update(kind="port", cores_all=nt, cpu=cpu_model())
+            extra[name] = e
 
     if head is None:
         print(json.dumps(dict(metric=METRIC, extra=extra)))
@@ -439,7 +546,10 @@ def main():
                    "M": head["M"], "K": head["K"], "batch": 1, "cb_block": 128,
                    "weight_copies": r["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic("oil4_gemv_11008x4096_b1")},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic("oil4_gemv_11008x4096_b1"),
+                     "floor_us": head.get("floor_us"),
+                     "frac_of_floor": (round(head["floor_us"] / (r["sec"] * 1e6), 4) if head.get("floor_us")
+                                       else None)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -238,6 +238,31 @@ int mth_oil4_gemv_swiglu(const uint8_t* packed, const uint16_t* codebooks, const
 int mth_i2s_gemv_act(const uint8_t* packed, float w_scale, const float* act, const float* amax, float* y,
                      int64_t M, int64_t K, mth_stream_t stream);
 
+/* The same pair for batches of 2..16 tokens (the decoder's batch path; the
+ * reference runs FFN::forward per token as above):
+ *
+ * mth_oil4_gemv_swiglu_batch: x [batch][K]; gu [batch][2F]: act of token t
+ * in gu[t*2F + i], i < F, = silu(g) * u, bit-identical to mth_oil4_gemv over
+ * the 2F rows (same batch) followed by mth_silu_mul; gu[t*2F + F ..] is
+ * overwritten.  amax [batch][mth_swiglu_batch_parts(F)] = max |act| over
+ * columns 256j .. 256j + 255.  Per-128 codebooks (cb_block 128) or one
+ * shared codebook (cb_block 0); K % 512 == 0, 512 <= K <= 8192, F % 4 ==
+ * 0, 16-byte aligned packed / codebooks / x.
+ *
+ * mth_i2s_gemv_act_batch: y [batch][M] = the I2_S GEMV of
+ * quantize_per_token(act[t*lda .. t*lda + K)) (src/int8_quant.cpp:24-31,
+ * quantised inside the launch), bit-identical to mth_quantize_per_token
+ * followed by mth_i2s_gemv; amax [batch][parts] the block maxima of |act|
+ * over 256 columns as mth_oil4_gemv_swiglu_batch writes them (parts =
+ * mth_swiglu_batch_parts(K)); inv_scale [batch] receives max|act| / 127.
+ * K % 256 == 0, K <= 16384, lda % 4 == 0, 16-byte aligned packed and act.
+ * Both use the stream's workspace (mth_workspace_reserve). */
+int64_t mth_swiglu_batch_parts(int64_t F);
+int mth_oil4_gemv_swiglu_batch(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_block, const float* x,
+                               float* gu, float* amax, int64_t F, int64_t K, int64_t batch, mth_stream_t stream);
+int mth_i2s_gemv_act_batch(const uint8_t* packed, float w_scale, const float* act, int64_t lda, const float* amax,
+                           float* inv_scale, float* y, int64_t M, int64_t K, int64_t batch, mth_stream_t stream);
+
 /* oil::math::add / mul (src/math.cpp:251-258, :269-276). */
 int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);
 int mth_mul(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream);

@@ -429,6 +429,49 @@ int mth_i2s_gemv_act(const uint8_t* packed, float w_scale, const float* act, con
                         "mth_i2s_gemv_act");
 }
 
+int64_t mth_swiglu_batch_parts(int64_t F) { return F > 0 && F < kMaxDim ? mth::oil4_bt_swiglu_parts(F) : 0; }
+
+int mth_oil4_gemv_swiglu_batch(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_block, const float* x,
+                               float* gu, float* amax, int64_t F, int64_t K, int64_t batch, mth_stream_t stream) {
+    REQUIRE(packed && codebooks && x && gu && amax, "mth_oil4_gemv_swiglu_batch: null pointer");
+    REQUIRE(F > 0 && K > 0 && F < kMaxDim && K < kMaxDim, "mth_oil4_gemv_swiglu_batch: bad sizes F=%lld K=%lld",
+            (long long)F, (long long)K);
+    REQUIRE(batch >= 2 && batch <= 16, "mth_oil4_gemv_swiglu_batch: batch=%lld outside 2..16", (long long)batch);
+    REQUIRE((((uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)x) & 15u) == 0,
+            "mth_oil4_gemv_swiglu_batch: packed, codebooks and x must be 16-byte aligned");
+    REQUIRE(mth::oil4_bt_swiglu_supported(F, K, cb_block, batch),
+            "mth_oil4_gemv_swiglu_batch: F=%lld K=%lld cb_block=%lld not supported (F %% 4 == 0, K %% 512 == 0, "
+            "512 <= K <= 8192, cb_block 0 or 128)",
+            (long long)F, (long long)K, (long long)cb_block);
+    void* partial = nullptr;
+    const size_t need = mth::oil4_bt_partial_bytes(2 * F, K);
+    const hipError_t e = workspace(S(stream), need, &partial);
+    if (e != hipSuccess) return workspace_fail("mth_oil4_gemv_swiglu_batch", e, need);
+    return check_launch(mth::launch_oil4_gemv_bt_swiglu(packed, codebooks, cb_block, x, mth::NormScale{}, gu, amax, F,
+                                                        K, batch, (float*)partial, S(stream)),
+                        "mth_oil4_gemv_swiglu_batch");
+}
+
+int mth_i2s_gemv_act_batch(const uint8_t* packed, float w_scale, const float* act, int64_t lda, const float* amax,
+                           float* inv_scale, float* y, int64_t M, int64_t K, int64_t batch, mth_stream_t stream) {
+    REQUIRE(packed && act && amax && inv_scale && y, "mth_i2s_gemv_act_batch: null pointer");
+    REQUIRE(M > 0 && K > 0 && M < (1ll << 31) && K <= 16384, "mth_i2s_gemv_act_batch: bad sizes M=%lld K=%lld",
+            (long long)M, (long long)K);
+    REQUIRE(batch >= 2 && batch <= 16, "mth_i2s_gemv_act_batch: batch=%lld outside 2..16", (long long)batch);
+    REQUIRE(lda >= K && lda % 4 == 0 && lda < kMaxDim, "mth_i2s_gemv_act_batch: lda=%lld (>= K, multiple of 4)",
+            (long long)lda);
+    REQUIRE((((uintptr_t)packed | (uintptr_t)act) & 15u) == 0,
+            "mth_i2s_gemv_act_batch: packed and act must be 16-byte aligned");
+    REQUIRE(mth::i2s_bt_supported(M, K, batch), "mth_i2s_gemv_act_batch: K=%lld not a multiple of 256", (long long)K);
+    void* partial = nullptr;
+    const size_t need = mth::i2s_bt_partial_bytes(M, K);
+    const hipError_t e = workspace(S(stream), need, &partial);
+    if (e != hipSuccess) return workspace_fail("mth_i2s_gemv_act_batch", e, need);
+    return check_launch(mth::launch_i2s_gemv_bt_f32act_y(packed, w_scale, act, lda, amax, mth::oil4_bt_swiglu_parts(K),
+                                                         inv_scale, y, M, K, batch, (float*)partial, S(stream)),
+                        "mth_i2s_gemv_act_batch");
+}
+
 int mth_add(const float* a, const float* b, float* c, int64_t n, mth_stream_t stream) {
     REQUIRE(a && b && c, "mth_add: null pointer");
     REQUIRE(n > 0 && n < kMaxDim, "mth_add: bad size");

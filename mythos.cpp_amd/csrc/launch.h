@@ -116,6 +116,10 @@ hipError_t launch_i2s_gemv_bt(const uint8_t* packed, float w_scale, const int8_t
 hipError_t launch_i2s_gemv_bt_f32act(const uint8_t* packed, float w_scale, const float* act, int64_t lda,
                                      const float* amax, int nmx, float* inv, float* y, int64_t M, int64_t K,
                                      int64_t batch, float* partial, Slices* out, hipStream_t s);
+// launch_i2s_gemv_bt_f32act with the slices reduced into y [batch][M].
+hipError_t launch_i2s_gemv_bt_f32act_y(const uint8_t* packed, float w_scale, const float* act, int64_t lda,
+                                       const float* amax, int nmx, float* inv, float* y, int64_t M, int64_t K,
+                                       int64_t batch, float* partial, hipStream_t s);
 hipError_t launch_i2s_gemv_bt_slices(const uint8_t* packed, float w_scale, const int8_t* act, const float* act_scale,
                                     float* y, int64_t M, int64_t K, int64_t batch, float* partial, Slices* out,
                                     hipStream_t s);

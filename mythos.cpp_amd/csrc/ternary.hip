@@ -1404,6 +1404,17 @@ hipError_t launch_i2s_gemv_bt_f32act(const uint8_t* packed, float w_scale, const
     return hipGetLastError();
 }
 
+hipError_t launch_i2s_gemv_bt_f32act_y(const uint8_t* packed, float w_scale, const float* act, int64_t lda,
+                                       const float* amax, int nmx, float* inv, float* y, int64_t M, int64_t K,
+                                       int64_t batch, float* partial, hipStream_t s) {
+    Slices out{};
+    const hipError_t e = launch_i2s_gemv_bt_f32act(packed, w_scale, act, lda, amax, nmx, inv, y, M, K, batch, partial,
+                                                   &out, s);
+    if (e != hipSuccess || out.n == 1) return e;
+    i2s_bt_reduce<<<ceil_div(batch * M, kWG), kWG, 0, s>>>(partial, w_scale, inv, y, (int)M, (int)batch, out.n);
+    return hipGetLastError();
+}
+
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o, int64_t M, int64_t N, int64_t K,
                            hipStream_t s) {
     i2s_gemm_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);

@@ -28,7 +28,8 @@ EXPORTS = (
     "mth_i2s_gemv", "mth_i2s_gemv_f32", "mth_i2s_gemm", "mth_i2s_gemm_vnni",
     "mth_tl1_gemm", "mth_tl2_gemm", "mth_tl_precompute_lut",
     "mth_rms_norm", "mth_add_rms_norm", "mth_silu", "mth_silu_mul", "mth_silu_mul_quant",
-    "mth_oil4_gemv_swiglu", "mth_i2s_gemv_act", "mth_add", "mth_mul",
+    "mth_oil4_gemv_swiglu", "mth_i2s_gemv_act", "mth_swiglu_batch_parts", "mth_oil4_gemv_swiglu_batch",
+    "mth_i2s_gemv_act_batch", "mth_add", "mth_mul",
     "mth_softmax", "mth_softmax_axis", "mth_axpby", "mth_gemv_f32", "mth_relu", "mth_gelu", "mth_scale",
     "mth_layer_norm",
     "mth_rope_tables", "mth_rope_kv", "mth_attention_decode", "mth_argmax",
@@ -85,6 +86,8 @@ _SIG = {
     "mth_silu_mul_quant": [VP, VP, VP, VP, I64, I64, I64, I64, VP],
     "mth_oil4_gemv_swiglu": [VP, VP, VP, VP, VP, I64, I64, VP],
     "mth_i2s_gemv_act": [VP, F32, VP, VP, VP, I64, I64, VP],
+    "mth_oil4_gemv_swiglu_batch": [VP, VP, I64, VP, VP, VP, I64, I64, I64, VP],
+    "mth_i2s_gemv_act_batch": [VP, F32, VP, I64, VP, VP, VP, I64, I64, I64, VP],
     "mth_add": [VP, VP, VP, I64, VP],
     "mth_mul": [VP, VP, VP, I64, VP],
     "mth_softmax": [VP, VP, I64, I64, VP],
@@ -109,6 +112,8 @@ _lib.mth_last_error.argtypes = []
 _lib.mth_last_error.restype = C.c_char_p
 _lib.mth_version.argtypes = []
 _lib.mth_version.restype = I32
+_lib.mth_swiglu_batch_parts.argtypes = [I64]
+_lib.mth_swiglu_batch_parts.restype = I64
 
 lib = _lib
 
@@ -322,6 +327,34 @@ def i2s_gemv_act(packed, w_scale, act, amax, y, M, K, stream=None):
     _check(_lib.mth_i2s_gemv_act(_ptr(packed, t.uint8, M * K // 4, "packed"), float(w_scale),
                                  _ptr(act, t.float32, K, "act"), _ptr(amax, t.float32, K // 8, "amax"),
                                  _ptr(y, t.float32, M, "y"), M, K, _stream(stream)))
+
+
+def swiglu_batch_parts(F):
+    """Block maxima per token written by oil4_gemv_swiglu_batch (one per 256 columns)."""
+    return int(_lib.mth_swiglu_batch_parts(F))
+
+
+def oil4_gemv_swiglu_batch(packed, codebooks, cb_block, x, gu, amax, F, K, batch, stream=None):
+    """Batches of 2..16: gate/up of one OIL4 weight of 2F rows and the SwiGLU;
+    act of token t in gu[t, :F] (gu is [batch][2F]), amax [batch][parts]."""
+    t = _torch()
+    nb = K // cb_block if cb_block else 1
+    _check(_lib.mth_oil4_gemv_swiglu_batch(
+        _ptr(packed, t.uint8, 2 * F * K // 2, "packed"),
+        _ptr(codebooks, t.int16, (2 * F * nb if cb_block else 1) * 16, "codebooks"), cb_block,
+        _ptr(x, t.float32, batch * K, "x"), _ptr(gu, t.float32, batch * 2 * F, "gu"),
+        _ptr(amax, t.float32, batch * swiglu_batch_parts(F), "amax"), F, K, batch, _stream(stream)))
+
+
+def i2s_gemv_act_batch(packed, w_scale, act, lda, amax, inv_scale, y, M, K, batch, stream=None):
+    """Batches of 2..16: I2_S GEMV of quantize_per_token(act rows, stride lda),
+    amax as from oil4_gemv_swiglu_batch; inv_scale [batch] = max|act| / 127."""
+    t = _torch()
+    _check(_lib.mth_i2s_gemv_act_batch(
+        _ptr(packed, t.uint8, M * K // 4, "packed"), float(w_scale), _ptr(act, t.float32, (batch - 1) * lda + K, "act"),
+        lda, _ptr(amax, t.float32, batch * swiglu_batch_parts(K), "amax"),
+        _ptr(inv_scale, t.float32, batch, "inv_scale"), _ptr(y, t.float32, batch * M, "y"), M, K, batch,
+        _stream(stream)))
 
 
 def add(a, b, c, n, stream=None):

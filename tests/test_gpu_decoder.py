@@ -488,3 +488,84 @@ def test_config5_b16_per_layer(kv, config5, oracle):
         check_layers(dec, orc, oracle, cfg, model, caches, prompts, pos,
                      sel=lambda b, l, pos=pos: (b + l) % 4 == 2 * pos % 4)
     dec.close()
+
+
+def scaled_down(model, div=128):
+    """The model with every down projection's scale divided by div (a power of
+    two: exact).  At hidden 4096 one int8 activation that the GPU's and the
+    oracle's FP32 sums (in different orders) round to opposite sides of a .5
+    boundary moves the logits by up to ~5e-4 at div 8 (measured at 2 and 8
+    layers; without such a flip the production path agrees to ~1e-6), by
+    1/16 of that at div 128 -- below the 1e-4 bar -- while the FFN as a whole
+    still moves the logits by far more than the bar (asserted where used)."""
+    return dict(model, layers=[dict(ly, down_scale=np.float32(ly["down_scale"] / div)) for ly in model["layers"]])
+
+
+def ffn_off(model):
+    """The model with every down projection's output 0 (scale 0)."""
+    return dict(model, layers=[dict(ly, down_scale=np.float32(0.0)) for ly in model["layers"]])
+
+
+def step_launches(cfg, batch):
+    """Kernel launches of the production decode step (the bench's path):
+    batch 1 -- embedding, per layer Q/K/V, attention, O with the residual
+    epilogue, gate/up with the SwiGLU epilogue, down with the quantisation
+    and the residual epilogue; final norm, lm_head, two argmax launches.
+    Batches -- per layer two residual adds of the split norm (the first
+    layer's done by the embedding), Q/K/V, attention, O, gate/up, its slice
+    reduction with the SwiGLU, down with the quantisation inside; final norm,
+    the batched lm_head and its slice reduction, two argmax launches."""
+    L = cfg["layers"]
+    return 1 + 5 * L + 1 + 1 + 2 if batch == 1 else 1 + 8 * L - 1 + 1 + 2 + 2
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_config5_production_path(batch, config5, oracle):
+    """The path bench.py times, at full config 5 (32 layers, hidden 4096,
+    ffn 11008, vocab 32000) with real ternary down weights: graph replay, no
+    taps, so the RMSNorms split over the launches around them, the SwiGLU in
+    the gate/up epilogue (batch 1) or its slice reduction (batch 16) and the
+    int8 quantisation inside the down projection.  The launch count pins
+    that path; the logits of every sequence after each of three
+    teacher-forced steps must be within 1e-4 of the oracle's (down scales
+    divided by 128, scaled_down; the FFN's own effect on the logits is
+    asserted to be > 1e-2).  KV cache FP32: a bf16 cache adds rounding
+    flips of K/V elements (values the two sides' FP32 sums put on opposite
+    sides of a bf16 rounding boundary) that alone move 8-layer logits by
+    ~1e-3; the bf16 store and load are checked element by element through
+    the taps in test_config5_b16_per_layer."""
+    cfg, model = config5
+    model = scaled_down(model)
+    steps, kv = 3, "f32"
+    prompts = synth.decoder_prompts(cfg, batch, steps, config=90 + batch)
+    dec = make(cfg, model, batch, kv)
+    dec.start(prompts)
+    ocfg = oracle_cfg(cfg, kv, max_seq=steps)
+    orc = oracle.decoder(ocfg, model)
+    caches = [orc.new_cache() for _ in range(batch)]
+    for pos in range(steps):
+        print(f"decoder config 5 production path b={batch}: step {pos}", flush=True)
+        dec.step(1, graph=True)
+        if pos == 0:
+            assert dec.launches_per_step == step_launches(cfg, batch)
+        got = dec.logits()
+        want = [orc.step(*caches[b], pos, int(prompts[b, pos]), threads=THREADS) for b in range(batch)]
+        errs = [rel(got[b], want[b]) for b in range(batch)]
+        assert max(errs) < TOL, (pos, errs)
+        if pos == 0:
+            no_ffn = oracle.decoder(ocfg, ffn_off(model))
+            assert rel(no_ffn.step(*no_ffn.new_cache(), 0, int(prompts[0, 0]), threads=THREADS), want[0]) > 1e-2
+    dec.close()
+
+
+@pytest.mark.parametrize("B", [4, 16])
+def test_config5_prefill(B, oracle):
+    """mth_decoder_prefill at config 5's widths (hidden 4096, ffn 11008,
+    32 heads of 128, vocab 32000) with two layers and a 64-token prompt: B =
+    16 makes one chunk of 1024 rows; B = 4 one of 256.  Last-position logits,
+    every layer's K/V rows 0..63 and two decode steps after it against the
+    oracle (down scales divided by 128, scaled_down; FP32 KV cache, as in
+    test_config5_production_path)."""
+    cfg = synth.decoder_config(layers=2, max_seq=72)
+    model = scaled_down(synth.decoder_model(cfg, config=93))
+    prefill_vs_oracle(cfg, model, B, 64, "f32", oracle, seed=94 + B)

@@ -325,6 +325,90 @@ def test_i2s_gemv_act_random_shapes(M, K, oracle, mth, dev):
     test_i2s_gemv_act_bit_exact(M, K, oracle, mth, dev)
 
 
+# ---------------------------------------- FFN in two launches (batches) --
+@pytest.mark.parametrize("F,K,H,batch", [
+    (11008, 4096, 4096, 16),   # config 5 at batch 16: 4 K slices of gate/up, 8 slices over 2 rounds of down
+    (11008, 4096, 4096, 2),    # config 5 at batch 2
+    (1024, 512, 512, 5),       # one K slice each (the in-place reduction, one round)
+    (300, 2048, 200, 3),       # F not a multiple of 256, ragged down rows
+])
+def test_ffn_batch_bit_exact(F, K, H, batch, oracle, mth, dev):
+    """The decoder's batched FFN pair through the C ABI, with real (all four
+    codes) ternary down weights: act bit-identical to the batched OIL4 GEMV
+    over 2F rows followed by mth_silu_mul, the block maxima exact, the GEMV
+    against the oracle; the down projection of the GPU's act (quantised
+    inside the launch from the block maxima) bit-exact against the oracle's
+    quantize_per_token + i2s_gemv, and its act scales equal to the oracle's."""
+    import torch
+    print(f"ffn batch F={F} K={K} H={H} batch={batch}", flush=True)
+    packed, cbs, x = synth.oil4(2 * F, K, batch, 128, config=5)
+    p, c, xd = to_dev(packed, dev), to_dev(cbs, dev), to_dev(x, dev)
+    parts = mth.swiglu_batch_parts(F)
+    assert parts == -(-F // 256)
+    gu, amax = empty(batch * 2 * F, torch.float32, dev), empty(batch * parts, torch.float32, dev)
+    mth.oil4_gemv_swiglu_batch(p, c, 128, xd, gu, amax, F, K, batch)
+    y, ref_act = empty(batch * 2 * F, torch.float32, dev), empty(batch * F, torch.float32, dev)
+    mth.oil4_gemv(p, c, 128, xd, y, 2 * F, K, batch)
+    mth.silu_mul(y, y[F:], ref_act, batch, F, 2 * F, 2 * F)
+    g = np.random.default_rng(F + K + batch)
+    wdown = g.integers(0, 256, (H, F // 4), dtype=np.uint8)
+    # F % 256 != 0: pad the down projection's K to a multiple of 256 with zero activations
+    Kd = -(-F // 256) * 256
+    if Kd != F:
+        wdown = np.concatenate([wdown, np.full((H, (Kd - F) // 4), 0x55, np.uint8)], axis=1)
+        gu2 = torch.zeros(batch * 2 * Kd, dtype=torch.float32, device=dev)
+        gu2.view(batch, 2 * Kd)[:, :F] = gu.view(batch, 2 * F)[:, :F]
+        act_in, lda = gu2, 2 * Kd
+    else:
+        act_in, lda = gu, 2 * F
+    down, inv = empty(batch * H, torch.float32, dev), empty(batch, torch.float32, dev)
+    mth.i2s_gemv_act_batch(to_dev(wdown, dev), 0.0159577, act_in, lda, amax, inv, down, H, Kd, batch)
+    torch.cuda.synchronize()
+    got = gu.cpu().numpy().reshape(batch, 2 * F)[:, :F]
+    want = ref_act.cpu().numpy().reshape(batch, F)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    pad = np.zeros((batch, parts * 256), np.float32)
+    pad[:, :F] = np.abs(want)
+    assert np.array_equal(amax.cpu().numpy().reshape(batch, parts), pad.reshape(batch, parts, 256).max(2))
+    ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, 2 * F, K, batch, 128, threads=8)
+    W = synth.dequant_oil4(packed, cbs, 2 * F, K, 128)
+    absw = np.abs(W).astype(np.float64) @ np.abs(x.astype(np.float64)).T
+    fp32_close(y.cpu().numpy().reshape(batch, 2 * F), ref, absw.T, 1e-5, "oil4_gemv (2F rows, batch)")
+    a = np.zeros((batch, Kd), np.float32)
+    a[:, :F] = got
+    _, _, inv_ref = oracle.quantize_per_token(a, batch, Kd)
+    assert np.array_equal(inv.cpu().numpy(), inv_ref)
+    ref_down = oracle.i2s_gemv_f32(wdown.ravel(), 0.0159577, a, H, Kd, batch, threads=8)
+    assert np.array_equal(down.cpu().numpy().reshape(batch, H), ref_down)
+
+
+@pytest.mark.parametrize("M,K,batch", [(4096, 11008 // 256 * 256, 16), (130, 16384, 2), (64, 256, 9)])
+def test_i2s_gemv_act_batch_inputs(M, K, batch, oracle, mth, dev):
+    """mth_i2s_gemv_act_batch on activations of very different magnitudes
+    per token (1e-30 .. 1e6, and an all-zero token: the 1e-10 floor), the
+    largest K (64 block maxima), a row stride larger than K."""
+    import torch
+    print(f"i2s_gemv_act_batch M={M} K={K} batch={batch}", flush=True)
+    g = np.random.default_rng(M + K + batch)
+    packed = g.integers(0, 256, (M, K // 4), dtype=np.uint8)
+    lda = K + 36
+    act = np.zeros((batch, lda), np.float32)
+    mags = [1e-30, 1e6, 0.0, 1.0, 3e-4, 7.5, 1e-12, 40.0, 1e3] * 2
+    for t in range(batch):
+        act[t, :K] = (g.normal(0, 1, K) * mags[t]).astype(np.float32)
+    parts = -(-K // 256)
+    amax = np.abs(act[:, :K]).reshape(batch, parts, 256).max(2)
+    y, inv = empty(batch * M, torch.float32, dev), empty(batch, torch.float32, dev)
+    mth.i2s_gemv_act_batch(to_dev(packed, dev), 0.0159577, to_dev(act.ravel(), dev), lda, to_dev(amax, dev), inv, y,
+                           M, K, batch)
+    torch.cuda.synchronize()
+    a = np.ascontiguousarray(act[:, :K])
+    _, _, inv_ref = oracle.quantize_per_token(a, batch, K)
+    assert np.array_equal(inv.cpu().numpy(), inv_ref)
+    ref = oracle.i2s_gemv_f32(packed.ravel(), 0.0159577, a, M, K, batch, threads=8)
+    assert np.array_equal(y.cpu().numpy().reshape(batch, M), ref)
+
+
 def test_ffn_building_blocks_reject_shapes(mth, dev):
     import torch
     p = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
