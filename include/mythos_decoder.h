@@ -41,6 +41,10 @@ extern "C" {
 typedef struct mth_decoder mth_decoder;
 
 typedef struct {
+    /* sizeof(mth_decoder_config) as the caller was compiled: mth_decoder_create
+     * rejects any other value, so a caller built against another layout of
+     * this struct fails cleanly instead of being misread (ABI major 2). */
+    int64_t struct_size;
     int64_t vocab, hidden, layers, heads, kv_heads, head_dim, ffn;
     int64_t max_seq;   /* KV-cache positions per sequence (prompt + generated) */
     int64_t cb_block;  /* OIL4 codebook block length (0 = one codebook per tensor) */

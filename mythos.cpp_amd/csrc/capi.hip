@@ -152,7 +152,9 @@ int api_ok() { return ok(); }
 extern "C" {
 
 const char* mth_last_error(void) { return g_err; }
-int mth_version(void) { return (1 << 16) | 1; }
+// 2.0: mth_decoder_config gained struct_size (first member); 1.x callers of
+// mth_decoder_create are rejected by its size check.
+int mth_version(void) { return (2 << 16) | 0; }
 
 int mth_workspace_reserve(int64_t bytes, mth_stream_t stream) {
     REQUIRE(bytes >= 0 && bytes < kMaxDim, "mth_workspace_reserve: bad size %lld", (long long)bytes);

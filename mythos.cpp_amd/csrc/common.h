@@ -76,6 +76,10 @@ struct AddOp {
 struct MaxOp {
     __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
 };
+// Maximum of unsigned values (e.g. the bit patterns of magnitudes).
+struct UMaxOp {
+    __device__ __forceinline__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
 
 // Transposed reduction of R per-lane values over the 64 lanes: halving
 // exchanges (lanes l ^ 32, l ^ 16, l ^ 8: each lane keeps the rows of its

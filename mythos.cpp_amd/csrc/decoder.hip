@@ -449,6 +449,12 @@ extern "C" {
 int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
     if (!cfg || !out) return api_fail(MTH_EINVAL, "mth_decoder_create: null pointer");
     *out = nullptr;
+    if (cfg->struct_size != (int64_t)sizeof(mth_decoder_config))
+        return api_fail(MTH_EINVAL,
+                        "mth_decoder_create: struct_size=%lld, this library's mth_decoder_config has %zu bytes "
+                        "(caller built against another header version; ABI %d.%d)",
+                        (long long)cfg->struct_size, sizeof(mth_decoder_config), mth_version() >> 16,
+                        mth_version() & 0xffff);
     const mth_decoder_config& c = *cfg;
     if (c.vocab <= 0 || c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 ||
         c.head_dim <= 0 || c.max_seq <= 0 || c.vocab >= (1ll << 31) || c.hidden >= (1ll << 24) ||

@@ -402,7 +402,9 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
     // x first (and the norm's partial sums), then (once every wave of the
     // workgroup has issued them) the weight streams: the CU returns loads in
     // issue order.
-    const bool xl = lane * 16 < KW;
+    // x: KW / 64 values per lane (every lane), XS B-fragment slots of 8
+    constexpr int XS = KW / 512;
+    static_assert(KW % 512 == 0 && XS >= 1 && XS <= 2, "oil4_gemv_v2: 2 or 4 phases of 256 columns per wave");
     constexpr int VW = PAIR ? (16 + NW - 1) / NW : 1;  // norm_scale<16> waves taken by this wave
     double np1[VW];
     if (PAIR && sw.ns.ssp) {
@@ -411,9 +413,9 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
         for (int i = 0; i < VW; ++i)
             np1[i] = last >= 0 ? sw.ns.ssp[min((wave + i * NW) * 64 + lane, last)] : 0.0;
     }
-    float4 xq[4];
+    float4 xq[2 * XS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xq[i] = ldf4(x + k0 + (xl ? lane * 16 : 0) + 4 * i);
+    for (int i = 0; i < 2 * XS; ++i) xq[i] = ldf4(x + k0 + lane * 8 * XS + 4 * i);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -439,37 +441,50 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
     }
 
     // ---- x slice -> power-of-two scale -> FP16 hi/lo B fragments --------
-    // lane l holds columns 16l .. 16l+15 = phase l/16, group (l%16)/4,
-    // MFMAs 2(l%4) and 2(l%4)+1
+    // lane l holds columns 8 XS l .. 8 XS l + 8 XS - 1; slot s of them starts
+    // at column c0 = 8 (XS l + s): phase c0 / 256, group (c0 % 256) / 64,
+    // MFMA (c0 % 64) / 8.  max|x| is taken over the magnitudes' bit patterns
+    // (no NaN canonicalisation; a NaN, above every finite pattern, gives
+    // shift 0, and the output is NaN either way).
     uint8_t* wl = lds + wave * L::per_wave;
     _Float16* xw = (_Float16*)wl;
-    float xv[16];
+    float xv[8 * XS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        xv[4 * i] = xl ? xq[i].x : 0.0f; xv[4 * i + 1] = xl ? xq[i].y : 0.0f;
-        xv[4 * i + 2] = xl ? xq[i].z : 0.0f; xv[4 * i + 3] = xl ? xq[i].w : 0.0f;
+    for (int i = 0; i < 2 * XS; ++i) {
+        xv[4 * i] = xq[i].x, xv[4 * i + 1] = xq[i].y, xv[4 * i + 2] = xq[i].z, xv[4 * i + 3] = xq[i].w;
     }
-    float mx = 0.0f;
+    uint32_t mb = 0, mn = 0xffffffffu;  // max |x| bits; min nonzero |x| bits - 1 (0 -> all ones)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(xv[i]));
-    const int sh = fp16_scale_shift(wave_max(mx));  // max|x|*2^sh < 2^15
-    if (xl) {
-        const int p = lane >> 4, qq = (lane & 15) >> 2;
+    for (int i = 0; i < 8 * XS; ++i) {
+        const uint32_t ab = __float_as_uint(xv[i]) & 0x7fffffffu;
+        mb = max(mb, ab);
+        mn = min(mn, ab - 1u);
+    }
+    const uint32_t wmax = group_reduce<64>(mb, UMaxOp{});
+    const int sh = fp16_scale_shift(__uint_as_float(wmax));  // max|x|*2^sh < 2^15
+    // A nonzero x_k more than 2^28 below max|x| (binade difference > 28) has
+    // an FP16 hi part that is subnormal or 0: its product keeps fewer than 11
+    // bits, and an infinite codebook entry times a hi part of 0 gives NaN
+    // where the reference's w * x_k is +-Inf (src/kernel_oil4.cpp:50).  Such a
+    // wave (also any wave whose x slice holds Inf or NaN) recomputes its rows
+    // with FP32 products below.
+    const bool lossy = __builtin_amdgcn_ballot_w64(
+                           mn != 0xffffffffu && (int)(wmax >> 23) - (int)((mn + 1u) >> 23) > 28) != 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int m = 2 * (lane & 3) + h;
-            half8 vh, vl;
+    for (int h = 0; h < XS; ++h) {
+        const int c0 = 8 * (XS * lane + h);
+        const int p = c0 >> 8, qq = (c0 & 255) >> 6, m = (c0 & 63) >> 3;
+        half8 vh, vl;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float xs = ldexpf(xv[8 * h + oil4_elem_col(t)], sh);
-                const _Float16 hh = (_Float16)xs;
-                vh[t] = hh;
-                vl[t] = (_Float16)(xs - (float)hh);
-            }
-            const int slot = ((p * 8 + m) * 4 + qq) * 8;
-            *(half8*)&xw[slot] = vh;
-            *(half8*)&xw[L::lo_off / 2 + slot] = vl;
+        for (int t = 0; t < 8; ++t) {
+            const float xs = ldexpf(xv[8 * h + oil4_elem_col(t)], sh);
+            const _Float16 hh = (_Float16)xs;
+            vh[t] = hh;
+            vl[t] = (_Float16)(xs - (float)hh);
         }
+        const int slot = ((p * 8 + m) * 4 + qq) * 8;
+        *(half8*)&xw[slot] = vh;
+        *(half8*)&xw[L::lo_off / 2 + slot] = vl;
     }
     wave_lds_order();
     __builtin_amdgcn_sched_barrier(0);  // no weight-data wait above this point
@@ -500,6 +515,29 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
     for (int i = 0; i < 4; ++i) {
         const float s = oil4_hi_lo(acc[i], lane_xor1(acc[i]));
         if (j == 0) part[wave * 16 + 4 * q + i] = ldexpf(s, -sh);
+    }
+    if (lossy) {
+        // the wave's 16 rows again with FP32 products (the reference's
+        // arithmetic): lane l takes columns 8 XS l .. of each row, the lanes'
+        // sums are added across the wave
+        const int nbr = K >> 7;
+        for (int r = 0; r < 16; ++r) {
+            const int row = PAIR ? (r < 8 ? blockIdx.x * 8 + r : sw.F + blockIdx.x * 8 + r - 8) : min(row0 + r, M - 1);
+            float sum = 0.0f;
+#pragma unroll
+            for (int h = 0; h < XS; ++h) {
+                const int c0 = k0 + 8 * (XS * lane + h);
+                const uint32_t d = *(const uint32_t*)(nib + (int64_t)row * (K >> 1) + (c0 >> 1));
+                const uint16_t* cb = SHARED ? cbs : cbs + ((int64_t)row * nbr + (c0 >> 7)) * 16;
+                const half8 wv = lookup8(d, cb_planes(ld16(cb), ld16(cb + 8)));
+                const float4 x0 = ldf4(x + c0), x1 = ldf4(x + c0 + 4);
+                const float xf[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int t = 0; t < 8; ++t) sum = fmaf((float)wv[t], xf[oil4_elem_col(t)], sum);
+            }
+            sum = group_reduce<64>(sum, AddOp{});
+            if (lane == 0) part[wave * 16 + r] = sum;
+        }
     }
     __syncthreads();
     if (PAIR) {

@@ -128,10 +128,12 @@ __device__ __forceinline__ half8 lookup8_natural(uint32_t d, const CbPlanes& p) 
 
 // DPP row rotation inside each 16-lane row (CTRL 0x121..0x12F = row_ror:1..15).
 // The empty asm pins the read in the convergent code: a DPP read sunk under a
-// partial exec mask would see its source lane disabled.
+// partial exec mask would see its source lane disabled.  mov_dpp has no
+// "old" operand (a rotation gives every lane a source), so the compiler
+// emits no initialising move per read.
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_row(uint32_t v) {
-    uint32_t r = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+    uint32_t r = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
     asm volatile("" : "+v"(r));
     return r;
 }

@@ -29,8 +29,8 @@ CONFIG_KEYS = ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "ff
 
 
 class Config(C.Structure):
-    _fields_ = [(k, C.c_int64) for k in CONFIG_KEYS] + [("eps", C.c_float), ("theta", C.c_float),
-                                                         ("kv_dtype", C.c_int64)]
+    _fields_ = [("struct_size", C.c_int64)] + [(k, C.c_int64) for k in CONFIG_KEYS] + \
+               [("eps", C.c_float), ("theta", C.c_float), ("kv_dtype", C.c_int64)]
 
 
 KV_DTYPES = {"f32": 0, "bf16": 1}
@@ -85,8 +85,8 @@ class Decoder:
         self.cfg = dict(cfg, max_batch=max_batch)
         self.device = device
         self.kv_dtype = kv_dtype
-        c = Config(*[int(self.cfg[k]) for k in CONFIG_KEYS], float(cfg["eps"]), float(cfg["theta"]),
-                   KV_DTYPES[kv_dtype])
+        c = Config(C.sizeof(Config), *[int(self.cfg[k]) for k in CONFIG_KEYS], float(cfg["eps"]),
+                   float(cfg["theta"]), KV_DTYPES[kv_dtype])
         h = VP()
         _check(_lib.mth_decoder_create(C.byref(c), C.byref(h)))
         self._h = h

@@ -59,7 +59,7 @@ def test_file_reader_header_matches_exports():
 
 
 def test_version(mth):
-    assert mth.version() >> 16 == 1
+    assert mth.version() >> 16 == 2   # 2.0: mth_decoder_config.struct_size
 
 
 NULL = None
@@ -166,14 +166,22 @@ def test_decoder_argument_errors(mth):
     import decoder
     lib = mth.lib
     h = C.c_void_p()
-    cfg = decoder.Config(1000, 256, 2, 2, 2, 128, 512, 16, 128, 1, 1e-5, 1e4)
+    size = C.sizeof(decoder.Config)
+    cfg = decoder.Config(size, 1000, 256, 2, 2, 2, 128, 512, 16, 128, 1, 1e-5, 1e4)
     bad = [dict(max_batch=17), dict(head_dim=96), dict(heads=3), dict(cb_block=100), dict(hidden=254),
-           dict(max_seq=0)]
+           dict(max_seq=0), dict(struct_size=size - 8), dict(struct_size=1000)]
     for b in bad:
-        c = decoder.Config(*[b.get(k, getattr(cfg, k)) for k in decoder.CONFIG_KEYS], cfg.eps, cfg.theta)
+        c = decoder.Config(b.get("struct_size", size), *[b.get(k, getattr(cfg, k)) for k in decoder.CONFIG_KEYS],
+                           cfg.eps, cfg.theta)
         rc = lib.mth_decoder_create(C.byref(c), C.byref(h))
         assert rc in (mth.MTH_EINVAL, mth.MTH_EUNSUPPORTED), (b, rc)
         assert mth.last_error().startswith("mth_decoder_create"), mth.last_error()
+        if "struct_size" in b:
+            assert "struct_size" in mth.last_error(), mth.last_error()
+    # a caller of the 1.x header (no struct_size: vocab first) is refused
+    old = (C.c_int64 * 11)(1000, 256, 2, 2, 2, 128, 512, 16, 128, 1, 0)
+    assert lib.mth_decoder_create(C.cast(old, C.POINTER(decoder.Config)), C.byref(h)) == mth.MTH_EINVAL
+    assert mth.version() >> 16 == 2
     assert lib.mth_decoder_step(None, 1, 1, None) == mth.MTH_EINVAL
     assert lib.mth_decoder_start(None, P, 1, 1, None) == mth.MTH_EINVAL
     assert lib.mth_decoder_read(None, None, None, None) == mth.MTH_EINVAL

@@ -170,3 +170,73 @@ def test_oil4_prefill_integer_bit_exact(path, M, N, K, block, oracle, mth, dev):
     torch.cuda.synchronize()
     ref16, _ = oracle.oil4_gemm_prefill(a, packed, cbs, M, N, K, block, threads=8)
     assert np.array_equal(c.view(torch.int16).cpu().numpy().view(np.uint16).reshape(M, N), ref16)
+
+
+@pytest.mark.parametrize("path,M,K,batch,block", GEMV_PATHS)
+def test_oil4_gemv_x_wide_range(path, M, K, batch, block, oracle, mth, dev):
+    """x with magnitudes spread over 2^-70 .. 2^6 (every binade, both signs,
+    some exact zeros): the FP16 hi/lo split of the MFMA paths loses the
+    bits of values far below max|x|, by at most max|c| max|x| 2^-40 per
+    product, which the 1e-5 bar of sum|w*x| absorbs; the batch-1 kernel
+    recomputes such waves with FP32 products."""
+    import torch
+    print(f"oil4 wide-range x path={path} M={M} K={K} batch={batch}", flush=True)
+    g = np.random.default_rng(zlib.crc32(f"{path}/wide".encode()))
+    packed = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    cbs = codebooks("edges", M, K // block, 11)
+    x = (g.choice([-1.0, 1.0], (batch, K)) * np.exp2(g.uniform(-70, 6, (batch, K)))).astype(np.float32)
+    x[:, ::37] = 0.0
+    y = empty(batch * M, torch.float32, dev)
+    mth.oil4_gemv(to_dev(packed, dev), to_dev(cbs, dev), block, to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, M, K, batch, block, threads=8)
+    W = synth.dequant_oil4(packed, cbs, M, K, block).astype(np.float64)
+    absw = (np.abs(W) @ np.abs(x.astype(np.float64)).T).T
+    fp32_close(y.cpu().numpy().reshape(batch, M), ref, absw, 1e-5, f"{path}/wide")
+
+
+# paths whose products come from an FP16 hi/lo split of x without an FP32
+# fallback (batch >= 2, codebook blocks of 256): an infinite codebook entry
+# times an x_k whose hi part underflows to 0 gives NaN, the reference +-Inf
+HILO_NO_FALLBACK = {"mfma", "bt"}
+
+
+@pytest.mark.parametrize("path,M,K,batch,block", GEMV_PATHS)
+def test_oil4_gemv_inf_times_tiny_x(path, M, K, batch, block, oracle, mth, dev):
+    """Every infinite codebook entry is selected only at columns where x is
+    2^-60 times smaller than the rest, so the reference's products there are
+    +-Inf (src/kernel_oil4.cpp:50).  The batch-1 kernel (its FP32 fallback),
+    the FP32 and generic kernels give the oracle's +-Inf; the hi/lo kernels
+    without a fallback give NaN in exactly those rows (pinned, documented)."""
+    import torch
+    print(f"oil4 inf x tiny path={path} M={M} K={K} batch={batch}", flush=True)
+    g = np.random.default_rng(zlib.crc32(f"{path}/inftiny".encode()))
+    nblk = K // block
+    cbs = codebooks("inf", M, nblk, 13).reshape(M, nblk, 16)
+    nib = g.integers(0, 16, (M, K), dtype=np.uint8)
+    x = g.normal(0, 1, (batch, K)).astype(np.float32)
+    x[:, 1::2] *= np.float32(2.0 ** -60)              # odd columns tiny
+    isinf = np.isinf(synth.fp16_bits_to_f32(cbs.ravel()).reshape(M, nblk, 16))
+    for r, b, e in zip(*np.nonzero(isinf)):            # infinite entry e of block b: only at odd columns
+        cols = np.arange(b * block, (b + 1) * block)
+        even = cols[(cols % 2 == 0) & (nib[r, cols] == e)]
+        nib[r, even] = (e + 1) % 16
+        nib[r, b * block + 1] = e                      # and used at least once
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    cbs = cbs.ravel()
+    y = empty(batch * M, torch.float32, dev)
+    mth.oil4_gemv(to_dev(packed, dev), to_dev(cbs, dev), block, to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, M, K, batch, block, threads=8)
+    got = y.cpu().numpy().reshape(batch, M)
+    with np.errstate(invalid="ignore", over="ignore"):
+        W = synth.dequant_oil4(packed, cbs, M, K, block).astype(np.float64)
+        absw = (np.abs(W) @ np.abs(x.astype(np.float64)).T).T
+    inf_rows = np.isinf(ref)
+    assert inf_rows.any()
+    if path in HILO_NO_FALLBACK:
+        assert np.isnan(got[inf_rows]).all(), f"{path}: pinned NaN-for-Inf divergence changed"
+        fin = np.isfinite(ref)
+        fp32_close(got[fin], ref[fin], absw[fin], 1e-5, f"{path}/inftiny finite rows")
+    else:
+        nonfinite_close(got, ref, absw, f"{path}/inftiny")
