@@ -9,9 +9,10 @@
  * never accumulated.
  *
  * Workspace.  The batched GEMVs (mth_oil8_gemv, mth_oil4_gemv, mth_i2s_gemv
- * with batch >= 2), mth_argmax, mth_oil4_gemm_prefill (an FP16 copy of A in
- * MFMA fragment order, ceil(M/16)*16*K*2 bytes, for K % 256 == 0, codebook
- * blocks of a multiple of 128 and N a multiple of 64, 96 or 112) and
+ * with batch >= 2), mth_argmax, mth_oil4_gemm_prefill (per-row shifts of A,
+ * 4 bytes per row, and an FP16 copy of A in MFMA fragment order,
+ * ceil(M/16)*16*K*2 bytes, for K % 256 == 0, codebook blocks of a multiple
+ * of 128 and N a multiple of 64, 96 or 112) and
  * mth_i2s_gemm_vnni (permuted activations,
  * for its MFMA shapes) keep intermediate data in a device workspace
  * the library owns, one per (device, stream).  The first call that needs more
@@ -124,9 +125,14 @@ int mth_oil4_gemv_noalloc(const uint8_t* packed, const uint16_t* codebooks, int6
  * definition): C[m*N + n] = bf16( sum_k A[m*K + k] * W[n][k] ), A bf16
  * [M][K] row-major, W OIL4 [N][K] with per-block codebooks as in
  * mth_oil4_gemv, FP32 accumulation, C bf16 [M][N] (round to nearest even).
- * Weights are dequantised to FP16 (exact) and activations converted
- * bf16 -> FP16 (exact for |a| in [2^-14, 65504]; smaller magnitudes lose
- * bits as FP16 subnormals, larger ones overflow). */
+ * Weights are dequantised to FP16 (exact).  Each row of A is scaled by a
+ * power of two that brings its maximum into [2^14, 2^15), converted
+ * bf16 -> FP16 (exact for every value within 2^-31 of the row's maximum; a
+ * row holding Inf or NaN is not scaled) and the row of C scaled back
+ * exactly before its bf16 rounding, so activations of any magnitude keep
+ * their bits.  K % 32 == 0, cb_block % 32 == 0, 16-byte aligned inputs
+ * (MTH_EUNSUPPORTED otherwise).  Uses the stream's workspace (4 bytes per row
+ * of A, plus an FP16 copy of A for the tile shapes above). */
 int mth_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* packed, const uint16_t* codebooks,
                           int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
                           mth_stream_t stream);

@@ -259,21 +259,23 @@ int mth_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* packed, const u
     REQUIRE(cb_block > 0 && K % cb_block == 0, "mth_oil4_gemm_prefill: K=%lld not a multiple of cb_block=%lld",
             (long long)K, (long long)cb_block);
     const bool aligned = (((uintptr_t)a_bf16 | (uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)c_bf16) & 15u) == 0;
-    const size_t need = aligned ? mth::oil4_prefill_workspace_bytes(M, N, K, cb_block) : 0;
-    if (need) {
-        void* a16 = nullptr;
-        const hipError_t e = workspace(S(stream), need, &a16);
-        if (e != hipSuccess) return workspace_fail("mth_oil4_gemm_prefill", e, need);
-        return check_launch(mth::launch_oil4_gemm_prefill_a16(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K,
-                                                             (uint16_t*)a16, S(stream)),
-                            "mth_oil4_gemm_prefill");
-    }
     if (!aligned || !mth::oil4_gemm_prefill_supported(M, N, K, cb_block))
         return fail(MTH_EUNSUPPORTED,
                     "mth_oil4_gemm_prefill: M=%lld N=%lld K=%lld cb_block=%lld not supported "
                     "(needs K %% 32 == 0, cb_block %% 32 == 0, 16-byte aligned inputs)",
                     (long long)M, (long long)N, (long long)K, (long long)cb_block);
-    return check_launch(mth::launch_oil4_gemm_prefill(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K, S(stream)),
+    // workspace: the per-row shifts of A, then (FP16-A kernels) A in FP16
+    const size_t a16 = mth::oil4_prefill_workspace_bytes(M, N, K, cb_block);
+    const size_t need = mth::oil4_prefill_shift_bytes(M) + a16;
+    void* ws = nullptr;
+    const hipError_t e = workspace(S(stream), need, &ws);
+    if (e != hipSuccess) return workspace_fail("mth_oil4_gemm_prefill", e, need);
+    if (a16)
+        return check_launch(mth::launch_oil4_gemm_prefill_a16(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K, ws,
+                                                             S(stream)),
+                            "mth_oil4_gemm_prefill");
+    return check_launch(mth::launch_oil4_gemm_prefill(a_bf16, packed, codebooks, cb_block, c_bf16, M, N, K, (int*)ws,
+                                                      S(stream)),
                         "mth_oil4_gemm_prefill");
 }
 

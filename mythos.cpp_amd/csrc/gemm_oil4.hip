@@ -6,7 +6,11 @@
 // (src/kernel_oil4.cpp:31-54) with per-128-weight-block FP16 codebooks.  Only
 // here is the work a dense contraction, so it runs on the matrix cores:
 //   * W tiles are dequantised in LDS: nibbles -> FP16 codebook value (exact);
-//   * A tiles are converted bf16 -> FP16 (exact for |a| in [2^-14, 65504]);
+//   * each row of A is scaled by a power of two 2^s (max|a| 2^s in [2^14,
+//     2^15), oil4_prefill_rowshift) and converted bf16 -> FP16, which is exact
+//     for every value within 2^-31 of the row's maximum; the output row is
+//     scaled back by 2^-s (exact) before its bf16 rounding, so no input range
+//     overflows FP16 or is flushed by it;
 //   * v_mfma_f32_16x16x32_f16 with FP32 accumulation; bf16 (RNE) output.
 // Tile: 128 (m) x 128 (n) x 32 (k) per 256-thread workgroup, 2x2 waves of
 // 64x64, register double-buffered global loads.
@@ -24,8 +28,9 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int LDA = BK + 8;  // halves per LDS row (80 B: 2-way bank aliasing at most)
 
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) {
-    const float lo = __uint_as_float(v << 16), hi = __uint_as_float(v & 0xffff0000u);
+// two bf16 -> two FP16 of a * 2^s (s: the row's shift)
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v, int s) {
+    const float lo = ldexpf(__uint_as_float(v << 16), s), hi = ldexpf(__uint_as_float(v & 0xffff0000u), s);
     const _Float16 hl = (_Float16)lo, hh = (_Float16)hi;
     return (uint32_t)__builtin_bit_cast(uint16_t, hl) | ((uint32_t)__builtin_bit_cast(uint16_t, hh) << 16);
 }
@@ -37,9 +42,33 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Per-row power-of-two shifts of A (one workgroup per row): rsh[m] = s with
+// max|a[m][*]| 2^s in [2^14, 2^15) (0 for an all-zero row or one holding
+// Inf / NaN), the scale fp16_scale_shift gives the decode kernels' x.
+__global__ __launch_bounds__(256) void oil4_prefill_rowshift(const uint16_t* __restrict__ a, int* __restrict__ rsh,
+                                                             int M, int K) {
+    __shared__ uint32_t red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const uint16_t* p = a + (int64_t)row * K;
+    uint32_t mb = 0;
+    // rounds of 2 chunks of 2048 columns, both loads issued before the first
+    // use (clamped to the row's last chunk, which is in bounds)
+    const int last = K - 8;
+    for (int c0 = 0; c0 < K; c0 += 4096) {
+        const uint4 v0 = ld16(p + min(c0 + 8 * tid, last)), v1 = ld16(p + min(c0 + 2048 + 8 * tid, last));
+        const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mb = max(mb, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+    }
+    mb = group_reduce<64>(mb, UMaxOp{});
+    if ((tid & 63) == 0) red[tid >> 6] = mb;
+    __syncthreads();
+    if (tid == 0) rsh[row] = fp16_scale_shift(__uint_as_float(max(max(red[0], red[1]), max(red[2], red[3])) << 16));
+}
+
 __global__ __launch_bounds__(256, 2) void oil4_gemm_prefill_k(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ nib, const uint16_t* __restrict__ cbs,
-    int cb_block, uint16_t* __restrict__ C, int M, int N, int K) {
+    int cb_block, uint16_t* __restrict__ C, int M, int N, int K, const int* __restrict__ rsh) {
     __shared__ __align__(16) _Float16 As[BM * LDA];
     __shared__ __align__(16) _Float16 Bs[BN * LDA];
     __shared__ __align__(16) uint16_t Cb[BN * 16];
@@ -55,6 +84,7 @@ __global__ __launch_bounds__(256, 2) void oil4_gemm_prefill_k(
     uint4 rc;         // codebook half: row tid>>1, entries (tid&1)*8..+7
     const int a_r = tid >> 2, a_c = (tid & 3) * 8;
     const int w_r = tid >> 1, w_h = tid & 1;
+    const int ash[2] = {rsh[min(m0 + a_r, M - 1)], rsh[min(m0 + 64 + a_r, M - 1)]};
 
     auto gload = [&](int k0) {
 #pragma unroll
@@ -84,8 +114,8 @@ __global__ __launch_bounds__(256, 2) void oil4_gemm_prefill_k(
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             uint4 v = ra[i];
-            v.x = bf16x2_to_f16x2(v.x); v.y = bf16x2_to_f16x2(v.y);
-            v.z = bf16x2_to_f16x2(v.z); v.w = bf16x2_to_f16x2(v.w);
+            v.x = bf16x2_to_f16x2(v.x, ash[i]); v.y = bf16x2_to_f16x2(v.y, ash[i]);
+            v.z = bf16x2_to_f16x2(v.z, ash[i]); v.w = bf16x2_to_f16x2(v.w, ash[i]);
             *(uint4*)&As[(a_r + 64 * i) * LDA + a_c] = v;
         }
         *(uint4*)&Cb[w_r * 16 + w_h * 8] = rc;
@@ -132,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void oil4_gemm_prefill_k(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + r;
-                if (m < M && n < N) C[(int64_t)m * N + n] = f32_to_bf16_rne(acc[i][j][r]);
+                if (m < M && n < N) C[(int64_t)m * N + n] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -rsh[m]));
             }
         }
 }
@@ -162,14 +192,15 @@ constexpr int PBM = 256, PBK = 64;
 // byte offset of 16-byte chunk c (0..7) of row r in a 128-byte-row tile
 __device__ __forceinline__ int pf_off(int r, int c) { return r * 128 + 16 * (c ^ ((r & 7) ^ ((r >> 3) & 1))); }
 
-// 8 bf16 -> 8 FP16 (through FP32: v_cvt_pk_f16_f32 rounds to nearest even)
-__device__ __forceinline__ half8 bf16x8_to_f16(uint4 v) {
+// 8 bf16 -> 8 FP16 of a * 2^s (through FP32: v_cvt_pk_f16_f32 rounds to
+// nearest even; exact inside FP16's range)
+__device__ __forceinline__ half8 bf16x8_to_f16(uint4 v, int s) {
     half8 r;
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        r[2 * i] = (_Float16)__uint_as_float(w[i] << 16);
-        r[2 * i + 1] = (_Float16)__uint_as_float(w[i] & 0xffff0000u);
+        r[2 * i] = (_Float16)ldexpf(__uint_as_float(w[i] << 16), s);
+        r[2 * i + 1] = (_Float16)ldexpf(__uint_as_float(w[i] & 0xffff0000u), s);
     }
     return r;
 }
@@ -184,7 +215,8 @@ struct PfLds {
 template <int BN>
 __global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __restrict__ A, const uint8_t* nib,
                                                             const uint16_t* cbs, int cb_block,
-                                                            uint16_t* __restrict__ C, int M, int N, int K) {
+                                                            uint16_t* __restrict__ C, int M, int N, int K,
+                                                            const int* __restrict__ rsh) {
     using L = PfLds<BN>;
     constexpr int NT = BN / 16;
     __shared__ __align__(16) uint8_t lds[L::bytes];
@@ -192,6 +224,9 @@ __global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __re
     const int m0 = blockIdx.y * PBM, n0 = blockIdx.x * BN;
     const int nb = K / cb_block;
     const int steps = K / PBK;
+    int ash[4];  // shifts of this lane's A fragment rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ash[i] = rsh[min(m0 + 64 * wave + 16 * i + (lane & 15), M - 1)];
 
     // ---- A: thread T loads 8 16-byte chunks per step (chunk id 256 i + T:
     // row id/8, 16-byte slot id%8 of that row in LDS, holding source chunk
@@ -267,7 +302,7 @@ __global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __re
                 half8 af[4], bfr[NT];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    af[i] = bf16x8_to_f16(*(const uint4*)(ab + pf_off(64 * wave + 16 * i + (lane & 15), c)));
+                    af[i] = bf16x8_to_f16(*(const uint4*)(ab + pf_off(64 * wave + 16 * i + (lane & 15), c)), ash[i]);
 #pragma unroll
                 for (int j = 0; j < NT; ++j) bfr[j] = *(const half8*)(wb + pf_off(16 * j + (lane & 15), c));
 #pragma unroll
@@ -288,7 +323,7 @@ __global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __re
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 64 * wave + 16 * i + 4 * (lane >> 4) + r;
-                if (m < M && n < N) C[(int64_t)m * N + n] = f32_to_bf16_rne(acc[i][j][r]);
+                if (m < M && n < N) C[(int64_t)m * N + n] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -rsh[m]));
             }
         }
 }
@@ -296,26 +331,47 @@ __global__ __launch_bounds__(256, 1) void oil4_prefill_mfma(const uint16_t* __re
 // ===================================================================
 // Prefill with FP16 A in MFMA fragment order (oil4_prefill_a16 + oil4_prefill_ws)
 // ===================================================================
-// oil4_prefill_a16 converts A (bf16, exact in FP16 inside its range) once per
-// call and writes it in the order the MFMA reads it: for 16-row group g and
-// 32-column chunk kc, the 64 lanes' 16-byte A fragments (lane l: row 16g + l %
-// 16, columns 32kc + 8(l / 16) .. + 7) are 1 KB contiguous.  Each fragment
-// load of the GEMM is then one 1 KB run (8 full 128-byte lines); read in the
-// natural row-major order, a fragment load touches 16 rows x 64 bytes (16
-// half-used lines at an 8 KB stride), which measured 96 -> 83 us at config 4.
-// Rows past M repeat row M - 1 (their outputs are never stored); the
-// workspace holds ceil(M / 16) * 16 rows.
+// oil4_prefill_a16 converts A (bf16) once per call and writes it in the
+// order the MFMA reads it: for 16-row group g and 32-column chunk kc, the 64
+// lanes' 16-byte A fragments (lane l: row 16g + l % 16, columns 32kc +
+// 8(l / 16) .. + 7) are 1 KB contiguous.  Each fragment load of the GEMM is
+// then one 1 KB run (8 full 128-byte lines); read in the natural row-major
+// order, a fragment load touches 16 rows x 64 bytes (16 half-used lines at
+// an 8 KB stride), which measured 96 -> 83 us at config 4.
+// One workgroup per row: the row's maximum first (its shift rsh[row], as
+// oil4_prefill_rowshift), then its 8-column pieces scaled, converted and
+// written to their fragment slots (the second read of the row hits the
+// cache).  The workgroups of one 16-row group run on one XCD (workgroup w on
+// XCD w % 8: w = 128 (g / 8) + 8 i + g % 8 for row i of group g), so the
+// group's 16-byte pieces of each 1 KB run meet in one L2.  Rows past M
+// repeat row M - 1 (their outputs are never stored); the workspace holds
+// ceil(M / 16) * 16 rows.
 __global__ __launch_bounds__(256) void oil4_prefill_a16(const uint16_t* __restrict__ a, uint16_t* __restrict__ a16,
-                                                        int M, int K, int64_t n16) {
-    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (o >= n16) return;
-    const int l = (int)(o & 63);
-    const int64_t q = o >> 6;
+                                                        int M, int K, int* __restrict__ rsh) {
+    __shared__ uint32_t red[4];
+    const int w = blockIdx.x, tid = threadIdx.x;
+    const int g = 8 * (w >> 7) + (w & 7), i = (w >> 3) & 15;
+    const int row = 16 * g + i;
+    if (16 * g >= M) return;  // a group past the last (grid rounded up to 8 groups)
+    const int src = min(row, M - 1);
+    const uint16_t* p = a + (int64_t)src * K;
+    const int nch = K / 8;  // 8-column pieces
+    uint32_t mb = 0;
+    for (int c = tid; c < nch; c += 256) {
+        const uint4 v = ld16(p + 8 * c);
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mb = max(mb, max(u[e] & 0x7fffu, (u[e] >> 16) & 0x7fffu));
+    }
+    mb = group_reduce<64>(mb, UMaxOp{});
+    if ((tid & 63) == 0) red[tid >> 6] = mb;
+    __syncthreads();
+    const int sh = fp16_scale_shift(__uint_as_float(max(max(red[0], red[1]), max(red[2], red[3])) << 16));
+    if (tid == 0 && row < M) rsh[row] = sh;
     const int kc32 = K / 32;
-    const int kc = (int)(q % kc32);
-    const int64_t g = q / kc32;
-    const int64_t r = min((int64_t)(16 * g + (l & 15)), (int64_t)M - 1);
-    *(half8*)(a16 + 8 * o) = bf16x8_to_f16(ld16(a + r * K + 32 * kc + 8 * (l >> 4)));
+    uint16_t* dst = a16 + (int64_t)g * kc32 * 512 + 8 * i;  // lane i of chunk 0
+    for (int c = tid; c < nch; c += 256)
+        *(half8*)(dst + (int64_t)(c >> 2) * 512 + 128 * (c & 3)) = bf16x8_to_f16(ld16(p + 8 * c), sh);
 }
 
 // ===================================================================
@@ -349,7 +405,7 @@ struct Pf2Lds {
 template <int BN, int PA, int BS>
 __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restrict__ A16, const uint8_t* nib,
                                                        const uint16_t* cbs, int cb_block, uint16_t* __restrict__ C,
-                                                       int M, int N, int K) {
+                                                       int M, int N, int K, const int* __restrict__ rsh) {
     using L = Pf2Lds<BN, BS>;
     constexpr int NT = BN / 16, PW = 4;
     static_assert(PA == 2 || PA == 4, "A ring index");
@@ -480,11 +536,13 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < NT; ++j)
+            for (int r = 0; r < 4; ++r) {
+                const int rr = 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+                const int sh = rsh[min(m0 + rr, M - 1)];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    st[(64 * wave + 16 * i + 4 * (lane >> 4) + r) * BN + 16 * j + (lane & 15)] =
-                        f32_to_bf16_rne(acc[i][j][r]);
+                for (int j = 0; j < NT; ++j)
+                    st[rr * BN + 16 * j + (lane & 15)] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -sh));
+            }
     }
     __syncthreads();
     const uint16_t* st = (const uint16_t*)lds;
@@ -539,19 +597,27 @@ size_t oil4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t cb_
     return v2 ? (size_t)(((M + 15) / 16) * 16 * K * 2) : 0;
 }
 
+size_t oil4_prefill_shift_bytes(int64_t M) { return (size_t)((M * 4 + 255) / 256 * 256); }
+
+static void launch_rowshift(const uint16_t* a_bf16, int* rsh, int64_t M, int64_t K, hipStream_t s) {
+    oil4_prefill_rowshift<<<(unsigned)M, 256, 0, s>>>(a_bf16, rsh, (int)M, (int)K);
+}
+
 hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                         int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
-                                        uint16_t* a16, hipStream_t s) {
-    const int64_t n16 = ((M + 15) / 16) * 16 * K / 8;
-    oil4_prefill_a16<<<(unsigned)((n16 + 255) / 256), 256, 0, s>>>(a_bf16, a16, (int)M, (int)K, n16);
+                                        void* ws, hipStream_t s) {
+    int* rsh = (int*)ws;
+    uint16_t* a16 = (uint16_t*)((char*)ws + oil4_prefill_shift_bytes(M));
+    const int64_t groups = (M + 15) / 16;
+    oil4_prefill_a16<<<(unsigned)(((groups + 7) / 8) * 128), 256, 0, s>>>(a_bf16, a16, (int)M, (int)K, rsh);
     const int bn = pick_bn_v2(M, N);
     const unsigned grid = (unsigned)(((M + PBM - 1) / PBM) * (N / bn));
     const int cbk = (int)cb_block, m = (int)M, n = (int)N, k = (int)K;
     switch (bn) {
-        case 128: oil4_prefill_ws<128, 2, 1><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
-        case 112: oil4_prefill_ws<112, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
-        case 96: oil4_prefill_ws<96, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
-        default: oil4_prefill_ws<64, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k); break;
+        case 128: oil4_prefill_ws<128, 2, 1><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        case 112: oil4_prefill_ws<112, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        case 96: oil4_prefill_ws<96, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        default: oil4_prefill_ws<64, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
     }
     return hipGetLastError();
 }
@@ -563,20 +629,24 @@ bool oil4_gemm_prefill_supported(int64_t M, int64_t N, int64_t K, int64_t cb_blo
 
 hipError_t launch_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                     int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
-                                    hipStream_t s) {
+                                    int* rsh, hipStream_t s) {
+    launch_rowshift(a_bf16, rsh, M, K, s);
     if (K % (4 * PBK) == 0 && cb_block % PBK == 0 && (M + PBM - 1) / PBM < 65536) {
         const int bn = pick_bn(M, N);
         const dim3 g2((unsigned)((N + bn - 1) / bn), (unsigned)((M + PBM - 1) / PBM));
         if (bn == 112)
-            oil4_prefill_mfma<112><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+            oil4_prefill_mfma<112><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K,
+                                           rsh);
         else if (bn == 96)
-            oil4_prefill_mfma<96><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+            oil4_prefill_mfma<96><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K,
+                                           rsh);
         else
-            oil4_prefill_mfma<128><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+            oil4_prefill_mfma<128><<<g2, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K,
+                                           rsh);
         return hipGetLastError();
     }
     dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-    oil4_gemm_prefill_k<<<grid, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K);
+    oil4_gemm_prefill_k<<<grid, 256, 0, s>>>(a_bf16, nib, cbs, (int)cb_block, c_bf16, (int)M, (int)N, (int)K, rsh);
     return hipGetLastError();
 }
 

@@ -152,17 +152,22 @@ hipError_t launch_tl2_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 
 // ---- OIL4 prefill GEMM (gemm_oil4.hip) -----------------------------------
+// Each row of A is scaled by a power of two into FP16's range and the output
+// row scaled back (per-row shifts: oil4_prefill_shift_bytes(M) of workspace,
+// rsh, filled by the launch).
+size_t oil4_prefill_shift_bytes(int64_t M);
 hipError_t launch_oil4_gemm_prefill(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                     int64_t cb_block, uint16_t* c_bf16,
-                                    int64_t M, int64_t N, int64_t K, hipStream_t s);
+                                    int64_t M, int64_t N, int64_t K, int* rsh, hipStream_t s);
 bool oil4_gemm_prefill_supported(int64_t M, int64_t N, int64_t K, int64_t cb_block);
 // The FP16-A kernels (oil4_prefill_a16 + oil4_prefill_ws) for K % 256 == 0, cb_block % 64 == 0
 // and N a multiple of 64, 96, 112 or 128: needs a workspace of
-// oil4_prefill_workspace_bytes (A converted to FP16; 0 = shape not covered).
+// oil4_prefill_shift_bytes(M) + oil4_prefill_workspace_bytes (the row shifts,
+// then A converted to FP16; 0 = shape not covered).
 size_t oil4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t cb_block);
 hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                        int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
-                                       uint16_t* a16, hipStream_t s);
+                                       void* ws, hipStream_t s);
 
 // ---- FP32 decode-step operators (dense.hip) ---------------------------------
 // x <- t + x (when t), then y = rms_norm(x) * gamma per row of dim.

@@ -240,3 +240,35 @@ def test_oil4_gemv_inf_times_tiny_x(path, M, K, batch, block, oracle, mth, dev):
         fp32_close(got[fin], ref[fin], absw[fin], 1e-5, f"{path}/inftiny finite rows")
     else:
         nonfinite_close(got, ref, absw, f"{path}/inftiny")
+
+
+@pytest.mark.parametrize("path,M,N,K,block", PREFILL_PATHS)
+def test_oil4_prefill_row_magnitudes(path, M, N, K, block, oracle, mth, dev):
+    """Rows of A scaled by 2^-30 .. 2^30 (bf16 N(0,1) values times a power
+    of two per row, an all-zero row too): FP16 holds neither end, so each row
+    is scaled into FP16's range and the output row scaled back.  One bf16
+    rounding of the oracle's FP32 result per element, as above; the largest
+    rows' outputs are finite and the smallest rows' nonzero."""
+    import torch
+    print(f"prefill row magnitudes path={path} M={M} N={N} K={K}", flush=True)
+    g = np.random.default_rng(zlib.crc32(f"{path}/rowmag".encode()))
+    exps = np.linspace(-30, 30, M).round()
+    a32 = (g.normal(0, 1, (M, K)) * np.exp2(exps)[:, None]).astype(np.float32)
+    a32[M // 2] = 0.0
+    a = synth.bf16_bits(a32)
+    packed = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    cbs = synth.float_to_half_trunc(g.normal(0, 0.02, N * (K // block) * 16).astype(np.float32))
+    c = torch.zeros(M * N, dtype=torch.bfloat16, device=dev)
+    mth.oil4_gemm_prefill(to_dev(a, dev).view(torch.bfloat16), to_dev(packed, dev), to_dev(cbs, dev), block, c,
+                          M, N, K)
+    torch.cuda.synchronize()
+    _, ref32 = oracle.oil4_gemm_prefill(a, packed, cbs, M, N, K, block, threads=8)
+    got = synth.bf16_to_f32(c.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(M, N).astype(np.float64)
+    ref = ref32.astype(np.float64)
+    W = synth.dequant_oil4(packed, cbs, N, K, block).astype(np.float64)
+    absw = np.abs(synth.bf16_to_f32(a).astype(np.float64)) @ np.abs(W).T
+    assert np.isfinite(got).all()
+    d = np.abs(got - ref)
+    bound = 2.0 ** -8 * np.abs(ref) + 1e-5 * absw
+    assert (d <= bound).all(), f"{path}: {(d > bound).sum()} elements out of bound, rows {np.unique(np.nonzero(d > bound)[0])[:8]}"
+    assert (got[M // 2] == 0).all() and (got[0] != 0).all() and (got[-1] != 0).all()
