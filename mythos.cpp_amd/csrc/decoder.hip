@@ -26,6 +26,9 @@
 // Block maxima of the batched SwiGLU per token (one per 256 columns of ffn):
 // the fused batch path covers ffn <= 64 * 256.
 constexpr int kAmxParts = 64;
+// Prefill chunks of at least this many rows run the FFN projections as
+// MFMA GEMMs (fewer: the batched GEMVs).
+constexpr int64_t kPfGemmRows = 128;
 
 struct mth_decoder {
     mth_decoder_config c{};
@@ -61,6 +64,7 @@ struct mth_decoder {
     float *pf_x = nullptr, *pf_h = nullptr, *pf_t = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
     float *pf_att = nullptr, *pf_gu = nullptr, *pf_inv = nullptr;
     int8_t* pf_aq = nullptr;
+    void* pf_ws = nullptr;  // the prefill GEMMs' scratch (A fragments, row shifts, permuted int8 activations)
 
     void drop_graph() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -164,7 +168,14 @@ hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
             TRY(oil8(d, L.wo, L.cbo, d->pf_att, d->pf_t, H, QD, s, R));
             TRY(mth::launch_rms_norm(d->pf_x, d->pf_t, L.ffn_norm, d->pf_h, R, H, c.eps, s));
             if (gate_up_fused(d, L)) {
-                TRY(oil4(d, L.wgate, L.cbgate, d->pf_h, d->pf_gu, 2 * F, H, s, R));
+                // chunks of >= kPfGemmRows rows: the FP32-row OIL4 GEMM on
+                // MFMA (each weight read once per 128 rows, not per 16)
+                if (R >= kPfGemmRows && mth::oil4_gemm_x32_supported(R, 2 * F, H, c.cb_block) &&
+                    ((((uintptr_t)L.wgate | (uintptr_t)L.cbgate) & 15u) == 0))
+                    TRY(mth::launch_oil4_gemm_x32(d->pf_h, L.wgate, L.cbgate, c.cb_block, d->pf_gu, R, 2 * F, H,
+                                                  d->pf_ws, s));
+                else
+                    TRY(oil4(d, L.wgate, L.cbgate, d->pf_h, d->pf_gu, 2 * F, H, s, R));
                 TRY(mth::launch_silu_mul_quant(d->pf_gu, d->pf_gu + F, d->pf_aq, d->pf_inv, nullptr, R, F, 2 * F,
                                                2 * F, s));
             } else {
@@ -173,7 +184,11 @@ hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
                 TRY(mth::launch_silu_mul_quant(d->pf_gu, d->pf_gu + R * F, d->pf_aq, d->pf_inv, nullptr, R, F, F, F,
                                                s));
             }
-            if ((((uintptr_t)L.wdown | (uintptr_t)d->pf_aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, R))
+            if (R >= kPfGemmRows && mth::i2s_gemm_workspace_bytes(H, R, F) != 0 &&
+                ((((uintptr_t)L.wdown | (uintptr_t)d->pf_aq) & 15u) == 0))  // int8 MFMA GEMM, bit-exact
+                TRY(mth::launch_i2s_gemm_rows(L.wdown, L.down_scale, d->pf_aq, d->pf_inv, d->pf_t, H, R, F, d->pf_ws,
+                                              s));
+            else if ((((uintptr_t)L.wdown | (uintptr_t)d->pf_aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, R))
                 TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->pf_aq, d->pf_inv, d->pf_t, H, F, R,
                                             d->bt_partial, s));
             else
@@ -520,6 +535,9 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->pf_aq, (size_t)(PR * F)},      {(void**)&d->pf_inv, (size_t)PR * 4},
         {(void**)&d->ssp, (size_t)(H / 4 + 2) * 8},  {(void**)&d->ssp2, (size_t)(H / 4 + 2) * 8},
         {(void**)&d->amx, (size_t)(B * kAmxParts) * 4},
+        {(void**)&d->pf_ws, PR >= kPfGemmRows ? std::max(mth::oil4_gemm_x32_workspace_bytes(PR, H),
+                                                         mth::i2s_gemm_workspace_bytes(H, PR, F))
+                                              : (size_t)0},
     };
     size_t total = 0;
     for (const Slot& sl : slots) total += round_up(sl.bytes);

@@ -395,18 +395,23 @@ __global__ __launch_bounds__(256) void oil4_prefill_a16(const uint16_t* __restri
 // on one XCD share an M tile (WG i runs on XCD i % 8), so an XCD's L2 holds
 // one M tile's rows of A.  C is staged through LDS as bf16 and written in
 // 16-byte pieces.
-template <int BN, int BS>
+template <int BN, int BS, bool X32 = false>
 struct Pf2Lds {
     static constexpr int w = BN * 128;                   // one K step's dequantised W tile
-    static constexpr int stage = 256 * BN * 2;           // C tile (bf16), after the main loop
+    static constexpr int stage = 256 * BN * (X32 ? 4 : 2);  // C tile (bf16, or FP32 sums), after the main loop
     static constexpr int bytes = (2 * BS * w > stage) ? 2 * BS * w : stage;
 };
 
-template <int BN, int PA, int BS>
+// X32 (the decoder's FP32 prompt rows, oil4_prefill_x32): M counts virtual
+// rows, 256 per tile: tile T's rows 0-127 are the FP16 hi parts and rows
+// 128-255 the lo parts of real rows 128 T .. 128 T + 127 (Mr real rows);
+// the epilogue adds the two halves' FP32 sums (products exact, sums FP32:
+// the FP32 dot product) and writes FP32 C [Mr][N].
+template <int BN, int PA, int BS, bool X32 = false>
 __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restrict__ A16, const uint8_t* nib,
-                                                       const uint16_t* cbs, int cb_block, uint16_t* __restrict__ C,
-                                                       int M, int N, int K, const int* __restrict__ rsh) {
-    using L = Pf2Lds<BN, BS>;
+                                                       const uint16_t* cbs, int cb_block, void* __restrict__ Cv,
+                                                       int M, int N, int K, const int* __restrict__ rsh, int Mr = 0) {
+    using L = Pf2Lds<BN, BS, X32>;
     constexpr int NT = BN / 16, PW = 4;
     static_assert(PA == 2 || PA == 4, "A ring index");
     static_assert(BS == 1 || BS == 2 || BS == 4, "barrier interval");
@@ -532,24 +537,109 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
             }
         }
         __syncthreads();
-        uint16_t* st = (uint16_t*)lds;
+        if constexpr (X32) {
+            float* st = (float*)lds;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int rr = 64 * wave + 16 * i + 4 * (lane >> 4) + r;
-                const int sh = rsh[min(m0 + rr, M - 1)];
+                for (int r = 0; r < 4; ++r) {
+                    const int rr = 64 * wave + 16 * i + 4 * (lane >> 4) + r;
 #pragma unroll
-                for (int j = 0; j < NT; ++j)
-                    st[rr * BN + 16 * j + (lane & 15)] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -sh));
-            }
+                    for (int j = 0; j < NT; ++j) st[rr * BN + 16 * j + (lane & 15)] = acc[i][j][r];
+                }
+        } else {
+            uint16_t* st = (uint16_t*)lds;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int rr = 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+                    const int sh = rsh[min(m0 + rr, M - 1)];
+#pragma unroll
+                    for (int j = 0; j < NT; ++j)
+                        st[rr * BN + 16 * j + (lane & 15)] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -sh));
+                }
+        }
     }
     __syncthreads();
-    const uint16_t* st = (const uint16_t*)lds;
-    constexpr int CPR = BN * 2 / 16;
-    for (int c = tid; c < 256 * CPR; c += 512) {
-        const int r = c / CPR, q = c % CPR;
-        if (m0 + r < M) *(uint4*)(C + (int64_t)(m0 + r) * N + n0 + 8 * q) = *(const uint4*)(st + r * BN + 8 * q);
+    if constexpr (X32) {
+        // real row 128 mt + r: (hi sum + lo sum) * 2^-shift
+        float* C = (float*)Cv;
+        const float* st = (const float*)lds;
+        constexpr int CPR = BN / 4;
+        for (int c = tid; c < 128 * CPR; c += 512) {
+            const int r = c / CPR, q = c % CPR, row = 128 * mt + r;
+            if (row < Mr) {
+                const int sh = rsh[row];
+                const float4 hi = *(const float4*)(st + r * BN + 4 * q), lo = *(const float4*)(st + (r + 128) * BN + 4 * q);
+                *(float4*)(C + (int64_t)row * N + n0 + 4 * q) =
+                    make_float4(ldexpf(hi.x + lo.x, -sh), ldexpf(hi.y + lo.y, -sh), ldexpf(hi.z + lo.z, -sh),
+                                ldexpf(hi.w + lo.w, -sh));
+            }
+        }
+    } else {
+        uint16_t* C = (uint16_t*)Cv;
+        const uint16_t* st = (const uint16_t*)lds;
+        constexpr int CPR = BN * 2 / 16;
+        for (int c = tid; c < 256 * CPR; c += 512) {
+            const int r = c / CPR, q = c % CPR;
+            if (m0 + r < M) *(uint4*)(C + (int64_t)(m0 + r) * N + n0 + 8 * q) = *(const uint4*)(st + r * BN + 8 * q);
+        }
+    }
+}
+
+// FP32 rows of A as FP16 hi / lo fragments for oil4_prefill_ws<X32>: one
+// workgroup per real row r (XCD-grouped as oil4_prefill_a16): the row's
+// maximum gives its shift (rsh[r], max|a| 2^s in [2^14, 2^15); 0 for a row
+// holding Inf / NaN); a 2^s = hi + lo, hi = fp16(a 2^s), lo = fp16(a 2^s -
+// hi), hi into virtual row 256 (r / 128) + r % 128, lo 128 rows below it.
+// Virtual rows of real rows past the last (Mr) hold zeros.
+__global__ __launch_bounds__(256) void oil4_prefill_a16x(const float* __restrict__ a, uint16_t* __restrict__ a16,
+                                                         int Mr, int K, int* __restrict__ rsh) {
+    __shared__ uint32_t red[4];
+    const int w = blockIdx.x, tid = threadIdx.x;
+    const int g = 8 * (w >> 7) + (w & 7), i = (w >> 3) & 15;
+    const int row = 16 * g + i;
+    const int tiles = (Mr + 127) / 128;
+    if (row >= 128 * tiles) return;
+    const bool real = row < Mr;
+    const float* p = a + (int64_t)(real ? row : 0) * K;
+    const int nch = K / 8;
+    uint32_t mb = 0;
+    if (real)
+        for (int c = tid; c < nch; c += 256) {
+            const float4 v0 = ldf4(p + 8 * c), v1 = ldf4(p + 8 * c + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mb = max(mb, __float_as_uint(v[e]) & 0x7fffffffu);
+        }
+    mb = group_reduce<64>(mb, UMaxOp{});
+    if ((tid & 63) == 0) red[tid >> 6] = mb;
+    __syncthreads();
+    const int sh = fp16_scale_shift(__uint_as_float(max(max(red[0], red[1]), max(red[2], red[3]))));
+    if (tid == 0 && real) rsh[row] = sh;
+    const int kc32 = K / 32;
+    const int vr = 256 * (row >> 7) + (row & 127);  // virtual row of the hi part; lo: vr + 128
+    uint16_t* dh = a16 + (int64_t)(vr >> 4) * kc32 * 512 + 8 * (vr & 15);
+    uint16_t* dl = a16 + (int64_t)((vr + 128) >> 4) * kc32 * 512 + 8 * (vr & 15);
+    for (int c = tid; c < nch; c += 256) {
+        half8 h, l;
+        if (real) {
+            const float4 v0 = ldf4(p + 8 * c), v1 = ldf4(p + 8 * c + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xs = ldexpf(v[e], sh);
+                h[e] = (_Float16)xs;
+                l[e] = (_Float16)(xs - (float)h[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = l[e] = (_Float16)0.0f;
+        }
+        const int64_t off = (int64_t)(c >> 2) * 512 + 128 * (c & 3);
+        *(half8*)(dh + off) = h;
+        *(half8*)(dl + off) = l;
     }
 }
 
@@ -618,6 +708,36 @@ hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* n
         case 112: oil4_prefill_ws<112, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
         case 96: oil4_prefill_ws<96, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
         default: oil4_prefill_ws<64, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+    }
+    return hipGetLastError();
+}
+
+bool oil4_gemm_x32_supported(int64_t Mr, int64_t N, int64_t K, int64_t cb_block) {
+    const int64_t mv = 256 * ((Mr + 127) / 128);
+    return Mr >= 1 && oil4_prefill_workspace_bytes(mv, N, K, cb_block) != 0 && K <= (1 << 20);
+}
+
+size_t oil4_gemm_x32_workspace_bytes(int64_t Mr, int64_t K) {
+    const int64_t mv = 256 * ((Mr + 127) / 128);
+    return oil4_prefill_shift_bytes(Mr) + (size_t)(mv * K * 2);
+}
+
+hipError_t launch_oil4_gemm_x32(const float* a, const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, float* c,
+                                int64_t Mr, int64_t N, int64_t K, void* ws, hipStream_t s) {
+    if (!oil4_gemm_x32_supported(Mr, N, K, cb_block)) return hipErrorInvalidValue;
+    int* rsh = (int*)ws;
+    uint16_t* a16 = (uint16_t*)((char*)ws + oil4_prefill_shift_bytes(Mr));
+    const int64_t tiles = (Mr + 127) / 128, mv = 256 * tiles;
+    const int64_t groups = tiles * 8;  // real 16-row groups of the padded rows
+    oil4_prefill_a16x<<<(unsigned)(((groups + 7) / 8) * 128), 256, 0, s>>>(a, a16, (int)Mr, (int)K, rsh);
+    const int bn = pick_bn_v2(mv, N);
+    const unsigned grid = (unsigned)(tiles * (N / bn));
+    const int cbk = (int)cb_block, m = (int)mv, n = (int)N, k = (int)K, mr = (int)Mr;
+    switch (bn) {
+        case 128: oil4_prefill_ws<128, 2, 1, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
+        case 112: oil4_prefill_ws<112, 4, 2, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
+        case 96: oil4_prefill_ws<96, 4, 2, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
+        default: oil4_prefill_ws<64, 4, 2, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
     }
     return hipGetLastError();
 }

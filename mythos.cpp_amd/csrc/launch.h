@@ -146,6 +146,12 @@ hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
 size_t i2s_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o,
                                 int64_t M, int64_t N, int64_t K, void* ws, hipStream_t s);
+// The prompt prefill's down projection on int8 MFMA: y [N][M] = the I2_S
+// GEMV of every token row n of the int8 activations a [N][K] with act scale
+// inv[n] (bit-identical to launch_i2s_gemv per row); ws:
+// i2s_gemm_workspace_bytes(M, N, K) bytes (nonzero: M, N >= 64, K % 256 == 0).
+hipError_t launch_i2s_gemm_rows(const uint8_t* w, float w_scale, const int8_t* a, const float* inv, float* y, int64_t M,
+                                int64_t N, int64_t K, void* ws, hipStream_t s);
 hipError_t launch_tl1_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 hipError_t launch_tl2_gemm(const uint8_t* w, const float* a, float* o,
@@ -168,6 +174,15 @@ size_t oil4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t cb_
 hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* nib, const uint16_t* cbs,
                                        int64_t cb_block, uint16_t* c_bf16, int64_t M, int64_t N, int64_t K,
                                        void* ws, hipStream_t s);
+
+// The prompt prefill's OIL4 projection with FP32 rows (FP32 accurate, the
+// decode GEMVs' arithmetic on MFMA): c [Mr][N] = a [Mr][K] W^T, each row of a
+// split into FP16 hi + lo after a power-of-two scale (two products per
+// weight, sums FP32).  ws: oil4_gemm_x32_workspace_bytes(Mr, K).
+bool oil4_gemm_x32_supported(int64_t Mr, int64_t N, int64_t K, int64_t cb_block);
+size_t oil4_gemm_x32_workspace_bytes(int64_t Mr, int64_t K);
+hipError_t launch_oil4_gemm_x32(const float* a, const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, float* c,
+                                int64_t Mr, int64_t N, int64_t K, void* ws, hipStream_t s);
 
 // ---- FP32 decode-step operators (dense.hip) ---------------------------------
 // x <- t + x (when t), then y = rms_norm(x) * gamma per row of dim.

@@ -1130,8 +1130,14 @@ __global__ __launch_bounds__(kWG) void i2s_act_perm(const int8_t* __restrict__ a
 // LDS byte offset of 16-byte slot q (0..15) of weight row r in a step tile
 __device__ __forceinline__ int tg_off(int r, int q) { return r * TGK + 16 * (q ^ (r & 7)); }
 
+// ROWS: the decoder prefill's down projection -- out is y [N][M] with
+// y[n][m] = ((float)sum * w_scale) * inv[n], each product rounded on its
+// own: the reference's i2s_gemv epilogue (src/kernel_i2s.cpp:32-40) for
+// every token row, bit for bit (the sums are exact integers below 2^24).
+template <bool ROWS = false>
 __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int8_t* ap, const int* __restrict__ sums,
-                                                     float* __restrict__ out, int M, int N, int K) {
+                                                     float* __restrict__ out, int M, int N, int K,
+                                                     float w_scale = 0.0f, const float* __restrict__ inv = nullptr) {
     __shared__ __align__(16) uint8_t wt[2][TGM * TGK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tm = (M + TGM - 1) / TGM, tn = (N + TGN - 1) / TGN;
@@ -1216,13 +1222,32 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
         const int n = n0 + 32 * wave + 16 * j + (lane & 15);
         if (n >= N) continue;
         const int as = sums[n];
+        if constexpr (ROWS) {
+            const float ts = inv[n];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + 16 * i + 4 * (lane >> 4);
+                float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 16 * i + 4 * (lane >> 4) + r;
-                if (m < M) out[(int64_t)m * N + n] = (float)(acc[i][j][r] - as);
+                for (int r = 0; r < 4; ++r) v[r] = fmul_rn(fmul_rn((float)(acc[i][j][r] - as), w_scale), ts);
+                float* dst = out + (int64_t)n * M + m;
+                if (m + 3 < M && ((uintptr_t)dst & 15u) == 0) {
+                    *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (m + r < M) dst[r] = v[r];
+                }
             }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + 16 * i + 4 * (lane >> 4) + r;
+                    if (m < M) out[(int64_t)m * N + n] = (float)(acc[i][j][r] - as);
+                }
+        }
     }
 }
 
@@ -1438,6 +1463,17 @@ hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o, int
         return hipGetLastError();
     }
     i2s_gemm_vnni_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_i2s_gemm_rows(const uint8_t* w, float w_scale, const int8_t* a, const float* inv, float* y, int64_t M,
+                                int64_t N, int64_t K, void* ws, hipStream_t s) {
+    if (!ws || i2s_gemm_workspace_bytes(M, N, K) == 0) return hipErrorInvalidValue;
+    int8_t* ap = (int8_t*)ws;
+    int* sums = (int*)((char*)ws + ((N * K + 255) / 256) * 256);
+    i2s_act_perm<<<(unsigned)N, kWG, 0, s>>>(a, ap, sums, (int)K);
+    const unsigned grid = (unsigned)(((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN));
+    i2s_gemm_mfma<true><<<grid, kWG, 0, s>>>(w, ap, sums, y, (int)M, (int)N, (int)K, w_scale, inv);
     return hipGetLastError();
 }
 
