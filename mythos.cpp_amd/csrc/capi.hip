@@ -46,6 +46,8 @@ inline hipStream_t S(mth_stream_t s) { return (hipStream_t)s; }
 // int32 row/column indices are used inside kernels for the fast paths; the
 // generic kernels index with int64.  Reject sizes whose byte counts overflow.
 constexpr int64_t kMaxDim = (int64_t)1 << 40;
+// batches of at least this many tokens run the OIL8 / OIL4 GEMVs as MFMA GEMMs
+constexpr int64_t kGemmRows = 128;
 
 // Device scratch (partial sums of the batched GEMVs' K slices, argmax
 // partials), one per (device, stream): calls on one stream are ordered and
@@ -178,6 +180,15 @@ int mth_oil8_gemv(const uint8_t* indices, const float* codebook, const float* x,
     REQUIRE(M > 0 && K > 0 && batch > 0 && M < kMaxDim && K < kMaxDim && batch <= 65536,
             "mth_oil8_gemv: bad sizes M=%lld K=%lld batch=%lld", (long long)M, (long long)K, (long long)batch);
     const bool aligned = (((uintptr_t)indices | (uintptr_t)x) & 15u) == 0;
+    const mth::Oil8Seg seg{indices, codebook, y, M};
+    if (batch >= kGemmRows && mth::oil8_gemm_x32_supported(&seg, 1, batch, K)) {
+        // >= 128 tokens: the MFMA GEMM (each weight read once per 128 tokens)
+        void* ws = nullptr;
+        const size_t need = mth::oil8_gemm_x32_workspace_bytes(batch, K);
+        const hipError_t e = workspace(S(stream), need, &ws);
+        if (e != hipSuccess) return workspace_fail("mth_oil8_gemv", e, need);
+        return check_launch(mth::launch_oil8_gemm_x32(x, &seg, 1, batch, K, ws, S(stream)), "mth_oil8_gemv");
+    }
     if (aligned && mth::oil8_bt_supported(M, K, batch)) {
         void* partial = nullptr;
         const size_t need = mth::oil8_bt_partial_bytes(M, K);
@@ -207,6 +218,16 @@ int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_b
     REQUIRE(cb_block == 0 || K % cb_block == 0, "mth_oil4_gemv: K=%lld not a multiple of cb_block=%lld",
             (long long)K, (long long)cb_block);
     const bool aligned = (((uintptr_t)packed | (uintptr_t)codebooks | (uintptr_t)x) & 15u) == 0;
+    if (aligned && ((uintptr_t)y & 15u) == 0 && batch >= kGemmRows &&
+        mth::oil4_gemm_x32_supported(batch, M, K, cb_block)) {
+        // >= 128 tokens: the MFMA GEMM (each weight read once per 128 tokens)
+        void* ws = nullptr;
+        const size_t need = mth::oil4_gemm_x32_workspace_bytes(batch, K);
+        const hipError_t e = workspace(S(stream), need, &ws);
+        if (e != hipSuccess) return workspace_fail("mth_oil4_gemv", e, need);
+        return check_launch(mth::launch_oil4_gemm_x32(x, packed, codebooks, cb_block, y, batch, M, K, ws, S(stream)),
+                            "mth_oil4_gemv");
+    }
     if (aligned && mth::oil4_bt_supported(M, K, cb_block, batch)) {
         void* partial = nullptr;
         const size_t need = mth::oil4_bt_partial_bytes(M, K);

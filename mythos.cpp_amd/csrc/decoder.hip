@@ -109,6 +109,9 @@ hipError_t qkv(const mth_decoder* d, const mth_decoder_layer& L, const float* h,
     const mth_decoder_config& c = d->c;
     const int64_t H = c.hidden, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
     const mth::Oil8Seg seg[3] = {{L.wq, L.cbq, q, QD}, {L.wk, L.cbk, k, KD}, {L.wv, L.cbv, v, KD}};
+    // prompt chunks of >= kPfGemmRows rows: the FP32-row OIL8 GEMM on MFMA
+    if (rows >= kPfGemmRows && d->pf_ws && mth::oil8_gemm_x32_supported(seg, 3, rows, H))
+        return mth::launch_oil8_gemm_x32(h, seg, 3, rows, H, d->pf_ws, s);
     if (((uintptr_t)h & 15u) == 0) {
         if (rows >= 2) {
             if (mth::oil8_bt_segs_fusable(seg, 3, H, rows))
@@ -165,7 +168,13 @@ hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
                                          (int)c.max_seq, s));
             TRY(mth::launch_attention_rows(d->pf_q, kc, vc, bf16, d->pf_att, R, (int)np, (int)p0, (int)c.heads,
                                            (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
-            TRY(oil8(d, L.wo, L.cbo, d->pf_att, d->pf_t, H, QD, s, R));
+            {
+                const mth::Oil8Seg so{L.wo, L.cbo, d->pf_t, H};
+                if (R >= kPfGemmRows && mth::oil8_gemm_x32_supported(&so, 1, R, QD))
+                    TRY(mth::launch_oil8_gemm_x32(d->pf_att, &so, 1, R, QD, d->pf_ws, s));
+                else
+                    TRY(oil8(d, L.wo, L.cbo, d->pf_att, d->pf_t, H, QD, s, R));
+            }
             TRY(mth::launch_rms_norm(d->pf_x, d->pf_t, L.ffn_norm, d->pf_h, R, H, c.eps, s));
             if (gate_up_fused(d, L)) {
                 // chunks of >= kPfGemmRows rows: the FP32-row OIL4 GEMM on
@@ -535,8 +544,10 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->pf_aq, (size_t)(PR * F)},      {(void**)&d->pf_inv, (size_t)PR * 4},
         {(void**)&d->ssp, (size_t)(H / 4 + 2) * 8},  {(void**)&d->ssp2, (size_t)(H / 4 + 2) * 8},
         {(void**)&d->amx, (size_t)(B * kAmxParts) * 4},
-        {(void**)&d->pf_ws, PR >= kPfGemmRows ? std::max(mth::oil4_gemm_x32_workspace_bytes(PR, H),
-                                                         mth::i2s_gemm_workspace_bytes(H, PR, F))
+        {(void**)&d->pf_ws, PR >= kPfGemmRows ? std::max({mth::oil4_gemm_x32_workspace_bytes(PR, H),
+                                                          mth::oil8_gemm_x32_workspace_bytes(PR, H),
+                                                          mth::oil8_gemm_x32_workspace_bytes(PR, QD),
+                                                          mth::i2s_gemm_workspace_bytes(H, PR, F)})
                                               : (size_t)0},
     };
     size_t total = 0;

@@ -588,12 +588,15 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
     }
 }
 
-// FP32 rows of A as FP16 hi / lo fragments for oil4_prefill_ws<X32>: one
-// workgroup per real row r (XCD-grouped as oil4_prefill_a16): the row's
-// maximum gives its shift (rsh[r], max|a| 2^s in [2^14, 2^15); 0 for a row
-// holding Inf / NaN); a 2^s = hi + lo, hi = fp16(a 2^s), lo = fp16(a 2^s -
-// hi), hi into virtual row 256 (r / 128) + r % 128, lo 128 rows below it.
-// Virtual rows of real rows past the last (Mr) hold zeros.
+// FP32 rows of A as FP16 hi / lo fragments for oil4_prefill_ws<X32> and
+// oil8_prefill_ws: one workgroup per real row r (XCD-grouped as
+// oil4_prefill_a16): the row's maximum gives its shift (rsh[r], max|a| 2^s in
+// [2^14, 2^15); 0 for an all-zero row; kRowNonFinite for a row holding Inf /
+// NaN, converted with s = 0: its hi / lo parts then carry NaN, and the OIL8
+// GEMM's workgroups over such a row take the FP32 path); a 2^s = hi + lo,
+// hi = fp16(a 2^s), lo = fp16(a 2^s - hi), hi into virtual row
+// 256 (r / 128) + r % 128, lo 128 rows below it.  Virtual rows of real rows
+// past the last (Mr) hold zeros.
 __global__ __launch_bounds__(256) void oil4_prefill_a16x(const float* __restrict__ a, uint16_t* __restrict__ a16,
                                                          int Mr, int K, int* __restrict__ rsh) {
     __shared__ uint32_t red[4];
@@ -616,8 +619,9 @@ __global__ __launch_bounds__(256) void oil4_prefill_a16x(const float* __restrict
     mb = group_reduce<64>(mb, UMaxOp{});
     if ((tid & 63) == 0) red[tid >> 6] = mb;
     __syncthreads();
-    const int sh = fp16_scale_shift(__uint_as_float(max(max(red[0], red[1]), max(red[2], red[3]))));
-    if (tid == 0 && real) rsh[row] = sh;
+    const uint32_t rmax = max(max(red[0], red[1]), max(red[2], red[3]));
+    const int sh = fp16_scale_shift(__uint_as_float(rmax));
+    if (tid == 0 && real) rsh[row] = rmax >= 0x7f800000u ? kRowNonFinite : sh;
     const int kc32 = K / 32;
     const int vr = 256 * (row >> 7) + (row & 127);  // virtual row of the hi part; lo: vr + 128
     uint16_t* dh = a16 + (int64_t)(vr >> 4) * kc32 * 512 + 8 * (vr & 15);
@@ -712,9 +716,17 @@ hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* n
     return hipGetLastError();
 }
 
+hipError_t launch_prefill_a16x(const float* a, int64_t Mr, int64_t K, void* ws, hipStream_t s) {
+    int* rsh = (int*)ws;
+    uint16_t* a16 = (uint16_t*)((char*)ws + oil4_prefill_shift_bytes(Mr));
+    const int64_t groups = ((Mr + 127) / 128) * 8;  // real 16-row groups of the padded rows
+    oil4_prefill_a16x<<<(unsigned)(((groups + 7) / 8) * 128), 256, 0, s>>>(a, a16, (int)Mr, (int)K, rsh);
+    return hipGetLastError();
+}
+
 bool oil4_gemm_x32_supported(int64_t Mr, int64_t N, int64_t K, int64_t cb_block) {
     const int64_t mv = 256 * ((Mr + 127) / 128);
-    return Mr >= 1 && oil4_prefill_workspace_bytes(mv, N, K, cb_block) != 0 && K <= (1 << 20);
+    return Mr >= 1 && cb_block > 0 && oil4_prefill_workspace_bytes(mv, N, K, cb_block) != 0 && K <= (1 << 20);
 }
 
 size_t oil4_gemm_x32_workspace_bytes(int64_t Mr, int64_t K) {
@@ -725,11 +737,11 @@ size_t oil4_gemm_x32_workspace_bytes(int64_t Mr, int64_t K) {
 hipError_t launch_oil4_gemm_x32(const float* a, const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, float* c,
                                 int64_t Mr, int64_t N, int64_t K, void* ws, hipStream_t s) {
     if (!oil4_gemm_x32_supported(Mr, N, K, cb_block)) return hipErrorInvalidValue;
-    int* rsh = (int*)ws;
-    uint16_t* a16 = (uint16_t*)((char*)ws + oil4_prefill_shift_bytes(Mr));
+    const hipError_t e = launch_prefill_a16x(a, Mr, K, ws, s);
+    if (e != hipSuccess) return e;
+    const int* rsh = (const int*)ws;
+    const uint16_t* a16 = (const uint16_t*)((const char*)ws + oil4_prefill_shift_bytes(Mr));
     const int64_t tiles = (Mr + 127) / 128, mv = 256 * tiles;
-    const int64_t groups = tiles * 8;  // real 16-row groups of the padded rows
-    oil4_prefill_a16x<<<(unsigned)(((groups + 7) / 8) * 128), 256, 0, s>>>(a, a16, (int)Mr, (int)K, rsh);
     const int bn = pick_bn_v2(mv, N);
     const unsigned grid = (unsigned)(tiles * (N / bn));
     const int cbk = (int)cb_block, m = (int)mv, n = (int)N, k = (int)K, mr = (int)Mr;

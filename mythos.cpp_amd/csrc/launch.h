@@ -183,6 +183,22 @@ bool oil4_gemm_x32_supported(int64_t Mr, int64_t N, int64_t K, int64_t cb_block)
 size_t oil4_gemm_x32_workspace_bytes(int64_t Mr, int64_t K);
 hipError_t launch_oil4_gemm_x32(const float* a, const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, float* c,
                                 int64_t Mr, int64_t N, int64_t K, void* ws, hipStream_t s);
+// The FP32 rows' FP16 hi / lo fragments both x32 GEMMs read: ws holds the
+// row shifts (oil4_prefill_shift_bytes(Mr)), then 256 virtual rows per 128
+// real rows of K FP16 values.  A row holding Inf or NaN gets the shift
+// kRowNonFinite.
+constexpr int kRowNonFinite = 1 << 20;
+hipError_t launch_prefill_a16x(const float* a, int64_t Mr, int64_t K, void* ws, hipStream_t s);
+
+// The prompt prefill's OIL8 projections (gemm_oil8.hip): y_s [Mr][rows_s] =
+// a [Mr][K] W_s^T for up to three weights in one launch (Q, K, V), FP32
+// accurate (FP16 hi / lo parts of rows and codebook entries, three products
+// per weight, FP32 sums); segments of a multiple of 64 rows, K % 256 == 0,
+// 16-byte aligned indices and outputs.  ws: oil8_gemm_x32_workspace_bytes.
+bool oil8_gemm_x32_supported(const Oil8Seg* seg, int nseg, int64_t Mr, int64_t K);
+size_t oil8_gemm_x32_workspace_bytes(int64_t Mr, int64_t K);
+hipError_t launch_oil8_gemm_x32(const float* a, const Oil8Seg* seg, int nseg, int64_t Mr, int64_t K, void* ws,
+                                hipStream_t s);
 
 // ---- FP32 decode-step operators (dense.hip) ---------------------------------
 // x <- t + x (when t), then y = rms_norm(x) * gamma per row of dim.

@@ -155,10 +155,10 @@ def test_gqa_teacher_forced(batch, oracle):
     dec.close()
 
 
-def prefill_vs_oracle(cfg, model, B, P, kv, oracle, seed, extra_steps=2):
+def prefill_vs_oracle(cfg, model, B, P, kv, oracle, seed, extra_steps=2, ltol=TOL):
     """mth_decoder_prefill against the oracle's P teacher-forced steps per
-    sequence: the last position's logits, every layer's K/V cache rows
-    0..P-1, the first generated token (greedy on the GPU's logits), then
+    sequence: the last position's logits (bar ltol), every layer's K/V cache
+    rows 0..P-1, the first generated token (greedy on the GPU's logits), then
     decode steps continuing from the prefilled cache."""
     prompts = synth.decoder_prompts(cfg, B, P, config=seed)
     print(f"decoder prefill B={B} P={P} kv={kv}", flush=True)
@@ -172,7 +172,8 @@ def prefill_vs_oracle(cfg, model, B, P, kv, oracle, seed, extra_steps=2):
                      for b in range(B)])
     got = dec.logits()
     for b in range(B):
-        assert rel(got[b], want[b]) < TOL, (b, rel(got[b], want[b]))
+        print(f"  sequence {b}: logits rel {rel(got[b], want[b]):.3e}", flush=True)
+        assert rel(got[b], want[b]) < ltol, (b, rel(got[b], want[b]))
     for l in range(cfg["layers"]):
         kg, vg = dec.read_kv(l)
         for b in range(B):
@@ -194,8 +195,9 @@ def prefill_vs_oracle(cfg, model, B, P, kv, oracle, seed, extra_steps=2):
         lg, toks = dec.logits(), dec.tokens()
         for b in range(B):
             w = orc.step(*caches[b], P + st, int(toks[b, P + st]), threads=THREADS)
-            assert rel(lg[b], w) < TOL, (st, b, rel(lg[b], w))
+            assert rel(lg[b], w) < ltol, (st, b, rel(lg[b], w))
     dec.close()
+    return want
 
 
 @pytest.mark.parametrize("B,kv", [(1, "f32"), (3, "bf16")])
@@ -204,13 +206,30 @@ def test_prefill_matches_oracle(B, kv, small, oracle):
     prefill_vs_oracle(cfg, model, B, 12, kv, oracle, seed=70 + B)
 
 
-def test_prefill_chunks_and_gqa(oracle):
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_prefill_chunks_and_gqa(kv, oracle):
     """16 sequences x 70 prompt positions = 1120 rows: two chunks (64
     positions, then 6) whose second attends to the first's cache rows;
-    grouped-query heads."""
+    grouped-query heads.  The first chunk's 1024 rows run every projection as
+    an MFMA GEMM (Q / K / V and O: OIL8, gate / up: OIL4, down: int8), the
+    second's 96 rows the batched GEMVs.  The GPU's FP32 sums run in another
+    order than the oracle's, so a value on a rounding boundary can round to
+    the other side: an int8 activation of the down projection one step apart
+    (the down scale is divided by 16, exactly, so such a step stays below the
+    bar; the FFN still moves the logits far more than the bar, asserted), and
+    with a bf16 cache a K or V value one bf16 ulp (2^-8) apart.  With an FP32
+    cache the logits and cache rows meet the 1e-4 bar; the bf16 cache's flips
+    over 1120 rows carry through attention into the logits, so that case has
+    the 1e-3 bar the cache rows of later layers have."""
     cfg = synth.decoder_config(**dict(MID, max_seq=80, heads=8, kv_heads=4, head_dim=64))
-    model = synth.decoder_model(cfg, config=68, random_gamma=True)
-    prefill_vs_oracle(cfg, model, 16, 70, "bf16", oracle, seed=69)
+    model = scaled_down(synth.decoder_model(cfg, config=68, random_gamma=True), 16)
+    want = prefill_vs_oracle(cfg, model, 16, 70, kv, oracle, seed=69, ltol=TOL if kv == "f32" else 1e-3)
+    if kv == "f32":
+        prompts = synth.decoder_prompts(cfg, 16, 70, config=69)
+        orc = oracle.decoder(oracle_cfg(cfg, kv), ffn_off(model))
+        cache = orc.new_cache()
+        off = [orc.step(*cache, pos, int(prompts[0, pos]), threads=THREADS) for pos in range(70)][-1]
+        assert rel(off, want[0]) > 10 * TOL  # measured 3.9e-3
 
 
 def test_prefill_then_generate_follows_oracle(small, oracle):
