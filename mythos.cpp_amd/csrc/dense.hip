@@ -1023,6 +1023,144 @@ bool attention_supported(int head_dim, int max_seq) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) && max_seq > 0 && max_seq <= 16384;
 }
 
+// ---- prompt attention --------------------------------------------------------
+// Workgroup (head h, sequence b, tile of up to 64 query rows): rows
+// b np + i (i in [64 z, 64 z + 64) and < np) of q / out, at positions
+// p0 + i, each attending causally to cache rows 0 .. p0 + i of kv head
+// h % kv_heads (the decode kernel's semantics, one workgroup per row, for a
+// whole tile of rows at once, so each K / V row is read once per 64 query
+// rows).  The context streams through LDS in tiles of 64 positions; per
+// tile: scores (FP32, dot products over d in order, times 1 / sqrt(D)) of a
+// 4 x 4 block per thread (rows 4 (t / 16) + a, positions t % 16 + 16 c),
+// the causal mask, a running maximum per row with the earlier tiles' sums
+// and outputs rescaled by exp(m_old - m_new), exp(s - m) into LDS, and
+// P V accumulated per thread for its 4 rows x D / 16 columns; at the end
+// the rows are divided by their sums.  The same softmax and weighted sum as
+// the decode kernel up to FP32 rounding order.
+template <int D, typename KV>
+__global__ __launch_bounds__(256) void attn_prefill_k(const float* __restrict__ q, const KV* __restrict__ kc,
+                                                      const KV* __restrict__ vc, float* __restrict__ out, int np,
+                                                      int p0, int heads, int kv_heads, int max_seq, float scale) {
+    constexpr int QT = 64, KT = 64, DP = D + 4, PP = KT + 4, NC = D / 64;
+    __shared__ __align__(16) float Qs[QT * DP];
+    __shared__ __align__(16) float Ks[KT * DP];
+    __shared__ __align__(16) float Vs[KT * DP];
+    __shared__ __align__(16) float Ps[QT * PP];
+    const int h = blockIdx.x, b = blockIdx.y, i0 = blockIdx.z * QT, tid = threadIdx.x;
+    const int nq = min(QT, np - i0);
+    const int kh = h % kv_heads;
+    const int64_t crow = ((int64_t)b * kv_heads + kh) * max_seq;  // cache row of position 0
+    const int64_t qstride = (int64_t)heads * D;
+    const int ctx = p0 + i0 + nq;  // positions the tile's last row attends to
+    const int qg = tid >> 4, kg = tid & 15;
+    for (int c = tid; c < QT * (D / 4); c += 256) {
+        const int r = c / (D / 4), d = 4 * (c % (D / 4));
+        *(float4*)(Qs + r * DP + d) = r < nq ? *(const float4*)(q + (int64_t)(b * np + i0 + r) * qstride + h * D + d)
+                                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float m[4], l[4];
+    float4 o[4][NC];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        m[a] = -INFINITY;
+        l[a] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) o[a][c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    for (int t0 = 0; t0 < ctx; t0 += KT) {
+        __syncthreads();  // the previous tile's K, V and P are consumed
+        for (int c = tid; c < KT * (D / 4); c += 256) {
+            const int r = c / (D / 4), d = 4 * (c % (D / 4)), t = t0 + r;
+            const bool in = t < ctx;
+            const int64_t off = (crow + (in ? t : 0)) * D + d;
+            *(float4*)(Ks + r * DP + d) = in ? kv_load4(kc + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            *(float4*)(Vs + r * DP + d) = in ? kv_load4(vc + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        __syncthreads();
+        float s[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[a][c] = 0.0f;
+        for (int d = 0; d < D; d += 4) {
+            float4 qv[4], kv[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) qv[a] = *(const float4*)(Qs + (4 * qg + a) * DP + d);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kv[c] = *(const float4*)(Ks + (kg + 16 * c) * DP + d);
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float t = s[a][c];
+                    t = fmaf(qv[a].x, kv[c].x, t);
+                    t = fmaf(qv[a].y, kv[c].y, t);
+                    t = fmaf(qv[a].z, kv[c].z, t);
+                    s[a][c] = fmaf(qv[a].w, kv[c].w, t);
+                }
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const int qp = p0 + i0 + 4 * qg + a;  // position of row a (rows past nq: masked like any row)
+            float tm = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int kp = t0 + kg + 16 * c;
+                s[a][c] = kp <= qp ? s[a][c] * scale : -INFINITY;
+                tm = fmaxf(tm, s[a][c]);
+            }
+            tm = group_reduce<16>(tm, MaxOp{});
+            const float mn = fmaxf(m[a], tm);  // finite: position 0 is in the first tile of every row
+            const float alpha = expf(m[a] - mn);
+            float rs = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float p = expf(s[a][c] - mn);
+                Ps[(4 * qg + a) * PP + kg + 16 * c] = p;
+                rs += p;
+            }
+            rs = group_reduce<16>(rs, AddOp{});
+            l[a] = fmaf(l[a], alpha, rs);
+            m[a] = mn;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                o[a][c].x *= alpha;
+                o[a][c].y *= alpha;
+                o[a][c].z *= alpha;
+                o[a][c].w *= alpha;
+            }
+        }
+        __syncthreads();
+        const int jn = min(KT, ctx - t0);
+        for (int j = 0; j < jn; ++j) {
+            float4 vv[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) vv[c] = *(const float4*)(Vs + j * DP + 4 * kg + 64 * c);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float p = Ps[(4 * qg + a) * PP + j];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    o[a][c].x = fmaf(p, vv[c].x, o[a][c].x);
+                    o[a][c].y = fmaf(p, vv[c].y, o[a][c].y);
+                    o[a][c].z = fmaf(p, vv[c].z, o[a][c].z);
+                    o[a][c].w = fmaf(p, vv[c].w, o[a][c].w);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        const int r = 4 * qg + a;
+        if (r >= nq) continue;
+        const float inv = 1.0f / l[a];
+        float* dst = out + (int64_t)(b * np + i0 + r) * qstride + h * D + 4 * kg;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            *(float4*)(dst + 64 * c) = make_float4(o[a][c].x * inv, o[a][c].y * inv, o[a][c].z * inv, o[a][c].w * inv);
+    }
+}
+
 template <bool ROPE, typename KV>
 static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& v, const NormScale& ns,
                                 const float* cos_t, const float* sin_t, KV* kc, KV* vc, float* out, const int* step,
@@ -1072,6 +1210,29 @@ hipError_t launch_attention_rows(const float* q, const void* kc, const void* vc,
                                  int64_t rows, int np, int p0, int heads, int kv_heads, int head_dim, int max_seq,
                                  hipStream_t s) {
     const Slices qs = plain_slices(q, (int64_t)heads * head_dim), none{nullptr, 0, 0, 0, 1.0f, nullptr};
+    // tiles of query rows (a prompt chunk of 16 positions or more per sequence)
+    const bool aligned = (((uintptr_t)q | (uintptr_t)out | (uintptr_t)kc | (uintptr_t)vc) & 15u) == 0;
+    if (np >= 16 && aligned && (head_dim == 64 || head_dim == 128) && rows % np == 0 && rows / np <= 65535 &&
+        heads <= 65535) {
+        const dim3 grid((unsigned)heads, (unsigned)(rows / np), (unsigned)((np + 63) / 64));
+        const float scale = 1.0f / sqrtf((float)head_dim);
+        if (head_dim == 64) {
+            if (kv_bf16)
+                attn_prefill_k<64, uint16_t><<<grid, 256, 0, s>>>(q, (const uint16_t*)kc, (const uint16_t*)vc, out, np,
+                                                                   p0, heads, kv_heads, max_seq, scale);
+            else
+                attn_prefill_k<64, float><<<grid, 256, 0, s>>>(q, (const float*)kc, (const float*)vc, out, np, p0,
+                                                                heads, kv_heads, max_seq, scale);
+        } else {
+            if (kv_bf16)
+                attn_prefill_k<128, uint16_t><<<grid, 256, 0, s>>>(q, (const uint16_t*)kc, (const uint16_t*)vc, out,
+                                                                    np, p0, heads, kv_heads, max_seq, scale);
+            else
+                attn_prefill_k<128, float><<<grid, 256, 0, s>>>(q, (const float*)kc, (const float*)vc, out, np, p0,
+                                                                 heads, kv_heads, max_seq, scale);
+        }
+        return hipGetLastError();
+    }
     if (kv_bf16)
         return run_attention<false, uint16_t>(qs, none, none, NormScale{}, nullptr, nullptr, (uint16_t*)kc,
                                               (uint16_t*)vc, out, nullptr, p0, rows, np, heads, kv_heads, head_dim,

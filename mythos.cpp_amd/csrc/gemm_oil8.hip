@@ -327,7 +327,7 @@ hipError_t launch_oil8_gemm_x32(const float* a, const Oil8Seg* seg, int nseg, in
     const int* rsh = (const int*)ws;
     const uint16_t* a16 = (const uint16_t*)((const char*)ws + oil4_prefill_shift_bytes(Mr));
     const int64_t tiles = (Mr + 127) / 128;
-    oil8_prefill_ws<BN, 2, 2><<<(unsigned)(tiles * t), 512, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
+    oil8_prefill_ws<BN, 4, 2><<<(unsigned)(tiles * t), 512, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
     return hipGetLastError();
 }
 

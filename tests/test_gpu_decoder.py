@@ -207,12 +207,15 @@ def test_prefill_matches_oracle(B, kv, small, oracle):
 
 
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
-def test_prefill_chunks_and_gqa(kv, oracle):
-    """16 sequences x 70 prompt positions = 1120 rows: two chunks (64
-    positions, then 6) whose second attends to the first's cache rows;
-    grouped-query heads.  The first chunk's 1024 rows run every projection as
-    an MFMA GEMM (Q / K / V and O: OIL8, gate / up: OIL4, down: int8), the
-    second's 96 rows the batched GEMVs.  The GPU's FP32 sums run in another
+@pytest.mark.parametrize("P", [70, 100])
+def test_prefill_chunks_and_gqa(P, kv, oracle):
+    """16 sequences x P prompt positions: two chunks (64 positions, then 6 or
+    36) whose second attends to the first's cache rows; grouped-query heads.
+    The first chunk's 1024 rows run every projection as an MFMA GEMM (Q / K /
+    V and O: OIL8, gate / up: OIL4, down: int8) and the attention in tiles of
+    64 query rows; the second chunk's rows the batched GEMVs (6 x 16 rows) or
+    the GEMMs (36 x 16), and the tiled attention over two context tiles (36
+    positions per sequence) or one workgroup per row (6).  The GPU's FP32 sums run in another
     order than the oracle's, so a value on a rounding boundary can round to
     the other side: an int8 activation of the down projection one step apart
     (the down scale is divided by 16, exactly, so such a step stays below the
@@ -221,14 +224,14 @@ def test_prefill_chunks_and_gqa(kv, oracle):
     cache the logits and cache rows meet the 1e-4 bar; the bf16 cache's flips
     over 1120 rows carry through attention into the logits, so that case has
     the 1e-3 bar the cache rows of later layers have."""
-    cfg = synth.decoder_config(**dict(MID, max_seq=80, heads=8, kv_heads=4, head_dim=64))
+    cfg = synth.decoder_config(**dict(MID, max_seq=P + 10, heads=8, kv_heads=4, head_dim=64))
     model = scaled_down(synth.decoder_model(cfg, config=68, random_gamma=True), 16)
-    want = prefill_vs_oracle(cfg, model, 16, 70, kv, oracle, seed=69, ltol=TOL if kv == "f32" else 1e-3)
+    want = prefill_vs_oracle(cfg, model, 16, P, kv, oracle, seed=69, ltol=TOL if kv == "f32" else 1e-3)
     if kv == "f32":
-        prompts = synth.decoder_prompts(cfg, 16, 70, config=69)
+        prompts = synth.decoder_prompts(cfg, 16, P, config=69)
         orc = oracle.decoder(oracle_cfg(cfg, kv), ffn_off(model))
         cache = orc.new_cache()
-        off = [orc.step(*cache, pos, int(prompts[0, pos]), threads=THREADS) for pos in range(70)][-1]
+        off = [orc.step(*cache, pos, int(prompts[0, pos]), threads=THREADS) for pos in range(P)][-1]
         assert rel(off, want[0]) > 10 * TOL  # measured 3.9e-3
 
 
