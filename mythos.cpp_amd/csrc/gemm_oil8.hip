@@ -64,21 +64,27 @@ struct Oil8GemmSegs {
     int t0[4];  // first N tile of each segment; t0[nseg] = all tiles
 };
 
-template <int BN, int BS>
+template <int BN, int BS, int CW>
 struct Q8Lds {
-    static constexpr int hdr = 1024 + 64;              // table, producer wave maxima
-    static constexpr int tile = BN * 256;              // one K step: hi tile, then lo tile
+    static constexpr int hdr = 1024 + 64;                  // table, producer wave maxima
+    static constexpr int tile = BN * 256;                  // one K step: hi tile, then lo tile
     static constexpr int ring = 2 * BS * tile;
-    static constexpr int stage = 128 * (BN + 4) * 4;   // C (FP32, rows padded by 4)
+    static constexpr int stage = 32 * CW * (BN + 4) * 4;  // C (FP32, rows padded by 4)
     static constexpr int bytes = hdr + (ring > stage ? ring : stage);
 };
 
-template <int BN, int PA, int BS>
-__global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restrict__ A16, const float* __restrict__ a32,
-                                                       Oil8GemmSegs sg, int Mr, int K, const int* __restrict__ rsh,
-                                                       int ntiles) {
-    using L = Q8Lds<BN, BS>;
+// CW consumer waves of 32 real rows each (4: tiles of 128 rows, two waves per
+// SIMD; 8: tiles of 256 rows, three waves per SIMD, so each SIMD has a second
+// consumer to issue MFMAs while one waits for LDS, and each W tile serves
+// twice the rows), then 4 producer waves.
+template <int BN, int PA, int BS, int CW>
+__global__ __launch_bounds__(64 * (CW + 4)) void oil8_prefill_ws(const uint16_t* __restrict__ A16,
+                                                                 const float* __restrict__ a32, Oil8GemmSegs sg,
+                                                                 int Mr, int K, const int* __restrict__ rsh,
+                                                                 int ntiles) {
+    using L = Q8Lds<BN, BS, CW>;
     constexpr int NT = BN / 16, TPR = 256 / BN, BPT = QBK / TPR, NV = BPT / 16, PW = 4;
+    constexpr int MT = 32 * CW, NTH = 64 * (CW + 4);  // real rows per tile, threads
     static_assert(PA == 2 || PA == 4, "A ring index");
     static_assert(BS == 1 || BS == 2 || BS == 4, "barrier interval");
     static_assert(BPT % 16 == 0, "producer piece");
@@ -87,7 +93,7 @@ __global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restric
     float* wred = (float*)(lds + 1024);
     uint8_t* ring = lds + L::hdr;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tm = (Mr + 127) / 128;
+    const int tm = (Mr + MT - 1) / MT;
     int mt, nt;
     {
         const int id = blockIdx.x, total = tm * ntiles;
@@ -114,19 +120,19 @@ __global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restric
     // ---- codebook scale and the non-finite check (codebook entries, rows of the tile)
     float cbv = 0.0f;
     bool fin = true;
-    if (wave >= 4) {
-        cbv = cb[tid - 256];
+    if (wave >= CW) {
+        cbv = cb[tid - 64 * CW];
         fin = __builtin_isfinite(cbv);
         const float m = wave_max(fabsf(cbv));
-        if (lane == 0) wred[wave - 4] = m;
-    } else if (tid < 128) {
-        const int row = 128 * mt + tid;
+        if (lane == 0) wred[wave - CW] = m;
+    } else if (tid < MT) {
+        const int row = MT * mt + tid;
         fin = !(row < Mr && rsh[row] == kRowNonFinite);
     }
     if (__syncthreads_or(!fin)) {
         // FP32 FMAs over the reference's products in column order
-        for (int o = tid; o < 128 * BN; o += 512) {
-            const int r = o / BN, n = o % BN, row = 128 * mt + r;
+        for (int o = tid; o < MT * BN; o += NTH) {
+            const int r = o / BN, n = o % BN, row = MT * mt + r;
             if (row >= Mr) continue;
             const uint8_t* w = idx + (int64_t)(n0 + n) * K;
             const float* a = a32 + (int64_t)row * K;
@@ -138,9 +144,9 @@ __global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restric
     }
     const int sw = fp16_scale_shift(fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3])));
 
-    if (wave >= 4) {
+    if (wave >= CW) {
         // ---------------- producers ----------------
-        const int t = tid - 256;
+        const int t = tid - 64 * CW;
         tab[t] = hl_pair(ldexpf(cbv, sw));
         const int wn = t / TPR, wh = t % TPR;
         const uint8_t* wrow = idx + (int64_t)(n0 + wn) * K + BPT * wh;
@@ -206,10 +212,11 @@ __global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restric
         __syncthreads();
     } else {
         // ---------------- consumers ----------------
-        // virtual 16-row groups: tile mt holds groups 16 mt .. 16 mt + 15, hi parts in the first 8;
-        // wave w: hi groups 2w, 2w + 1 (real rows 32w .. 32w + 31 of the tile) and their lo groups
+        // virtual 16-row groups: 128 real rows are 16 groups, the hi parts in the first 8;
+        // wave w: hi groups 2w', 2w' + 1 (w' = w % 4) of the 128-row block w / 4 of the tile (real rows
+        // 32w .. 32w + 31 of the tile) and their lo groups
         const int kc32 = K / 32;
-        const int gb = 16 * mt + 2 * wave;
+        const int gb = 16 * (MT / 128 * mt + wave / 4) + 2 * (wave % 4);
         const half8* af16 = (const half8*)A16 + lane;
         half8 af[PA][4][2];
         auto load_a = [&](int step, int b) {
@@ -268,7 +275,7 @@ __global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restric
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int rr = 32 * wave + 16 * i + 4 * (lane >> 4) + r;
-                const int sh = rsh[min(128 * mt + rr, Mr - 1)] + sw;
+                const int sh = rsh[min(MT * mt + rr, Mr - 1)] + sw;
 #pragma unroll
                 for (int j = 0; j < NT; ++j)
                     st[rr * (BN + 4) + 16 * j + (lane & 15)] = ldexpf(acc[i][j][r] + acc[i + 2][j][r], -sh);
@@ -277,8 +284,8 @@ __global__ __launch_bounds__(512) void oil8_prefill_ws(const uint16_t* __restric
     }
     constexpr int CPR = BN / 4;
     const float* st = (const float*)ring;
-    for (int c = tid; c < 128 * CPR; c += 512) {
-        const int r = c / CPR, q = c % CPR, row = 128 * mt + r;
+    for (int c = tid; c < MT * CPR; c += NTH) {
+        const int r = c / CPR, q = c % CPR, row = MT * mt + r;
         if (row < Mr) *(float4*)(y + (int64_t)row * N + n0 + 4 * q) = *(const float4*)(st + r * (BN + 4) + 4 * q);
     }
 }
@@ -297,14 +304,16 @@ bool oil8_gemm_x32_supported(const Oil8Seg* seg, int nseg, int64_t Mr, int64_t K
     return tiles * ((Mr + 127) / 128) < (1ll << 31) && Mr * K < (1ll << 40);
 }
 
-size_t oil8_gemm_x32_workspace_bytes(int64_t Mr, int64_t K) { return oil4_gemm_x32_workspace_bytes(Mr, K); }
+// the row shifts, then the hi / lo fragments of Mr rows rounded up to 256
+// (the tiles of 256 rows read both 128-row blocks)
+size_t oil8_gemm_x32_workspace_bytes(int64_t Mr, int64_t K) {
+    return oil4_prefill_shift_bytes(Mr) + (size_t)(2 * ((Mr + 255) / 256 * 256) * K * 2);
+}
 
 hipError_t launch_oil8_gemm_x32(const float* a, const Oil8Seg* seg, int nseg, int64_t Mr, int64_t K, void* ws,
                                 hipStream_t s) {
     if (!oil8_gemm_x32_supported(seg, nseg, Mr, K)) return hipErrorInvalidValue;
     constexpr int BN = 64;
-    hipError_t e = launch_prefill_a16x(a, Mr, K, ws, s);
-    if (e != hipSuccess) return e;
     Oil8GemmSegs g{};
     int t = 0;
     for (int i = 0; i < 3; ++i) {
@@ -326,8 +335,15 @@ hipError_t launch_oil8_gemm_x32(const float* a, const Oil8Seg* seg, int nseg, in
     for (int i = nseg; i < 3; ++i) g.t0[i] = t + 1;  // never selected
     const int* rsh = (const int*)ws;
     const uint16_t* a16 = (const uint16_t*)((const char*)ws + oil4_prefill_shift_bytes(Mr));
-    const int64_t tiles = (Mr + 127) / 128;
-    oil8_prefill_ws<BN, 4, 2><<<(unsigned)(tiles * t), 512, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
+    // tiles of 256 rows (8 consumer waves) when they fill a round of 256 CUs, else of 128
+    const int64_t t256 = (Mr + 255) / 256, t128 = (Mr + 127) / 128;
+    const bool wide = t256 * t >= 256;
+    hipError_t e = launch_prefill_a16x(a, Mr, K, ws, s, wide ? 256 * t256 : 128 * t128);
+    if (e != hipSuccess) return e;
+    if (wide)
+        oil8_prefill_ws<BN, 2, 2, 8><<<(unsigned)(t256 * t), 768, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
+    else
+        oil8_prefill_ws<BN, 4, 2, 4><<<(unsigned)(t128 * t), 512, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
     return hipGetLastError();
 }
 

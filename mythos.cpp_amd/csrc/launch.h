@@ -185,10 +185,11 @@ hipError_t launch_oil4_gemm_x32(const float* a, const uint8_t* nib, const uint16
                                 int64_t Mr, int64_t N, int64_t K, void* ws, hipStream_t s);
 // The FP32 rows' FP16 hi / lo fragments both x32 GEMMs read: ws holds the
 // row shifts (oil4_prefill_shift_bytes(Mr)), then 256 virtual rows per 128
-// real rows of K FP16 values.  A row holding Inf or NaN gets the shift
-// kRowNonFinite.
+// real rows of K FP16 values, for `cover` real rows (a multiple of 128, >= Mr;
+// 0: Mr rounded up to 128; rows past Mr are zeros).  A row holding Inf or NaN
+// gets the shift kRowNonFinite.
 constexpr int kRowNonFinite = 1 << 20;
-hipError_t launch_prefill_a16x(const float* a, int64_t Mr, int64_t K, void* ws, hipStream_t s);
+hipError_t launch_prefill_a16x(const float* a, int64_t Mr, int64_t K, void* ws, hipStream_t s, int64_t cover = 0);
 
 // The prompt prefill's OIL8 projections (gemm_oil8.hip): y_s [Mr][rows_s] =
 // a [Mr][K] W_s^T for up to three weights in one launch (Q, K, V), FP32

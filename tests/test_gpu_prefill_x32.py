@@ -140,8 +140,10 @@ def run_oil4(mth, dev, packed, cbs, block, x, M, K, B):
 
 @pytest.mark.parametrize("M,K,B", [
     (11008, 4096, 256),  # config 2 weights
-    (22016, 4096, 128),  # the decoder's fused gate / up at config 5
+    (22016, 4096, 128),  # the decoder's fused gate / up at config 5, one M tile
     (448, 1024, 130),    # ragged last M tile
+    (4096, 1024, 1024),  # 128-column tiles (a full round of 256 workgroups)
+    (2048, 512, 2000),   # 128-column tiles, 16 M tiles, the last one ragged
 ])
 def test_oil4_gemm_x32(M, K, B, oracle, mth, dev):
     print(f"oil4 x32 GEMM M={M} K={K} B={B}", flush=True)
@@ -153,8 +155,8 @@ def test_oil4_gemm_x32(M, K, B, oracle, mth, dev):
     fp32_close(got, ref, absw, 1e-5, "oil4 x32 GEMM")
 
 
-def test_oil4_gemm_x32_integer_bit_exact(oracle, mth, dev):
-    M, K, B = 192, 1024, 140
+@pytest.mark.parametrize("M,K,B", [(192, 1024, 140), (4096, 512, 1024)])
+def test_oil4_gemm_x32_integer_bit_exact(M, K, B, oracle, mth, dev):
     g = np.random.default_rng(24)
     nib = g.integers(0, 16, (M, K), dtype=np.uint8)
     packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
