@@ -341,7 +341,7 @@ hipError_t launch_oil8_gemm_x32(const float* a, const Oil8Seg* seg, int nseg, in
     hipError_t e = launch_prefill_a16x(a, Mr, K, ws, s, wide ? 256 * t256 : 128 * t128);
     if (e != hipSuccess) return e;
     if (wide)
-        oil8_prefill_ws<BN, 2, 2, 8><<<(unsigned)(t256 * t), 768, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
+        oil8_prefill_ws<BN, 2, 1, 8><<<(unsigned)(t256 * t), 768, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
     else
         oil8_prefill_ws<BN, 4, 2, 4><<<(unsigned)(t128 * t), 512, 0, s>>>(a16, a, g, (int)Mr, (int)K, rsh, t);
     return hipGetLastError();
