@@ -226,6 +226,20 @@ def bench_prefill(mth, dev, M, N, K, steps, warmup, block=128):
     return dict(sec=sec, steps=n, flop=flop, copies=n_cp)
 
 
+def bench_tl2_gemm(mth, dev, M, N, K, steps, warmup):
+    """tl2_gemm with the reference's per-(m,n) weight rows (src/kernel_tl.cpp:109-168):
+    M*N rows of ceil(K/4) code bytes, each used once (a streaming kernel)."""
+    import torch
+    bpr = (2 * K + 7) // 8
+    w = np.random.default_rng(9).integers(0, 256, M * N * bpr, dtype=np.uint8)
+    a = np.random.default_rng(10).normal(0, 1, N * K).astype(np.float32)
+    w_d, a_d = dev_copy(w, dev), dev_copy(a, dev)
+    o = torch.empty(M * N, dtype=torch.float32, device=dev)
+    ws = replicate(w_d, w.nbytes)
+    sec, n = time_graph(lambda i: mth.tl2_gemm(ws[i], a_d, o, M, N, K), len(ws), steps, warmup)
+    return dict(sec=sec, steps=n, bytes=w.nbytes + a.nbytes + 4 * M * N, copies=len(ws))
+
+
 def bench_ternary_gemm(mth, dev, M, N, K, steps, warmup):
     """Ternary prefill GEMM (i2s_gemm_vnni, int8 MFMA): M weight rows x N
     tokens x K; weights rotated over 4 copies (the 5.6 MB of activations and
@@ -385,7 +399,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,i2sb16,floor,prefill,"
+    ap.add_argument("--only", default="", help="comma list: oil4,oil4b16,oil8,oil8b16,i2s,i2sb16,tl2,floor,prefill,"
                                                "ternary_gemm,decode (default all); floor: each GEMV's streaming floor")
     ap.add_argument("--decode-batches", default="1,16", help="comma list of decode batch sizes (config 5)")
     args = ap.parse_args()
@@ -456,6 +470,10 @@ def main():
         r = bench_i2s_gemv_i8(mth, dev, 4096, 11008, 16, args.steps, args.warmup)
         extra["i2s_gemv_4096x11008_b16_int8"] = e = gemv_entry("i2s_gemv_4096x11008_b16_int8", r)
         log(f"i2s b=16 (int8 acts, 4096x11008): {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
+    if want("tl2"):
+        r = bench_tl2_gemm(mth, dev, 4096, 4, 4095, args.steps, args.warmup)
+        extra["tl2_gemm_4096x4x4095"] = e = gemv_entry("tl2_gemm_4096x4x4095", r)
+        log(f"tl2 gemm (per-(m,n) rows, 4096x4x4095): {e['us']:.2f} us/launch, {e['GBps']:.0f} GB/s")
     if want("prefill"):
         r = bench_prefill(mth, dev, 512, 14336, 4096, args.steps, args.warmup)
         tf = r["flop"] / r["sec"] / 1e12

@@ -386,6 +386,13 @@ int mth_tl2_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int6
     REQUIRE(w && act && out, "mth_tl2_gemm: null pointer");
     REQUIRE(M > 0 && N > 0 && K > 0 && M * N < kMaxDim && K < (1ll << 24), "mth_tl2_gemm: bad sizes");
     REQUIRE(K % 3 == 0, "mth_tl2_gemm: K=%lld must be a multiple of 3", (long long)K);
+    const size_t need = mth::tl2_workspace_bytes(w, M, N, K);
+    if (need) {
+        void* ws = nullptr;
+        const hipError_t e = workspace(S(stream), need, &ws);
+        if (e != hipSuccess) return workspace_fail("mth_tl2_gemm", e, need);
+        return check_launch(mth::launch_tl2_gemm_ws(w, act, out, M, N, K, ws, S(stream)), "mth_tl2_gemm");
+    }
     return check_launch(mth::launch_tl2_gemm(w, act, out, M, N, K, S(stream)), "mth_tl2_gemm");
 }
 

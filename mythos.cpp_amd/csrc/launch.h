@@ -156,6 +156,12 @@ hipError_t launch_tl1_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 hipError_t launch_tl2_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
+// Whole 16-byte segments per weight row (ceil(K/4) % 16 == 0, aligned w):
+// the activations quantised once per row into ws (tl2_workspace_bytes, 0 when
+// the shape takes launch_tl2_gemm), then a streaming v_dot4 kernel.
+size_t tl2_workspace_bytes(const uint8_t* w, int64_t M, int64_t N, int64_t K);
+hipError_t launch_tl2_gemm_ws(const uint8_t* w, const float* a, float* o, int64_t M, int64_t N, int64_t K, void* ws,
+                              hipStream_t s);
 
 // ---- OIL4 prefill GEMM (gemm_oil4.hip) -----------------------------------
 // Each row of A is scaled by a power of two into FP16's range and the output

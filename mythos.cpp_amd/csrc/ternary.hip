@@ -822,6 +822,76 @@ __global__ __launch_bounds__(kWG) void tl2_gemm_k(const uint8_t* __restrict__ w,
     if (lane == 0) o[id] = __fdiv_rn((float)acc, sc);
 }
 
+// The same sums when every weight row is whole 16-byte segments (ceil(K/4)
+// % 16 == 0, 16-byte aligned w).  The tl2_gemm codes are the I2_S codes (2
+// bits per weight, weight i at bits 2(i % 4) of byte i / 4, decode_tl2
+// :81-86: 00 -> -1, 01 -> 0, 1x -> +1), so the sum is the I2_S kernels'
+// sum_k u q - sum_k q on v_dot4 (u = t + 1).  tl2_quant_k quantises each
+// activation row once (the reference's per-row loop :118-129 is
+// quantize_per_token's arithmetic: absmax with the 1e-10 floor, 127/max,
+// round half away) straight into the operand order: byte-transposed per 16
+// columns (column 4b + j at byte 4j + b) and zero-padded to whole 64-column
+// segments, so codes past K meet q = 0.  tl2_rows_k: wave = R rows (m, n)
+// of one activation row n; lane l takes segments l, l + 64, ... of its R
+// rows (16 code bytes each) and the segment's 64 q bytes, loaded once for
+// the R rows.  No weight is shared between outputs (every (m, n) has its
+// own row in the reference's layout), so this is a streaming kernel.
+__global__ __launch_bounds__(kWG) void tl2_quant_k(const float* __restrict__ a, int8_t* __restrict__ qt,
+                                                   float* __restrict__ qscale, int K, int stride) {
+    __shared__ float red[kWaves];
+    const int64_t n = blockIdx.x;
+    const float* x = a + n * K;
+    const float sc = __fdiv_rn(127.0f, block_absmax(x, K, red));
+    int8_t* dst = qt + n * stride;
+    for (int i = threadIdx.x; i < stride; i += kWG)
+        dst[(i & ~15) | ((i & 3) << 2) | ((i >> 2) & 3)] = i < K ? (int8_t)quant_i8(x[i], sc) : (int8_t)0;
+    if (threadIdx.x == 0) qscale[n] = sc;
+}
+
+template <int R>
+__global__ __launch_bounds__(kWG) void tl2_rows_k(const uint8_t* __restrict__ w, const int8_t* __restrict__ qt,
+                                                  const float* __restrict__ qscale, float* __restrict__ o,
+                                                  int64_t M, int64_t N, int bpr) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t n = blockIdx.y, m0 = ((int64_t)blockIdx.x * kWaves + wave) * R;
+    if (m0 >= M) return;  // uniform per wave, no barrier in this kernel
+    const int nseg = bpr / 16;
+    const int8_t* qn = qt + n * (int64_t)nseg * 64;
+    int acc[R], asum = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0;
+    for (int seg = lane; seg < nseg; seg += 64) {
+        uint4 wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t m = min(m0 + r, M - 1);
+            wv[r] = ld_stream(w + (m * N + n) * bpr + (int64_t)seg * 16);
+        }
+        uint32_t A[4][4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint4 v = *(const uint4*)(qn + seg * 64 + 16 * d);
+            A[d][0] = v.x, A[d][1] = v.y, A[d][2] = v.z, A[d][3] = v.w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asum = dot4(A[d][j], 0x01010101u, asum);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = tdot16(wv[r].x, A[0], acc[r]);
+            acc[r] = tdot16(wv[r].y, A[1], acc[r]);
+            acc[r] = tdot16(wv[r].z, A[2], acc[r]);
+            acc[r] = tdot16(wv[r].w, A[3], acc[r]);
+        }
+    }
+    asum = group_sum_i<64>(asum);
+    const float sc = qscale[n];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int tot = group_sum_i<64>(acc[r]) - asum;
+        if (lane == 0 && m0 + r < M) o[(m0 + r) * N + n] = __fdiv_rn((float)tot, sc);
+    }
+}
+
 __global__ __launch_bounds__(kWG) void dequantize_k(const int8_t* __restrict__ src, float* __restrict__ dst,
                                                     int64_t n, float inv) {
     const int64_t i = (int64_t)blockIdx.x * kWG + threadIdx.x;
@@ -1486,6 +1556,26 @@ hipError_t launch_tl1_gemm(const uint8_t* w, const float* a, float* o, int64_t M
 hipError_t launch_tl2_gemm(const uint8_t* w, const float* a, float* o, int64_t M, int64_t N, int64_t K,
                            hipStream_t s) {
     tl2_gemm_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);
+    return hipGetLastError();
+}
+
+constexpr int kTl2R = 4;  // rows per wave
+
+size_t tl2_workspace_bytes(const uint8_t* w, int64_t M, int64_t N, int64_t K) {
+    const int64_t bpr = (2 * K + 7) / 8;  // = 16 * segments; the transposed q rows are 64 * segments bytes
+    const bool fast = bpr % 16 == 0 && aligned16(w) && K <= (1 << 20) && N <= 65535 &&
+                      (M + kWaves * kTl2R - 1) / (kWaves * kTl2R) < (1ll << 31);
+    return fast ? (size_t)(((N * bpr * 4 + 255) / 256) * 256 + N * 4) : 0;
+}
+
+hipError_t launch_tl2_gemm_ws(const uint8_t* w, const float* a, float* o, int64_t M, int64_t N, int64_t K, void* ws,
+                              hipStream_t s) {
+    const int bpr = (int)((2 * K + 7) / 8), stride = 4 * bpr;
+    int8_t* qt = (int8_t*)ws;
+    float* qscale = (float*)((char*)ws + ((N * (int64_t)stride + 255) / 256) * 256);
+    tl2_quant_k<<<(unsigned)N, kWG, 0, s>>>(a, qt, qscale, (int)K, stride);
+    const dim3 grid((unsigned)((M + kWaves * kTl2R - 1) / (kWaves * kTl2R)), (unsigned)N);
+    tl2_rows_k<kTl2R><<<grid, kWG, 0, s>>>(w, qt, qscale, o, M, N, bpr);
     return hipGetLastError();
 }
 

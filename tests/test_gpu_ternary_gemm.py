@@ -49,7 +49,11 @@ def test_tl1_gemm_bit_exact(M, N, K, oracle, mth, dev):
     assert np.array_equal(out.cpu().numpy(), oracle.tl1_gemm(w, a, M, N, K))
 
 
-@pytest.mark.parametrize("M,N,K", [(4, 4, 12), (5, 3, 36), (2, 2, 9), (8, 2, 1023)])
+# ceil(K / 4) % 16 == 0 (1023, 3069, 4095, 12285) takes the streaming v_dot4
+# kernel over activations quantised once per row, the others one wave per
+# output; codes past K (the last byte's spare fields) are random in both
+@pytest.mark.parametrize("M,N,K", [(4, 4, 12), (5, 3, 36), (2, 2, 9), (8, 2, 1023), (64, 16, 3069), (33, 5, 4095),
+                                   (256, 16, 12285), (17, 1, 1023)])
 def test_tl2_gemm_bit_exact(M, N, K, oracle, mth, dev):
     import torch
     g = np.random.default_rng(M + N + K + 7)
