@@ -1037,6 +1037,7 @@ bool attention_supported(int head_dim, int max_seq) {
 // P V accumulated per thread for its 4 rows x D / 16 columns; at the end
 // the rows are divided by their sums.  The same softmax and weighted sum as
 // the decode kernel up to FP32 rounding order.
+namespace {
 template <int D, typename KV>
 __global__ __launch_bounds__(256) void attn_prefill_k(const float* __restrict__ q, const KV* __restrict__ kc,
                                                       const KV* __restrict__ vc, float* __restrict__ out, int np,
@@ -1160,6 +1161,8 @@ __global__ __launch_bounds__(256) void attn_prefill_k(const float* __restrict__ 
             *(float4*)(dst + 64 * c) = make_float4(o[a][c].x * inv, o[a][c].y * inv, o[a][c].z * inv, o[a][c].w * inv);
     }
 }
+
+}  // namespace
 
 template <bool ROPE, typename KV>
 static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& v, const NormScale& ns,
