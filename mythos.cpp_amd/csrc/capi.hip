@@ -181,7 +181,7 @@ int mth_oil8_gemv(const uint8_t* indices, const float* codebook, const float* x,
             "mth_oil8_gemv: bad sizes M=%lld K=%lld batch=%lld", (long long)M, (long long)K, (long long)batch);
     const bool aligned = (((uintptr_t)indices | (uintptr_t)x) & 15u) == 0;
     const mth::Oil8Seg seg{indices, codebook, y, M};
-    if (batch >= kGemmRows && mth::oil8_gemm_x32_supported(&seg, 1, batch, K)) {
+    if (aligned && batch >= kGemmRows && mth::oil8_gemm_x32_supported(&seg, 1, batch, K)) {
         // >= 128 tokens: the MFMA GEMM (each weight read once per 128 tokens)
         void* ws = nullptr;
         const size_t need = mth::oil8_gemm_x32_workspace_bytes(batch, K);

@@ -110,7 +110,7 @@ hipError_t qkv(const mth_decoder* d, const mth_decoder_layer& L, const float* h,
     const int64_t H = c.hidden, QD = c.heads * c.head_dim, KD = c.kv_heads * c.head_dim;
     const mth::Oil8Seg seg[3] = {{L.wq, L.cbq, q, QD}, {L.wk, L.cbk, k, KD}, {L.wv, L.cbv, v, KD}};
     // prompt chunks of >= kPfGemmRows rows: the FP32-row OIL8 GEMM on MFMA
-    if (rows >= kPfGemmRows && d->pf_ws && mth::oil8_gemm_x32_supported(seg, 3, rows, H))
+    if (rows >= kPfGemmRows && d->pf_ws && ((uintptr_t)h & 15u) == 0 && mth::oil8_gemm_x32_supported(seg, 3, rows, H))
         return mth::launch_oil8_gemm_x32(h, seg, 3, rows, H, d->pf_ws, s);
     if (((uintptr_t)h & 15u) == 0) {
         if (rows >= 2) {
@@ -170,7 +170,7 @@ hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
                                            (int)c.kv_heads, (int)c.head_dim, (int)c.max_seq, s));
             {
                 const mth::Oil8Seg so{L.wo, L.cbo, d->pf_t, H};
-                if (R >= kPfGemmRows && mth::oil8_gemm_x32_supported(&so, 1, R, QD))
+                if (R >= kPfGemmRows && ((uintptr_t)d->pf_att & 15u) == 0 && mth::oil8_gemm_x32_supported(&so, 1, R, QD))
                     TRY(mth::launch_oil8_gemm_x32(d->pf_att, &so, 1, R, QD, d->pf_ws, s));
                 else
                     TRY(oil8(d, L.wo, L.cbo, d->pf_att, d->pf_t, H, QD, s, R));
