@@ -9,11 +9,16 @@
  * never accumulated.
  *
  * Workspace.  The batched GEMVs (mth_oil8_gemv, mth_oil4_gemv, mth_i2s_gemv
- * with batch >= 2), mth_argmax, mth_oil4_gemm_prefill (per-row shifts of A,
+ * with batch >= 2; for batches of >= 128 tokens mth_oil8_gemv and
+ * mth_oil4_gemv run as MFMA GEMMs and keep each token row's FP16 hi / lo parts,
+ * 4 * K bytes per token rounded up to 128 (OIL4) or 256 (OIL8) tokens,
+ * plus 4 bytes per token),
+ * mth_argmax, mth_oil4_gemm_prefill (per-row shifts of A,
  * 4 bytes per row, and an FP16 copy of A in MFMA fragment order,
  * ceil(M/16)*16*K*2 bytes, for K % 256 == 0, codebook blocks of a multiple
- * of 128 and N a multiple of 64, 96 or 112) and
- * mth_i2s_gemm_vnni (permuted activations,
+ * of 128 and N a multiple of 64, 96 or 112), mth_tl2_gemm (each activation
+ * row quantised once: N * ceil(K/4) * 4 bytes plus 4 bytes per row, when
+ * ceil(K/4) % 16 == 0) and mth_i2s_gemm_vnni (permuted activations,
  * for its MFMA shapes) keep intermediate data in a device workspace
  * the library owns, one per (device, stream).  The first call that needs more
  * than the stream's workspace holds allocates a larger one (hipMalloc, at
@@ -79,7 +84,11 @@ int mth_oil8_gemm(const uint8_t* indices, const float* codebook, const float* ac
 /* Decode GEMV over one OIL8 weight matrix shared by `batch` tokens (the
  * reference's oil8_gemm with N = 1, once per token, src/kernel_oil8.cpp:30-60):
  *   y[t*M + m] = sum_k codebook[indices[m*K + k]] * x[t*K + k],  t < batch.
- * Fast path: K % 16 == 0, K <= 4096, indices and x 16-byte aligned. */
+ * Fast path: K % 16 == 0, K <= 4096, indices and x 16-byte aligned.  Batches
+ * of >= 128 tokens with M % 64 == 0, K % 256 == 0 and 16-byte aligned y run
+ * as the prompt prefill's MFMA GEMM (FP16 hi / lo parts of x and codebook,
+ * FP32 sums: the FP32 bar; rows or codebooks holding Inf / NaN take FP32
+ * products). */
 int mth_oil8_gemv(const uint8_t* indices, const float* codebook, const float* x, float* y,
                   int64_t M, int64_t K, int64_t batch, mth_stream_t stream);
 
@@ -101,7 +110,10 @@ int mth_oil4_gemm(const uint8_t* packed, const uint16_t* codebook, const float* 
  * packed: M rows of K/2 bytes, nibble order as above.  cb_block = 0 selects
  * a single shared 16-entry codebook.  Requires K even and, for cb_block > 0,
  * K % cb_block == 0.  Fast path: K % 32 == 0, K <= 4096, cb_block % 32 == 0,
- * 16-byte aligned packed / codebooks / x. */
+ * 16-byte aligned packed / codebooks / x.  Batches of >= 128 tokens with
+ * cb_block a multiple of 128, K % 256 == 0, M a multiple of 64, 96, 112 or
+ * 128 and 16-byte aligned y run as the prompt prefill's MFMA GEMM (FP16 hi /
+ * lo parts of x, FP32 sums). */
 int mth_oil4_gemv(const uint8_t* packed, const uint16_t* codebooks, int64_t cb_block,
                   const float* x, float* y, int64_t M, int64_t K, int64_t batch,
                   mth_stream_t stream);
@@ -184,7 +196,10 @@ int mth_tl1_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int6
                  mth_stream_t stream);
 
 /* oil::kernel::tl2_gemm (include/oil/kernel.h:26-27, src/kernel_tl.cpp:109-168).
- * Requires K % 3 == 0 (the reference reads past the activation row otherwise). */
+ * Requires K % 3 == 0 (the reference reads past the activation row otherwise).
+ * Rows of whole 16-byte segments (ceil(K/4) % 16 == 0) and a 16-byte aligned
+ * w stream through a v_dot4 kernel after one quantisation per activation row
+ * (workspace); other shapes run one wave per output.  Bit-exact either way. */
 int mth_tl2_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int64_t N, int64_t K,
                  mth_stream_t stream);
 
