@@ -50,8 +50,10 @@ def test_oil8_gemm_x32(M, K, B, oracle, mth, dev):
     fp32_close(got, ref, absw8(idx, cb, x), 1e-5, "oil8 x32 GEMM")
 
 
-def test_oil8_gemm_x32_integer_bit_exact(oracle, mth, dev):
-    M, K, B = 384, 2048, 200
+# (4096, 512, 1024): tiles of 256 rows on 8 consumer waves (they fill a round of
+# 256 workgroups); the others tiles of 128 rows on 4
+@pytest.mark.parametrize("M,K,B", [(384, 2048, 200), (4096, 512, 1024)])
+def test_oil8_gemm_x32_integer_bit_exact(M, K, B, oracle, mth, dev):
     g = np.random.default_rng(21)
     idx = g.integers(0, 256, (M, K), dtype=np.uint8)
     cb = (np.arange(256) - 128).astype(np.float32) * 3
@@ -61,12 +63,12 @@ def test_oil8_gemm_x32_integer_bit_exact(oracle, mth, dev):
     assert np.array_equal(got, oracle.oil8_gemv(idx, cb, x, M, K, B))
 
 
-def test_oil8_gemm_x32_range(oracle, mth, dev):
+@pytest.mark.parametrize("M,K,B", [(256, 2048, 160), (4096, 256, 1024)])
+def test_oil8_gemm_x32_range(M, K, B, oracle, mth, dev):
     """Codebook magnitudes 2^-60 .. 2^40 and row scales 2^-40 .. 2^40 (every
     product and sum a normal FP32 number), an all-zero row too: the
     power-of-two scales of rows and codebook put every hi / lo part in FP16's
     range, so the FP32 bar holds for every row."""
-    M, K, B = 256, 2048, 160
     g = np.random.default_rng(22)
     idx = g.integers(0, 256, (M, K), dtype=np.uint8)
     cb = (g.normal(0, 1, 256) * np.exp2(g.integers(-60, 40, 256))).astype(np.float32)
@@ -81,13 +83,13 @@ def test_oil8_gemm_x32_range(oracle, mth, dev):
         fp32_close(got[t], ref[t], aw[t], 1e-5, f"oil8 x32 range row {t}")
 
 
+@pytest.mark.parametrize("M,K,B", [(192, 1024, 300), (4096, 256, 1000)])
 @pytest.mark.parametrize("where", ["codebook_inf", "codebook_nan", "x_inf", "x_nan"])
-def test_oil8_gemm_x32_non_finite(where, oracle, mth, dev):
+def test_oil8_gemm_x32_non_finite(where, M, K, B, oracle, mth, dev):
     """Workgroups whose codebook or rows hold Inf / NaN sum the reference's
     FP32 products directly: non-finite outputs match the oracle's class (NaN,
     +Inf, -Inf) element by element, finite ones the FP32 bar (the other M
-    tiles keep the MFMA path)."""
-    M, K, B = 192, 1024, 300
+    tiles keep the MFMA path).  (4096, 256, 1000): tiles of 256 rows."""
     g = np.random.default_rng(23)
     idx = g.integers(0, 256, (M, K), dtype=np.uint8)
     cb = g.normal(0, 0.02, 256).astype(np.float32)
@@ -106,7 +108,7 @@ def test_oil8_gemm_x32_non_finite(where, oracle, mth, dev):
         x[1, 77] = np.inf
         x[290, 3] = -np.inf
     else:
-        x[140, 500] = np.nan
+        x[140, 200] = np.nan
     print(f"oil8 x32 GEMM non-finite {where}", flush=True)
     got = run_oil8(mth, dev, idx, cb, x, M, K, B)
     with np.errstate(all="ignore"):
