@@ -91,6 +91,12 @@ void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch, ResidOut ro) 
 #pragma unroll
     for (int q = 0; q < 4; ++q) xq[q] = ldf4(x + kl + 4 * q);
     const float cbv = cb[tid];
+    // residual epilogue operands of token 0 (lane r of wave 0: row m0 + r), issued before the weight stream so the
+    // epilogue does not wait for a round trip at the end; every lane loads (clamped), no branch around the loads
+    const int rrow = min(m0 + (lane % R), M - 1);
+    const float* rxp = ro.x ? ro.x : x;
+    const float* rgp = ro.x ? ro.gamma : x;
+    const float rx0 = rxp[ro.x ? rrow : 0], rg0 = rgp[ro.x ? rrow : 0];
     __builtin_amdgcn_sched_barrier(0);
     uint4 w[R];
 #pragma unroll
@@ -136,9 +142,9 @@ void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch, ResidOut ro) 
                 // residual epilogue (ResidOut, common.h): rows of this workgroup
                 double sq = 0.0;
                 if (wr) {
-                    const float r = v + ro.x[i];
+                    const float r = v + (t == 0 ? rx0 : ro.x[i]);
                     ro.x[i] = r;
-                    ro.xg[i] = r * ro.gamma[m0 + lane];
+                    ro.xg[i] = r * (t == 0 ? rg0 : ro.gamma[m0 + lane]);
                     sq = (double)r * r;
                 }
                 sq = wave_sum_dbl(sq);

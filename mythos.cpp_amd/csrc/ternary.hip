@@ -407,6 +407,9 @@ __global__ __launch_bounds__(kIaT) void i2s_act_k(const float* __restrict__ act,
     float4 av[NA];
 #pragma unroll
     for (int j = 0; j < NA; ++j) av[j] = ((const float4*)act)[min(tid + j * T, n4 - 1)];
+    // residual epilogue operands (lane r < R: row row0 + r), issued before the weights (clamped, unconditional)
+    const int rrow = min(row0 + (lane % R), M - 1);
+    const float rx0 = (res.x ? res.x : act)[res.x ? rrow : 0], rg0 = (res.x ? res.gamma : act)[res.x ? rrow : 0];
     uint4 w[R][NSEG];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -490,9 +493,9 @@ __global__ __launch_bounds__(kIaT) void i2s_act_k(const float* __restrict__ act,
     if (lane < R) {
         double sq = 0.0;
         if (row < M) {
-            const float r = vr + res.x[row];
+            const float r = vr + rx0;
             res.x[row] = r;
-            res.xg[row] = r * res.gamma[row];
+            res.xg[row] = r * rg0;
             sq = (double)r * r;
         }
         rsq[wave * R + lane] = sq;
