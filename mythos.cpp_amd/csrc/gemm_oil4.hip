@@ -377,10 +377,10 @@ __global__ __launch_bounds__(256) void oil4_prefill_a16(const uint16_t* __restri
 // ===================================================================
 // Prefill kernel, producer / consumer waves (oil4_prefill_ws)
 // ===================================================================
-// A workgroup has 8 waves, two per SIMD, and computes a 256 x BN tile of C:
-// waves 0-3 (consumers) hold the accumulators of 64 rows each and run
+// A workgroup has 8 waves, two per SIMD (or 12 with CW = 8 consumers), and computes a 256 x BN tile of C:
+// waves 0-3 (consumers) hold the accumulators of 64 rows each (32 with CW = 8) and run
 // v_mfma_f32_16x16x32_f16 with A fragments loaded from L2 into a ring of PA
-// registers sets (PA - 1 K steps ahead); waves 4-7 (producers) dequantise W
+// registers sets (PA - 1 K steps ahead); waves CW .. CW + 3 (producers) dequantise W
 // (v_perm lookups, oil4_common.h) into a ring of 2 BS FP16 tiles in LDS, one
 // tile per K step of 64, BS steps ahead of the consumers; one barrier per BS
 // steps hands the tiles over.  The SIMD interleaves the two waves, so the
@@ -407,8 +407,11 @@ struct Pf2Lds {
 // 128-255 the lo parts of real rows 128 T .. 128 T + 127 (Mr real rows);
 // the epilogue adds the two halves' FP32 sums (products exact, sums FP32:
 // the FP32 dot product) and writes FP32 C [Mr][N].
-template <int BN, int PA, int BS, bool X32 = false>
-__global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restrict__ A16, const uint8_t* nib,
+// CW: consumer waves (4: 64 rows each, one per SIMD; 8: 32 rows each, two per SIMD beside the producer wave);
+// the workgroup has ws_threads(CW) threads.
+constexpr int ws_threads(int cw) { return 64 * (cw + 4); }
+template <int BN, int PA, int BS, bool X32 = false, int CW = 4>
+__global__ __launch_bounds__(ws_threads(CW)) void oil4_prefill_ws(const uint16_t* __restrict__ A16, const uint8_t* nib,
                                                        const uint16_t* cbs, int cb_block, void* __restrict__ Cv,
                                                        int M, int N, int K, const int* __restrict__ rsh, int Mr = 0) {
     using L = Pf2Lds<BN, BS, X32>;
@@ -433,9 +436,12 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
     const int m0 = mt * PBM, n0 = nt * BN;
     const int steps = K / PBK;
 
-    if (wave >= 4) {
+    static_assert(CW == 4 || CW == 8, "consumer waves");
+    constexpr int NG = 16 / CW;  // 16-row groups per consumer wave
+    constexpr int NTH = ws_threads(CW);
+    if (wave >= CW) {
         // ---------------- producers ----------------
-        const int t = tid - 256;
+        const int t = tid - 64 * CW;
         const bool wt = t < 2 * BN;
         const int wn = t >> 1, wh = t & 1;
         const int wrow = n0 + (wt ? wn : 0);
@@ -495,20 +501,20 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
     } else {
         // ---------------- consumers ----------------
         const int kc32 = K / 32;
-        const int g0 = (m0 >> 4) + 4 * wave, gmax = ((M + 15) >> 4) - 1;
+        const int g0 = (m0 >> 4) + NG * wave, gmax = ((M + 15) >> 4) - 1;
         const half8* af16 = (const half8*)A16 + lane;
-        half8 af[PA][4][2];
+        half8 af[PA][NG][2];
         auto load_a = [&](int step, int b) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NG; ++i) {
                 const int g = min(g0 + i, gmax);
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) af[b][i][kk] = af16[((int64_t)g * kc32 + 2 * step + kk) * 64];
             }
         };
-        floatx4 acc[4][NT];
+        floatx4 acc[NG][NT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NG; ++i)
 #pragma unroll
             for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -527,7 +533,7 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
                     for (int j = 0; j < NT; ++j)
                         bfr[j] = *(const half8*)(cur + pf_off(16 * j + (lane & 15), 4 * kk + (lane >> 4)));
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < NG; ++i)
 #pragma unroll
                         for (int j = 0; j < NT; ++j)
                             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u % PA][i][kk], bfr[j], acc[i][j], 0,
@@ -540,20 +546,20 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
         if constexpr (X32) {
             float* st = (float*)lds;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int rr = 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+                    const int rr = 16 * NG * wave + 16 * i + 4 * (lane >> 4) + r;
 #pragma unroll
                     for (int j = 0; j < NT; ++j) st[rr * BN + 16 * j + (lane & 15)] = acc[i][j][r];
                 }
         } else {
             uint16_t* st = (uint16_t*)lds;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int rr = 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+                    const int rr = 16 * NG * wave + 16 * i + 4 * (lane >> 4) + r;
                     const int sh = rsh[min(m0 + rr, M - 1)];
 #pragma unroll
                     for (int j = 0; j < NT; ++j)
@@ -567,7 +573,7 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
         float* C = (float*)Cv;
         const float* st = (const float*)lds;
         constexpr int CPR = BN / 4;
-        for (int c = tid; c < 128 * CPR; c += 512) {
+        for (int c = tid; c < 128 * CPR; c += NTH) {
             const int r = c / CPR, q = c % CPR, row = 128 * mt + r;
             if (row < Mr) {
                 const int sh = rsh[row];
@@ -581,7 +587,7 @@ __global__ __launch_bounds__(512) void oil4_prefill_ws(const uint16_t* __restric
         uint16_t* C = (uint16_t*)Cv;
         const uint16_t* st = (const uint16_t*)lds;
         constexpr int CPR = BN * 2 / 16;
-        for (int c = tid; c < 256 * CPR; c += 512) {
+        for (int c = tid; c < 256 * CPR; c += NTH) {
             const int r = c / CPR, q = c % CPR;
             if (m0 + r < M) *(uint4*)(C + (int64_t)(m0 + r) * N + n0 + 8 * q) = *(const uint4*)(st + r * BN + 8 * q);
         }
@@ -706,11 +712,12 @@ hipError_t launch_oil4_gemm_prefill_a16(const uint16_t* a_bf16, const uint8_t* n
     const int bn = pick_bn_v2(M, N);
     const unsigned grid = (unsigned)(((M + PBM - 1) / PBM) * (N / bn));
     const int cbk = (int)cb_block, m = (int)M, n = (int)N, k = (int)K;
+    constexpr int T4 = ws_threads(4);
     switch (bn) {
-        case 128: oil4_prefill_ws<128, 2, 1><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
-        case 112: oil4_prefill_ws<112, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
-        case 96: oil4_prefill_ws<96, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
-        default: oil4_prefill_ws<64, 4, 2><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        case 128: oil4_prefill_ws<128, 2, 1><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        case 112: oil4_prefill_ws<112, 4, 2><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        case 96: oil4_prefill_ws<96, 4, 2><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
+        default: oil4_prefill_ws<64, 4, 2><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c_bf16, m, n, k, rsh); break;
     }
     return hipGetLastError();
 }
@@ -746,15 +753,20 @@ hipError_t launch_oil4_gemm_x32(const float* a, const uint8_t* nib, const uint16
     // 128-column tiles whenever they fill a round of 256 CUs: they halve the
     // A fragment loads per product and the W tile is dequantised for twice the
     // columns per barrier (measured at 1024 rows x 22016 x 4096: 528 -> 461 us
-    // against the best-fill 64-column tiles)
+    // against the best-fill 64-column tiles), on 8 consumer waves of 32 rows
+    // (two per SIMD: one issues MFMAs while the other waits; 468 -> 434 us;
+    // at config 4's 512 x 14336 x 4096 they measured slower, 70 -> 73-78 us)
     const int bn = (N % 128 == 0 && tiles * (N / 128) >= 256) ? 128 : pick_bn_v2(mv, N);
     const unsigned grid = (unsigned)(tiles * (N / bn));
     const int cbk = (int)cb_block, m = (int)mv, n = (int)N, k = (int)K, mr = (int)Mr;
+    constexpr int T4 = ws_threads(4);
     switch (bn) {
-        case 128: oil4_prefill_ws<128, 2, 1, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
-        case 112: oil4_prefill_ws<112, 4, 2, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
-        case 96: oil4_prefill_ws<96, 4, 2, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
-        default: oil4_prefill_ws<64, 4, 2, true><<<grid, 512, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
+        case 128:
+            oil4_prefill_ws<128, 4, 1, true, 8><<<grid, ws_threads(8), 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr);
+            break;
+        case 112: oil4_prefill_ws<112, 4, 2, true><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
+        case 96: oil4_prefill_ws<96, 4, 2, true><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
+        default: oil4_prefill_ws<64, 4, 2, true><<<grid, T4, 0, s>>>(a16, nib, cbs, cbk, c, m, n, k, rsh, mr); break;
     }
     return hipGetLastError();
 }
