@@ -427,10 +427,12 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
     __builtin_amdgcn_sched_barrier(0);
 
     Oil4TileLoads<NPH, SHARED> w;
-    if (PAIR)
-        w.issue_rows(nib, cbs, blockIdx.x * 8, sw.F + blockIdx.x * 8, M, K, k0, lane);
-    else
-        w.issue(nib, cbs, row0, M, K, k0, lane);
+    const int rowA = PAIR ? blockIdx.x * 8 : row0, rowB = PAIR ? sw.F + blockIdx.x * 8 : row0 + 8;
+    // Phase 0's weights (and its phase pair's codebooks) now, the other phases' after the x conversion: a CU
+    // returns loads in issue order, so the phase-0 data of every workgroup on the CU comes back before any
+    // workgroup's later phases and each wave computes phase 0 while the rest streams in (11008 x 4096:
+    // 11.08 -> 10.40 us against issuing every phase here; after phase 0's products instead: 11.01 us).
+    w.template issue_phases<0, 1>(nib, cbs, rowA, rowB, M, K, k0, lane);
     CbPlanes shared_planes;
     if (SHARED) shared_planes = cb_planes(ld16(cbs), ld16(cbs + 8));
     // (PAIR) norm_scale<16>'s wave sums of this wave's virtual waves, before
@@ -494,6 +496,10 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
     }
     wave_lds_order();
     __builtin_amdgcn_sched_barrier(0);  // no weight-data wait above this point
+    if constexpr (NPH > 1) {
+        w.template issue_phases<1, NPH>(nib, cbs, rowA, rowB, M, K, k0, lane);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     // B of MFMA (p, m): column 0 = hi, column 1 = lo; D column n depends on B
     // column n only, so the other columns repeat them and are discarded.

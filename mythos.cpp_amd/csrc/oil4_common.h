@@ -190,6 +190,12 @@ struct Oil4TileLoads {
     // past M - 1 read row M - 1).
     __device__ __forceinline__ void issue_rows(const uint8_t* nib, const uint16_t* cbs, int rowA, int rowB, int M,
                                                int K, int k0, int lane) {
+        issue_phases<0, NPH>(nib, cbs, rowA, rowB, M, K, k0, lane);
+    }
+    // Phases P0 .. P1 - 1 only (P0 even: a phase pair's codebooks load with its first phase).
+    template <int P0, int P1>
+    __device__ __forceinline__ void issue_phases(const uint8_t* nib, const uint16_t* cbs, int rowA, int rowB, int M,
+                                                 int K, int k0, int lane) {
         const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
         const int nbr = K >> 7;  // codebook blocks per row
         const uint8_t* nx = nib + (int64_t)min(rowA + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
@@ -199,7 +205,7 @@ struct Oil4TileLoads {
         const uint16_t* cl0 = cbs + ((int64_t)min(rowA + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
         const uint16_t* cl1 = cbs + ((int64_t)min(rowB + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
 #pragma unroll
-        for (int p = 0; p < NPH; ++p) {
+        for (int p = P0; p < P1; ++p) {
             if (!SHARED && p % 2 == 0) {
                 c0[p / 2] = ld16(cl0 + (p / 2) * 64);
                 c1[p / 2] = ld16(cl1 + (p / 2) * 64);
