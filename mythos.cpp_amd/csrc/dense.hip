@@ -398,10 +398,11 @@ __device__ __forceinline__ uint2 kv_raw4(const uint16_t* p) { return *(const uin
 // head kh = h % kv_heads, cache rows [b][kh][t][D].
 // Latency, not bandwidth, bounds this kernel at decode sizes, so the cache
 // rows are loaded as early as their order of use allows (the CU returns
-// loads in issue order): first each thread's K row of the first 256
-// positions, then the V rows it accumulates in P*V (up to VP of them,
-// positions sl + SL j, kept packed), so the scores wait only for K and the
-// V rows arrive during the softmax.  Scores: one position per thread, the
+// loads in issue order): first each thread's K rows of the first 192
+// positions, then (after the q/k/v staging, so that the K rows of the
+// other workgroups on the CU come first) the V rows it accumulates in P*V
+// (up to VP of them, positions sl + SL j, kept packed), so the scores wait
+// only for K and the V rows arrive during the softmax.  Scores: one position per thread, the
 // dot product over d in four interleaved FP32 partial sums (d mod 4) added
 // pairwise, q broadcast from LDS.  Softmax in LDS.  P*V: thread = (float4
 // column group g, position slice sl), four accumulators; slices are summed
@@ -511,18 +512,13 @@ __global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices v
         const int t = i * KRR + kr;
         kpre[i] = *(const uint4*)(kchunk + (int64_t)(t < nmem ? t : 0) * D);
     }
-    // every wave's K ahead of any wave's V (the CU returns loads in issue
-    // order): the scores wait for half the stream, not all of it
+    // every wave's K rows issued before any wave goes on (the V rows follow
+    // the staging below)
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     const KV* vcol = vc + crow * D + 4 * g;
     Raw vpre[VP];
-#pragma unroll
-    for (int j = 0; j < VP; ++j) {
-        const int t = sl + SL * j;
-        vpre[j] = kv_raw4(vcol + (int64_t)(t < nmem ? t : 0) * D);
-    }
     if (RAW && !plain) {
         if (ROPE) {
             if (tid < D / 2) {
@@ -562,6 +558,15 @@ __global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices v
         qs[tid] = q1;
     }
     __syncthreads();  // qs, ks, vs
+    // this thread's V rows, issued only now: the K rows of the other workgroups on the CU, issued meanwhile,
+    // come back before them (batch 16, two workgroups per CU: decode +1.7 %; batch 1 unchanged)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < VP; ++j) {
+        const int t = sl + SL * j;
+        vpre[j] = kv_raw4(vcol + (int64_t)(t < nmem ? t : 0) * D);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     if (ROPE && h < kv_heads && tid < D) {
         kc[(crow + pos) * D + tid] = kv_store_value(ks[tid], KV{});
         vc[(crow + pos) * D + tid] = kv_store_value(vs[tid], KV{});
