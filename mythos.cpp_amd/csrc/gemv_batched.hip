@@ -733,13 +733,21 @@ __global__ __launch_bounds__(WV * 64) void oil4_gemv_bp(const uint8_t* nib, cons
         h3_exchange(sl.wx, sl.wy, lane, xa, yb);
         const uint8_t* bbuf = lds + ph * L::bphase;
         floatx4 acc_h = {0.0f, 0.0f, 0.0f, 0.0f}, acc_l = {0.0f, 0.0f, 0.0f, 0.0f};
+        // the unit's 16 B fragments read before its lookups (the compiler otherwise reads each pair just
+        // before its MFMAs and waits for the LDS round trip eight times per unit; 22016 x 4096 at 16
+        // tokens 27.7 -> 26.9 us)
+        half8 bh[8], bl[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            bh[m] = *(const half8*)(bbuf + bt_slot(m, q, j));
+            bl[m] = *(const half8*)(bbuf + L::frag + bt_slot(m, q, j));
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const half8 a = lookup8(m < 4 ? u4get(xa, m) : u4get(yb, m - 4), pl);
-            const half8 bh = *(const half8*)(bbuf + bt_slot(m, q, j));
-            const half8 bl = *(const half8*)(bbuf + L::frag + bt_slot(m, q, j));
-            acc_h = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_h, 0, 0, 0);
-            acc_l = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_l, 0, 0, 0);
+            acc_h = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh[m], acc_h, 0, 0, 0);
+            acc_l = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl[m], acc_l, 0, 0, 0);
         }
         const int shn = shifts[ph * kBtTok + j];
 #pragma unroll
