@@ -421,8 +421,8 @@ __device__ __forceinline__ uint2 kv_raw4(const uint16_t* p) { return *(const uin
 // > 1: the prompt rows of a prefill chunk, each attending causally).
 // ns (ROPE, NormScale in common.h): q/k/v are projections of x * gamma and
 // get the RMSNorm's 1 / rms here.
-// NT: threads per workgroup (256, or 1024 for a decode step of few heads:
-// the same work in 16 waves, each phase a quarter as long).
+// NT: threads per workgroup (256, or 512 for a decode step of few heads:
+// the same work in 8 waves, each phase half as long).
 template <int D, bool ROPE, typename KV, int NT = kT>
 __global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices vin, NormScale ns,
                                                   const float* __restrict__ cos_t, const float* __restrict__ sin_t,
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices v
     double npart[kNormBatch];
     if (ROPE && ns.ssp) norm_issue(ns, row, tid, NT, npart);
     const bool plain = q.n == 1 && !q.tscale && (!ROPE || (kin.n == 1 && vin.n == 1 && !kin.tscale && !vin.tscale));
-    // (16 waves: split-K q/k/v summed on the spot, the registers are short)
+    // (more than 4 waves: split-K q/k/v summed on the spot, the registers are short)
     constexpr bool RAW = NT <= kT;
     float raw[RAW ? (ROPE ? 6 : 1) : 1][kMaxSlices];
     float q1 = 0.0f, q2 = 0.0f, k1 = 0.0f, k2 = 0.0f, v1 = 0.0f, v2 = 0.0f, c = 0.0f, sn = 0.0f;
@@ -1180,25 +1180,26 @@ static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& 
     const float scale = 1.0f / sqrtf((float)head_dim);
     const size_t lds = (size_t)max_seq * sizeof(float);
     const dim3 grid((unsigned)heads, (unsigned)rows);
-    // few workgroups (a decode step of a handful of sequences): 16 waves each
+    // few workgroups (a decode step of a handful of sequences): 8 waves each (16 measured 0.9 % slower for a
+    // batch-1 decode step once the V rows were issued after the staging, 4 waves 1.3 % slower)
     const bool wide = ROPE && np == 1 && rows * heads <= 128;
     if (head_dim == 64) {
         if (wide)
-            attention_k<64, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+            attention_k<64, ROPE, KV, 512><<<grid, 512, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
                                                                     ctx0, np, heads, kv_heads, max_seq, scale);
         else
             attention_k<64, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0, np,
                                                             heads, kv_heads, max_seq, scale);
     } else if (head_dim == 128) {
         if (wide)
-            attention_k<128, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+            attention_k<128, ROPE, KV, 512><<<grid, 512, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
                                                                      ctx0, np, heads, kv_heads, max_seq, scale);
         else
             attention_k<128, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0,
                                                              np, heads, kv_heads, max_seq, scale);
     } else {
         if (wide)
-            attention_k<256, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+            attention_k<256, ROPE, KV, 512><<<grid, 512, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
                                                                      ctx0, np, heads, kv_heads, max_seq, scale);
         else
             attention_k<256, ROPE, KV><<<grid, kT, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step, ctx0,
