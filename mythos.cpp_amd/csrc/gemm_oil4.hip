@@ -578,9 +578,11 @@ __global__ __launch_bounds__(ws_threads(CW)) void oil4_prefill_ws(const uint16_t
             if (row < Mr) {
                 const int sh = rsh[row];
                 const float4 hi = *(const float4*)(st + r * BN + 4 * q), lo = *(const float4*)(st + (r + 128) * BN + 4 * q);
+                // oil4_hi_lo: an infinite hi sum (an infinite codebook entry) is the result, as the reference's
+                // single product w * x_k gives, not hi + lo, which is NaN where the lo part has the other sign
                 *(float4*)(C + (int64_t)row * N + n0 + 4 * q) =
-                    make_float4(ldexpf(hi.x + lo.x, -sh), ldexpf(hi.y + lo.y, -sh), ldexpf(hi.z + lo.z, -sh),
-                                ldexpf(hi.w + lo.w, -sh));
+                    make_float4(ldexpf(oil4_hi_lo(hi.x, lo.x), -sh), ldexpf(oil4_hi_lo(hi.y, lo.y), -sh),
+                                ldexpf(oil4_hi_lo(hi.z, lo.z), -sh), ldexpf(oil4_hi_lo(hi.w, lo.w), -sh));
             }
         }
     } else {

@@ -10,6 +10,7 @@ chosen by shape (the launcher's dispatch rules):
   valu     batch 1, cb_block 64               (oil4_gemv_valu, FP32 FMA)
   generic  K = 1000, cb_block 100             (oil4_generic)
   bt       batch 4, cb_block 128              (oil4_gemv_bt, split-K MFMA)
+  x32      batch 130, cb_block 128            (oil4_prefill_a16x + oil4_prefill_ws<X32>, the GEMM route)
   prefill  bf16 A: oil4_prefill_ws (N % 96 == 0), oil4_prefill_mfma, oil4_gemm_prefill_k
 
 A flush of subnormals to zero would turn the all-subnormal case's outputs into
@@ -35,6 +36,7 @@ GEMV_PATHS = [  # name, M, K, batch, cb_block
     ("valu", 96, 1024, 1, 64),
     ("generic", 40, 1000, 1, 100),
     ("bt", 200, 2048, 4, 128),
+    ("x32", 256, 1024, 130, 128),  # >= 128 tokens: the FP32-row MFMA GEMM (rows split into FP16 hi / lo)
 ]
 # producer/consumer FP16-A kernel (N a multiple of 96), the LDS-staged kernel
 # (N fits no tile of the former), the first kernel (codebook block 32)
@@ -198,7 +200,7 @@ def test_oil4_gemv_x_wide_range(path, M, K, batch, block, oracle, mth, dev):
 # paths whose products come from an FP16 hi/lo split of x without an FP32
 # fallback (batch >= 2, codebook blocks of 256): an infinite codebook entry
 # times an x_k whose hi part underflows to 0 gives NaN, the reference +-Inf
-HILO_NO_FALLBACK = {"mfma", "bt"}
+HILO_NO_FALLBACK = {"mfma", "bt", "x32"}
 
 
 @pytest.mark.parametrize("path,M,K,batch,block", GEMV_PATHS)
