@@ -274,3 +274,36 @@ def test_oil4_prefill_row_magnitudes(path, M, N, K, block, oracle, mth, dev):
     bound = 2.0 ** -8 * np.abs(ref) + 1e-5 * absw
     assert (d <= bound).all(), f"{path}: {(d > bound).sum()} elements out of bound, rows {np.unique(np.nonzero(d > bound)[0])[:8]}"
     assert (got[M // 2] == 0).all() and (got[0] != 0).all() and (got[-1] != 0).all()
+
+
+@pytest.mark.parametrize("where", ["x_inf", "x_nan"])
+@pytest.mark.parametrize("path,M,K,batch,block", GEMV_PATHS)
+def test_oil4_gemv_nonfinite_x(path, M, K, batch, block, where, oracle, mth, dev):
+    """Activations holding +-Inf or NaN (src/kernel_oil4.cpp:50 multiplies
+    them in FP32): every output of such a token must be in the oracle's class
+    (NaN, +Inf, -Inf), the other tokens' outputs within the FP32 bar."""
+    import torch
+    print(f"oil4 non-finite x {where} path={path} M={M} K={K} batch={batch}", flush=True)
+    g = np.random.default_rng(zlib.crc32(f"{path}/{where}".encode()))
+    packed = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    cbs = codebooks("edges", M, K // block, 17)
+    x = g.normal(0, 1, (batch, K)).astype(np.float32)
+    if where == "x_inf":
+        x[0, 7] = np.inf
+        x[-1, K // 2 + 3] = -np.inf
+    else:
+        x[0, 33] = np.nan
+    y = empty(batch * M, torch.float32, dev)
+    mth.oil4_gemv(to_dev(packed, dev), to_dev(cbs, dev), block, to_dev(x, dev), y, M, K, batch)
+    torch.cuda.synchronize()
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = oracle.oil4_gemv_blocked(packed.ravel(), cbs, x, M, K, batch, block, threads=8)
+        W = synth.dequant_oil4(packed, cbs, M, K, block).astype(np.float64)
+        absw = (np.abs(W) @ np.abs(x.astype(np.float64)).T).T
+    got = y.cpu().numpy().reshape(batch, M)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), f"{path}/{where}: NaN classes differ"
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)), f"{path}/{where}: +Inf classes differ"
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref)), f"{path}/{where}: -Inf classes differ"
+    fin = np.isfinite(ref)
+    if fin.any():
+        fp32_close(got[fin], ref[fin], absw[fin], 1e-5, f"{path}/{where} finite outputs")
