@@ -18,8 +18,7 @@
  * ceil(M/16)*16*K*2 bytes, for K % 256 == 0, codebook blocks of a multiple
  * of 128 and N a multiple of 64, 96 or 112), mth_tl2_gemm (each activation
  * row quantised once: N * ceil(K/4) * 4 bytes plus 4 bytes per row, when
- * ceil(K/4) % 16 == 0) and mth_i2s_gemm_vnni (permuted activations,
- * for its MFMA shapes) keep intermediate data in a device workspace
+ * ceil(K/4) % 16 == 0) keep intermediate data in a device workspace
  * the library owns, one per (device, stream).  The first call that needs more
  * than the stream's workspace holds allocates a larger one (hipMalloc, at
  * least double the old size) and retires the old block WITHOUT freeing it, so
@@ -185,8 +184,7 @@ int mth_i2s_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int6
 /* oil::kernel::i2s_gemm_vnni (include/oil/kernel.h:63-65, body at
  * src/kernel_i2s.cpp:201-235): int8 activations, exact integer dot as FP32.
  * M >= 64, N >= 64, K % 256 == 0 with 16-byte aligned w / act run on int8
- * MFMA (bit-exact) and use N*K + 4*N bytes of workspace; other shapes run one
- * wave per output. */
+ * MFMA (bit-exact, no workspace); other shapes run one wave per output. */
 int mth_i2s_gemm_vnni(const uint8_t* w, const int8_t* act, float* out, int64_t M, int64_t N, int64_t K,
                       mth_stream_t stream);
 

@@ -364,14 +364,7 @@ int mth_i2s_gemm_vnni(const uint8_t* w, const int8_t* act, float* out, int64_t M
                       mth_stream_t stream) {
     REQUIRE(w && act && out, "mth_i2s_gemm_vnni: null pointer");
     REQUIRE(M > 0 && N > 0 && K > 0 && M * N < kMaxDim && K < (1ll << 24), "mth_i2s_gemm_vnni: bad sizes");
-    const bool aligned = (((uintptr_t)w | (uintptr_t)act) & 15u) == 0;
-    const size_t need = aligned ? mth::i2s_gemm_workspace_bytes(M, N, K) : 0;
-    void* ws = nullptr;
-    if (need) {
-        const hipError_t e = workspace(S(stream), need, &ws);
-        if (e != hipSuccess) return workspace_fail("mth_i2s_gemm_vnni", e, need);
-    }
-    return check_launch(mth::launch_i2s_gemm_vnni(w, act, out, M, N, K, ws, S(stream)), "mth_i2s_gemm_vnni");
+    return check_launch(mth::launch_i2s_gemm_vnni(w, act, out, M, N, K, S(stream)), "mth_i2s_gemm_vnni");
 }
 
 int mth_tl1_gemm(const uint8_t* w, const float* act, float* out, int64_t M, int64_t N, int64_t K,

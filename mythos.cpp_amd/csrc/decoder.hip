@@ -193,10 +193,9 @@ hipError_t enqueue_prefill(const mth_decoder* d, hipStream_t s) {
                 TRY(mth::launch_silu_mul_quant(d->pf_gu, d->pf_gu + R * F, d->pf_aq, d->pf_inv, nullptr, R, F, F, F,
                                                s));
             }
-            if (R >= kPfGemmRows && mth::i2s_gemm_workspace_bytes(H, R, F) != 0 &&
+            if (R >= kPfGemmRows && mth::i2s_gemm_mfma_ok(H, R, F) &&
                 ((((uintptr_t)L.wdown | (uintptr_t)d->pf_aq) & 15u) == 0))  // int8 MFMA GEMM, bit-exact
-                TRY(mth::launch_i2s_gemm_rows(L.wdown, L.down_scale, d->pf_aq, d->pf_inv, d->pf_t, H, R, F, d->pf_ws,
-                                              s));
+                TRY(mth::launch_i2s_gemm_rows(L.wdown, L.down_scale, d->pf_aq, d->pf_inv, d->pf_t, H, R, F, s));
             else if ((((uintptr_t)L.wdown | (uintptr_t)d->pf_aq) & 15u) == 0 && mth::i2s_bt_supported(H, F, R))
                 TRY(mth::launch_i2s_gemv_bt(L.wdown, L.down_scale, d->pf_aq, d->pf_inv, d->pf_t, H, F, R,
                                             d->bt_partial, s));
@@ -546,8 +545,7 @@ int mth_decoder_create(const mth_decoder_config* cfg, mth_decoder** out) {
         {(void**)&d->amx, (size_t)(B * kAmxParts) * 4},
         {(void**)&d->pf_ws, PR >= kPfGemmRows ? std::max({mth::oil4_gemm_x32_workspace_bytes(PR, H),
                                                           mth::oil8_gemm_x32_workspace_bytes(PR, H),
-                                                          mth::oil8_gemm_x32_workspace_bytes(PR, QD),
-                                                          mth::i2s_gemm_workspace_bytes(H, PR, F)})
+                                                          mth::oil8_gemm_x32_workspace_bytes(PR, QD)})
                                               : (size_t)0},
     };
     size_t total = 0;

@@ -141,17 +141,18 @@ hipError_t launch_i2s_act(const float* act, const float* amax, const uint8_t* pa
                           int64_t M, int64_t K, const ResidOut& ro, int* nparts, hipStream_t s);
 hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
-// ws: null (one wave per output) or i2s_gemm_workspace_bytes(M, N, K) bytes of
-// device scratch for the int8-MFMA kernel (0 = shape not covered by it).
-size_t i2s_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+// Shapes the int8-MFMA kernel covers (M, N >= 64, K % 256 == 0, 32-bit
+// offsets); launch_i2s_gemm_vnni takes it for them when w and a are 16-byte
+// aligned, else one wave per output.
+bool i2s_gemm_mfma_ok(int64_t M, int64_t N, int64_t K);
 hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o,
-                                int64_t M, int64_t N, int64_t K, void* ws, hipStream_t s);
+                                int64_t M, int64_t N, int64_t K, hipStream_t s);
 // The prompt prefill's down projection on int8 MFMA: y [N][M] = the I2_S
 // GEMV of every token row n of the int8 activations a [N][K] with act scale
-// inv[n] (bit-identical to launch_i2s_gemv per row); ws:
-// i2s_gemm_workspace_bytes(M, N, K) bytes (nonzero: M, N >= 64, K % 256 == 0).
+// inv[n] (bit-identical to launch_i2s_gemv per row); i2s_gemm_mfma_ok(M, N, K)
+// and 16-byte aligned w, a (else hipErrorInvalidValue).
 hipError_t launch_i2s_gemm_rows(const uint8_t* w, float w_scale, const int8_t* a, const float* inv, float* y, int64_t M,
-                                int64_t N, int64_t K, void* ws, hipStream_t s);
+                                int64_t N, int64_t K, hipStream_t s);
 hipError_t launch_tl1_gemm(const uint8_t* w, const float* a, float* o,
                            int64_t M, int64_t N, int64_t K, hipStream_t s);
 hipError_t launch_tl2_gemm(const uint8_t* w, const float* a, float* o,

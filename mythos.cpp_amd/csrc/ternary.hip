@@ -1161,151 +1161,175 @@ inline int ib_slices(int64_t M, int64_t K) {
 // order is permuted alike on both operands: in a 16-column group whose codes
 // are the dword q (column 4b + f in field f of byte b), plane f of the u-codes,
 // (ucode(q) >> 2f) & 0x03030303, holds column 4b + f at byte b -- two VALU
-// per four weights.  The activations are permuted to the same order once per
-// call (i2s_act_perm: a 4x4 byte transpose of every 16-byte group), which also
-// writes each token's sum over k.
-//   * workgroup tile 64 weight rows x 128 tokens, K steps of 256, one per CU
-//     at config size (4096 x 512); XCD-aware: the workgroups of a token tile
-//     share two XCDs, whose L2 then holds those tokens' activations;
-//   * weights: 4 KB of codes per step, staged 3 steps ahead in registers,
-//     decoded once per workgroup into a double-buffered LDS tile (XOR-swizzled
-//     16-byte slots, conflict-free fragment reads);
-//   * activations: every wave reads the B fragments of its 32 tokens straight
-//     from L2 into registers, one step ahead;
-//   * wave w: all 64 rows x tokens 32w..32w+31 (4 x 2 accumulator tiles).
-constexpr int TGM = 64, TGN = 128, TGK = 256;
+// per four weights -- and the activations' 16-byte group is put in the same
+// order by a 4x4 byte transpose (8 v_perm) on its way into LDS; the token
+// sums over k come from the same loads (v_dot4 with ones).
+//   * workgroup tile 128 weight rows x 64 tokens, K steps of 256, one per CU
+//     at config size (4096 x 512): per step 8 KB of codes and 16 KB of
+//     activations enter the CU (a 64 x 128 tile needs 4 + 32 KB; the step
+//     time follows the bytes the CU has in flight, not a unit's rate);
+//   * tile order: the tn token tiles of one weight-row tile on consecutive
+//     workgroups, i.e. spread over the XCDs (at tn = 8 each XCD's L2 holds one
+//     token tile for all of its workgroups; blocking the XCDs' tiles so each
+//     L2 serves a quarter of the codes measured slower);
+//   * weights: wave w decodes its own 32 rows straight into A fragments in
+//     registers (no LDS): lane (r, g) loads 16 code bytes of row r, whose four
+//     dwords are its fragments of the step's four chunks (the chunks' k order
+//     is taken alike on the B side); codes 2 steps ahead;
+//   * activations: each wave loads 16 tokens, 2 steps ahead in registers, into
+//     a double-buffered LDS tile (XOR-swizzled 16-byte slots, conflict-free);
+//   * wave w: rows 32w..32w+31 x all 64 tokens (2 x 4 accumulator tiles).
+constexpr int TGM = 128, TGN = 64, TGK = 256;
 
-// 16-byte groups of a [N][K] int8 -> permuted order; sums[n] = sum_k a[n][k].
-// One workgroup per token.
-__global__ __launch_bounds__(kWG) void i2s_act_perm(const int8_t* __restrict__ a, int8_t* __restrict__ ap,
-                                                    int* __restrict__ sums, int K) {
-    __shared__ int red[kWaves];
-    const int64_t row = blockIdx.x;
-    const int8_t* src = a + row * K;
-    int8_t* dst = ap + row * K;
-    int sum = 0;
-    for (int g = threadIdx.x; g < K / 16; g += kWG) {
-        const uint4 v = ld16(src + 16 * g);
-        uint4 o;
-        o.x = byte_t4x4(v.x, v.y, v.z, v.w, 0);
-        o.y = byte_t4x4(v.x, v.y, v.z, v.w, 1);
-        o.z = byte_t4x4(v.x, v.y, v.z, v.w, 2);
-        o.w = byte_t4x4(v.x, v.y, v.z, v.w, 3);
-        *(uint4*)(dst + 16 * g) = o;
-        sum = dot4(v.x, 0x01010101u, dot4(v.y, 0x01010101u, dot4(v.z, 0x01010101u, dot4(v.w, 0x01010101u, sum))));
-    }
-    sum = group_sum_i<64>(sum);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
-    __syncthreads();
-    if (threadIdx.x == 0) sums[row] = ((red[0] + red[1]) + red[2]) + red[3];
+// LDS byte offset of 16-byte slot q (0..15) of token row n in a step tile
+__device__ __forceinline__ int tg_off(int n, int q) { return n * TGK + 16 * (q ^ (n & 7)); }
+
+// 4x4 byte transpose of a 16-byte group: byte i of dword s of the result is
+// byte s of dword i of v (column 4i + s of the group -> byte position 4s + i)
+__device__ __forceinline__ uint4 group_t4x4(const uint4& v) {
+    const uint32_t lo_xy = __builtin_amdgcn_perm(v.y, v.x, 0x05010400u), hi_xy = __builtin_amdgcn_perm(v.y, v.x, 0x07030602u);
+    const uint32_t lo_zw = __builtin_amdgcn_perm(v.w, v.z, 0x05010400u), hi_zw = __builtin_amdgcn_perm(v.w, v.z, 0x07030602u);
+    return make_uint4(__builtin_amdgcn_perm(lo_zw, lo_xy, 0x05040100u), __builtin_amdgcn_perm(lo_zw, lo_xy, 0x07060302u),
+                      __builtin_amdgcn_perm(hi_zw, hi_xy, 0x05040100u), __builtin_amdgcn_perm(hi_zw, hi_xy, 0x07060302u));
 }
-
-// LDS byte offset of 16-byte slot q (0..15) of weight row r in a step tile
-__device__ __forceinline__ int tg_off(int r, int q) { return r * TGK + 16 * (q ^ (r & 7)); }
 
 // ROWS: the decoder prefill's down projection -- out is y [N][M] with
 // y[n][m] = ((float)sum * w_scale) * inv[n], each product rounded on its
 // own: the reference's i2s_gemv epilogue (src/kernel_i2s.cpp:32-40) for
 // every token row, bit for bit (the sums are exact integers below 2^24).
 template <bool ROWS = false>
-__global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int8_t* ap, const int* __restrict__ sums,
-                                                     float* __restrict__ out, int M, int N, int K,
-                                                     float w_scale = 0.0f, const float* __restrict__ inv = nullptr) {
-    __shared__ __align__(16) uint8_t wt[2][TGM * TGK];
+__global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int8_t* a, float* __restrict__ out, int M,
+                                                     int N, int K, float w_scale = 0.0f,
+                                                     const float* __restrict__ inv = nullptr) {
+    __shared__ __align__(16) uint8_t bt[2][TGN * TGK];
+    __shared__ int asum[TGN];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tm = (M + TGM - 1) / TGM, tn = (N + TGN - 1) / TGN;
-    int mt, nt;
-    {
-        const int id = blockIdx.x, total = tm * tn;
-        if (total % 8 == 0 && 8 % tn == 0) {  // 8 / tn XCDs per token tile
-            const int grp = 8 / tn, xcd = id % 8;
-            nt = xcd / grp;
-            mt = (id / 8) * grp + xcd % grp;
-        } else {
-            mt = id / tn;
-            nt = id % tn;
-        }
-    }
-    const int m0 = mt * TGM, n0 = nt * TGN;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tn = (N + TGN - 1) / TGN;
+    const int m0 = (blockIdx.x / tn) * TGM, n0 = (blockIdx.x % tn) * TGN;
     const int bpr = K / 4, steps = K / TGK;
 
-    // ---- weight codes: thread -> row tid/4, code bytes 16 (tid%4) .. +15 of the step
-    const int wr = tid >> 2, wc = tid & 3;
-    const uint8_t* wsrc = w + (int64_t)min(m0 + wr, M - 1) * bpr + 16 * wc;
-    uint4 wv[4];
-    auto decode = [&](const uint4& v, uint8_t* tile) {
-        const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+    // ---- codes: lane (r16, g), row tile i: row m0 + 32 wave + 16 i + r16, code bytes 16 g .. 16 g + 15 of the
+    // step, i.e. code dwords 4g + c (c = 0..3), each 16 columns; the planes of dword 4g + c are the lane's A
+    // fragment of chunk c, so chunk c's B fragment of lane (n, g) is the 16-column group 4g + c of token n
+    // (addresses: a uniform base per step plus a loop-invariant 32-bit lane offset, so that no load's
+    // destination registers share a dying address pair)
+    uint32_t woff[2];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {  // code dword g: columns 64 wc + 16 g .. +15
-            const uint32_t u = ucode(q[g]);
-            *(uint4*)(tile + tg_off(wr, 4 * wc + g)) =
-                make_uint4(u & 0x03030303u, (u >> 2) & 0x03030303u, (u >> 4) & 0x03030303u, (u >> 6) & 0x03030303u);
+    for (int i = 0; i < 2; ++i) woff[i] = (uint32_t)min(m0 + 32 * wave + 16 * i + r16, M - 1) * (uint32_t)bpr + 16 * g;
+    constexpr int LEAD = 2;  // steps between a load's issue and its use (codes) / its LDS store (activations)
+    uint4 cw[LEAD + 1][2];
+    // ---- activations: wave w loads token n0 + 16 w + r16, bytes 64 c + 16 g (group 4c + g) of the step
+    const uint32_t boff = (uint32_t)min(n0 + 16 * wave + r16, N - 1) * (uint32_t)K + 16 * g;
+    uint4 bw[LEAD + 1][4];
+    int tsum = 0;  // sum of the bytes this lane loads of its token
+
+    auto load_codes = [&](int step, uint4 (&dst)[2]) {
+        const uint8_t* base = w + (int64_t)min(step, steps - 1) * (TGK / 4);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dst[i] = ld16(base + woff[i]);
+    };
+    auto load_acts = [&](int step, uint4 (&dst)[4]) {
+        const int8_t* base = a + (int64_t)min(step, steps - 1) * TGK;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dst[c] = ld16(base + boff + 64 * c);
+    };
+    // B(step) into LDS in the codes' k order, its bytes into tsum (steps past the end add nothing)
+    auto store_acts = [&](const uint4 (&src)[4], uint8_t* tile, bool real) {
+        const uint32_t ones = real ? 0x01010101u : 0u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            *(uint4*)(tile + tg_off(16 * wave + r16, 4 * c + g)) = group_t4x4(src[c]);
+            tsum = dot4(src[c].x, ones, dot4(src[c].y, ones, dot4(src[c].z, ones, dot4(src[c].w, ones, tsum))));
         }
     };
-    // ---- activations: lane (n = lane%16, g = lane/16), tokens n0 + 32 wave + 16 j + n
-    const int8_t* bsrc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) bsrc[j] = ap + (int64_t)min(n0 + 32 * wave + 16 * j + (lane & 15), N - 1) * K + 16 * (lane >> 4);
-    i32x4 bv[2][2][4];  // [buffer][j][k chunk c]
-    auto load_b = [&](int step, int b) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) bv[b][j][c] = *(const i32x4*)(bsrc[j] + step * TGK + 64 * c);
-    };
 
-    i32x4 acc[4][2];
+    i32x4 acc[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+        for (int j = 0; j < 4; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
+    // prologue: the loads of steps 0 .. LEAD - 1 in the loop's order (B(t) then codes(t) per step t, so that
+    // the loop head sees the same loads in flight from both of its predecessors); B(0) into LDS
 #pragma unroll
-    for (int u = 0; u < 4; ++u) wv[u] = ld_stream(wsrc + (int64_t)min(u, steps - 1) * (TGK / 4));
-    load_b(0, 0);
-    decode(wv[0], wt[0]);
+    for (int k = 0; k < LEAD; ++k) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_acts(k, bw[k]);
+        load_codes(k, cw[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store_acts(bw[0], bt[0], true);
     __syncthreads();
-    for (int s0 = 0; s0 < steps; s0 += 4) {
+
+    constexpr int U = LEAD + 1;  // unroll: every register slot index a constant
+    // the step count rounded up to whole unrolled rounds (no exit inside a round: an exit per step made the
+    // compiler rotate the accumulators' registers at the loop head, waiting there for every load in flight);
+    // the steps past the end take all-zero A fragments (the plane mask pm)
+    const int steps_u = (steps + U - 1) / U * U;
+    for (int s0 = 0; s0 < steps_u; s0 += U) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int step = s0 + u;
-            if (step >= steps) break;
-            // the loads at the top of the step (the compiler otherwise sinks them below the step's MFMAs, and
-            // B(step + 1) then has less than a step to come back behind the weight stream; 66.7 -> 64.7 us at
-            // 4096 x 512 x 11008)
+            const uint32_t pm = step < steps ? 0x03030303u : 0u;
+            // loads at the top of the step: B(step + LEAD) and codes(step + LEAD) into the slots that B(step - 1)
+            // and codes(step - 1) left
             __builtin_amdgcn_sched_barrier(0);
-            load_b(min(step + 1, steps - 1), (u + 1) & 1);
+            load_acts(step + LEAD, bw[(u + LEAD) % U]);
+            load_codes(step + LEAD, cw[(u + LEAD) % U]);
             __builtin_amdgcn_sched_barrier(0);
-            decode(wv[(u + 1) & 3], wt[(u + 1) & 1]);                                  // W(step + 1)
-            wv[u & 3] = ld_stream(wsrc + (int64_t)min(step + 4, steps - 1) * (TGK / 4));  // slot of W(step)
-            __builtin_amdgcn_sched_barrier(0);
-            const uint8_t* cur = wt[u & 1];
+            // A fragments of this step
+            i32x4 af[2][4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint4 q = cw[u][i];
+                const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t uc = ucode(d[c]);
+                    af[i][c] = i32x4{(int)(uc & pm), (int)((uc >> 2) & pm), (int)((uc >> 4) & pm), (int)((uc >> 6) & pm)};
+                }
+            }
+            // B(step + 1) into the other LDS tile (read by the previous step, before its barrier); the tiles
+            // alternate by step parity (U is odd)
+            store_acts(bw[(u + 1) % U], bt[(step + 1) & 1], step + 1 < steps);
+            const uint8_t* cur = bt[step & 1];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                i32x4 af[4];
+                i32x4 bf[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    af[i] = *(const i32x4*)(cur + tg_off(16 * i + (lane & 15), 4 * c + (lane >> 4)));
+                for (int j = 0; j < 4; ++j) bf[j] = *(const i32x4*)(cur + tg_off(16 * j + r16, 4 * g + c));
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bv[u & 1][j][c], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i][c], bf[j], acc[i][j], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
         }
     }
-    // D: lane l holds rows 16 i + 4 (l/16) + r, token 16 j + l%16 (of the wave's 32)
+    // token sums: the four lane groups l, l ^ 16, l ^ 32, l ^ 48 of token 16 wave + r16, then through LDS
+    {
+        uint32_t t = (uint32_t)tsum;
+        const auto r32 = __builtin_amdgcn_permlane32_swap(t, t, false, false);
+        t = lane_pin(r32[0]) + lane_pin(r32[1]);
+        const auto r16s = __builtin_amdgcn_permlane16_swap(t, t, false, false);
+        t = lane_pin(r16s[0]) + lane_pin(r16s[1]);
+        if (g == 0) asum[16 * wave + r16] = (int)t;
+    }
+    __syncthreads();
+    // D: lane l holds rows 32 wave + 16 i + 4 (l/16) + r, token 16 j + l%16
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + 32 * wave + 16 * j + (lane & 15);
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 16 * j + r16;
         if (n >= N) continue;
-        const int as = sums[n];
+        const int as = asum[16 * j + r16];
         if constexpr (ROWS) {
             const float ts = inv[n];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + 16 * i + 4 * (lane >> 4);
+            for (int i = 0; i < 2; ++i) {
+                const int m = m0 + 32 * wave + 16 * i + 4 * g;
                 float v[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = fmul_rn(fmul_rn((float)(acc[i][j][r] - as), w_scale), ts);
@@ -1320,10 +1344,10 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int m = m0 + 16 * i + 4 * (lane >> 4) + r;
+                    const int m = m0 + 32 * wave + 16 * i + 4 * g + r;
                     if (m < M) out[(int64_t)m * N + n] = (float)(acc[i][j][r] - as);
                 }
         }
@@ -1525,20 +1549,17 @@ hipError_t launch_i2s_gemm(const uint8_t* w, const float* a, float* o, int64_t M
     return hipGetLastError();
 }
 
-size_t i2s_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-    const bool mfma = M >= 64 && N >= 64 && K % TGK == 0 && K < (1ll << 24) && M < (1ll << 31) && N < (1ll << 31) &&
-                      ((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN) < (1ll << 31);
-    return mfma ? (size_t)(((N * K + 255) / 256) * 256 + N * 4) : 0;
+bool i2s_gemm_mfma_ok(int64_t M, int64_t N, int64_t K) {
+    // (the kernel's lane offsets into the codes and the activations are 32-bit)
+    return M >= 64 && N >= 64 && K % TGK == 0 && K < (1ll << 24) && M * (K / 4) < (1ll << 32) &&
+           N * K < (1ll << 32) && ((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN) < (1ll << 31);
 }
 
 hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o, int64_t M, int64_t N, int64_t K,
-                                void* ws, hipStream_t s) {
-    if (ws) {  // i2s_gemm_workspace_bytes(M, N, K) bytes: permuted activations, then token sums
-        int8_t* ap = (int8_t*)ws;
-        int* sums = (int*)((char*)ws + ((N * K + 255) / 256) * 256);
-        i2s_act_perm<<<(unsigned)N, kWG, 0, s>>>(a, ap, sums, (int)K);
+                                hipStream_t s) {
+    if (i2s_gemm_mfma_ok(M, N, K) && (((uintptr_t)w | (uintptr_t)a) & 15u) == 0) {
         const unsigned grid = (unsigned)(((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN));
-        i2s_gemm_mfma<<<grid, kWG, 0, s>>>(w, ap, sums, o, (int)M, (int)N, (int)K);
+        i2s_gemm_mfma<<<grid, kWG, 0, s>>>(w, a, o, (int)M, (int)N, (int)K);
         return hipGetLastError();
     }
     i2s_gemm_vnni_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);
@@ -1546,13 +1567,10 @@ hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o, int
 }
 
 hipError_t launch_i2s_gemm_rows(const uint8_t* w, float w_scale, const int8_t* a, const float* inv, float* y, int64_t M,
-                                int64_t N, int64_t K, void* ws, hipStream_t s) {
-    if (!ws || i2s_gemm_workspace_bytes(M, N, K) == 0) return hipErrorInvalidValue;
-    int8_t* ap = (int8_t*)ws;
-    int* sums = (int*)((char*)ws + ((N * K + 255) / 256) * 256);
-    i2s_act_perm<<<(unsigned)N, kWG, 0, s>>>(a, ap, sums, (int)K);
+                                int64_t N, int64_t K, hipStream_t s) {
+    if (!i2s_gemm_mfma_ok(M, N, K) || (((uintptr_t)w | (uintptr_t)a) & 15u) != 0) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN));
-    i2s_gemm_mfma<true><<<grid, kWG, 0, s>>>(w, ap, sums, y, (int)M, (int)N, (int)K, w_scale, inv);
+    i2s_gemm_mfma<true><<<grid, kWG, 0, s>>>(w, a, y, (int)M, (int)N, (int)K, w_scale, inv);
     return hipGetLastError();
 }
 

@@ -26,7 +26,7 @@ def run(mth, dev, w, a, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 128, 1024), (100, 70, 512), (64, 64, 256), (192, 300, 768),
-                                   (130, 129, 2048)])
+                                   (130, 129, 2048), (512, 200, 1280), (1000, 130, 2816)])
 def test_i2s_gemm_mfma_vs_oracle(M, N, K, oracle, mth, dev):
     print(f"i2s_gemm_vnni mfma M={M} N={N} K={K}", flush=True)
     g = np.random.default_rng(M * 7 + N * 3 + K)
