@@ -1294,6 +1294,7 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
             // alternate by step parity (U is odd)
             store_acts(bw[(u + 1) % U], bt[(step + 1) & 1], step + 1 < steps);
             const uint8_t* cur = bt[step & 1];
+            if (step < steps)  // (a padded step's products are zero: skip them)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 i32x4 bf[4];
