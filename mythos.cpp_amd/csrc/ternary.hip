@@ -1172,13 +1172,15 @@ inline int ib_slices(int64_t M, int64_t K) {
 //     workgroups, i.e. spread over the XCDs (at tn = 8 each XCD's L2 holds one
 //     token tile for all of its workgroups; blocking the XCDs' tiles so each
 //     L2 serves a quarter of the codes measured slower);
-//   * weights: wave w decodes its own 32 rows straight into A fragments in
-//     registers (no LDS): lane (r, g) loads 16 code bytes of row r, whose four
-//     dwords are its fragments of the step's four chunks (the chunks' k order
-//     is taken alike on the B side); codes 2 steps ahead;
-//   * activations: each wave loads 16 tokens, 2 steps ahead in registers, into
-//     a double-buffered LDS tile (XOR-swizzled 16-byte slots, conflict-free);
-//   * wave w: rows 32w..32w+31 x all 64 tokens (2 x 4 accumulator tiles).
+//   * 8 waves: wave (wr, wk) holds rows 32wr..32wr+31 x all 64 tokens (2 x 4
+//     accumulator tiles) over chunks 2wk, 2wk+1 (64 columns each) of a step;
+//   * weights: each wave decodes its own rows and chunks straight into A
+//     fragments in registers (no LDS): lane (r, g) loads 8 code bytes of row
+//     r, whose two dwords are its fragments of the two chunks (the chunks' k
+//     order is taken alike on the B side); codes 2 steps ahead;
+//   * activations: each wave loads half the step of 16 tokens, 2 steps ahead
+//     in registers, into a double-buffered LDS tile (XOR-swizzled 16-byte
+//     slots, conflict-free).
 constexpr int TGM = 128, TGN = 64, TGK = 256;
 
 // LDS byte offset of 16-byte slot q (0..15) of token row n in a step tile
@@ -1197,53 +1199,57 @@ __device__ __forceinline__ uint4 group_t4x4(const uint4& v) {
 // y[n][m] = ((float)sum * w_scale) * inv[n], each product rounded on its
 // own: the reference's i2s_gemv epilogue (src/kernel_i2s.cpp:32-40) for
 // every token row, bit for bit (the sums are exact integers below 2^24).
+// 8 waves, two per SIMD (one SIMD's pair interleaves its decode, LDS reads and MFMAs: 41.2 -> 39.7 us against
+// 4 waves of all four chunks at 4096 x 512 x 11008): wave (wr, wk) holds rows 32 wr .. 32 wr + 31 x all 64
+// tokens for chunks 2 wk, 2 wk + 1 of every step; the two K halves' sums meet through LDS at the end.
+constexpr int TGT = 512;
 template <bool ROWS = false>
-__global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int8_t* a, float* __restrict__ out, int M,
+__global__ __launch_bounds__(TGT) void i2s_gemm_mfma(const uint8_t* w, const int8_t* a, float* __restrict__ out, int M,
                                                      int N, int K, float w_scale = 0.0f,
                                                      const float* __restrict__ inv = nullptr) {
     __shared__ __align__(16) uint8_t bt[2][TGN * TGK];
-    __shared__ int asum[TGN];
+    __shared__ int asum[2][TGN];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, wk = wave >> 2;
     const int r16 = lane & 15, g = lane >> 4;
     const int tn = (N + TGN - 1) / TGN;
     const int m0 = (blockIdx.x / tn) * TGM, n0 = (blockIdx.x % tn) * TGN;
     const int bpr = K / 4, steps = K / TGK;
 
-    // ---- codes: lane (r16, g), row tile i: row m0 + 32 wave + 16 i + r16, code bytes 16 g .. 16 g + 15 of the
-    // step, i.e. code dwords 4g + c (c = 0..3), each 16 columns; the planes of dword 4g + c are the lane's A
-    // fragment of chunk c, so chunk c's B fragment of lane (n, g) is the 16-column group 4g + c of token n
-    // (addresses: a uniform base per step plus a loop-invariant 32-bit lane offset, so that no load's
-    // destination registers share a dying address pair)
+    // ---- codes: lane (r16, g), row tile i: row m0 + 32 wr + 16 i + r16, code dwords 4g + 2wk and 4g + 2wk + 1
+    // of the step (16 columns each): the planes of dword 4g + c are the lane's A fragment of chunk c, so chunk
+    // c's B fragment of lane (n, g) is the 16-column group 4g + c of token n (addresses: a uniform base per step
+    // plus a loop-invariant 32-bit lane offset, so that no load's destination registers share a dying address)
     uint32_t woff[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) woff[i] = (uint32_t)min(m0 + 32 * wave + 16 * i + r16, M - 1) * (uint32_t)bpr + 16 * g;
+    for (int i = 0; i < 2; ++i)
+        woff[i] = (uint32_t)min(m0 + 32 * wr + 16 * i + r16, M - 1) * (uint32_t)bpr + 16 * g + 8 * wk;
     constexpr int LEAD = 2;  // steps between a load's issue and its use (codes) / its LDS store (activations)
-    uint4 cw[LEAD + 1][2];
-    // ---- activations: wave w loads token n0 + 16 w + r16, bytes 64 c + 16 g (group 4c + g) of the step
-    const uint32_t boff = (uint32_t)min(n0 + 16 * wave + r16, N - 1) * (uint32_t)K + 16 * g;
-    uint4 bw[LEAD + 1][4];
+    uint2 cw[LEAD + 1][2];
+    // ---- activations: wave (wr, wk) loads token n0 + 16 wr + r16, bytes 64 c + 16 g (group 4c + g) of the
+    // step for c = 2 wk, 2 wk + 1
+    const uint32_t boff = (uint32_t)min(n0 + 16 * wr + r16, N - 1) * (uint32_t)K + 16 * g + 128 * wk;
+    uint4 bw[LEAD + 1][2];
     int tsum = 0;  // sum of the bytes this lane loads of its token
-
-    auto load_codes = [&](int step, uint4 (&dst)[2]) {
+    auto load_codes = [&](int step, uint2 (&dst)[2]) {
         const uint8_t* base = w + (int64_t)min(step, steps - 1) * (TGK / 4);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) dst[i] = ld16(base + woff[i]);
+        for (int i = 0; i < 2; ++i) dst[i] = *(const uint2*)(base + woff[i]);
     };
-    auto load_acts = [&](int step, uint4 (&dst)[4]) {
+    auto load_acts = [&](int step, uint4 (&dst)[2]) {
         const int8_t* base = a + (int64_t)min(step, steps - 1) * TGK;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dst[c] = ld16(base + boff + 64 * c);
+        for (int cc = 0; cc < 2; ++cc) dst[cc] = ld16(base + boff + 64 * cc);
     };
     // B(step) into LDS in the codes' k order, its bytes into tsum (steps past the end add nothing)
-    auto store_acts = [&](const uint4 (&src)[4], uint8_t* tile, bool real) {
+    auto store_acts = [&](const uint4 (&src)[2], uint8_t* tile, bool real) {
         const uint32_t ones = real ? 0x01010101u : 0u;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            *(uint4*)(tile + tg_off(16 * wave + r16, 4 * c + g)) = group_t4x4(src[c]);
-            tsum = dot4(src[c].x, ones, dot4(src[c].y, ones, dot4(src[c].z, ones, dot4(src[c].w, ones, tsum))));
+        for (int cc = 0; cc < 2; ++cc) {
+            *(uint4*)(tile + tg_off(16 * wr + r16, 4 * (2 * wk + cc) + g)) = group_t4x4(src[cc]);
+            tsum = dot4(src[cc].x, ones, dot4(src[cc].y, ones, dot4(src[cc].z, ones, dot4(src[cc].w, ones, tsum))));
         }
     };
-
     i32x4 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -1261,11 +1267,10 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
     __builtin_amdgcn_sched_barrier(0);
     store_acts(bw[0], bt[0], true);
     __syncthreads();
-
     constexpr int U = LEAD + 1;  // unroll: every register slot index a constant
     // the step count rounded up to whole unrolled rounds (no exit inside a round: an exit per step made the
     // compiler rotate the accumulators' registers at the loop head, waiting there for every load in flight);
-    // the steps past the end take all-zero A fragments (the plane mask pm)
+    // the steps past the end take all-zero A fragments (the plane mask pm) and skip their products
     const int steps_u = (steps + U - 1) / U * U;
     for (int s0 = 0; s0 < steps_u; s0 += U) {
 #pragma unroll
@@ -1279,15 +1284,15 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
             load_codes(step + LEAD, cw[(u + LEAD) % U]);
             __builtin_amdgcn_sched_barrier(0);
             // A fragments of this step
-            i32x4 af[2][4];
+            i32x4 af[2][2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const uint4 q = cw[u][i];
-                const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+                const uint2 q = cw[u][i];
+                const uint32_t d[2] = {q.x, q.y};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const uint32_t uc = ucode(d[c]);
-                    af[i][c] = i32x4{(int)(uc & pm), (int)((uc >> 2) & pm), (int)((uc >> 4) & pm), (int)((uc >> 6) & pm)};
+                for (int cc = 0; cc < 2; ++cc) {
+                    const uint32_t uc = ucode(d[cc]);
+                    af[i][cc] = i32x4{(int)(uc & pm), (int)((uc >> 2) & pm), (int)((uc >> 4) & pm), (int)((uc >> 6) & pm)};
                 }
             }
             // B(step + 1) into the other LDS tile (read by the previous step, before its barrier); the tiles
@@ -1296,41 +1301,57 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
             const uint8_t* cur = bt[step & 1];
             if (step < steps)  // (a padded step's products are zero: skip them)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int cc = 0; cc < 2; ++cc) {
                 i32x4 bf[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) bf[j] = *(const i32x4*)(cur + tg_off(16 * j + r16, 4 * g + c));
+                for (int j = 0; j < 4; ++j) bf[j] = *(const i32x4*)(cur + tg_off(16 * j + r16, 4 * g + 2 * wk + cc));
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i][c], bf[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i][cc], bf[j], acc[i][j], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
         }
     }
-    // token sums: the four lane groups l, l ^ 16, l ^ 32, l ^ 48 of token 16 wave + r16, then through LDS
+    // token sums: the four lane groups l, l ^ 16, l ^ 32, l ^ 48 of token 16 wr + r16 (per K half), via LDS
     {
         uint32_t t = (uint32_t)tsum;
         const auto r32 = __builtin_amdgcn_permlane32_swap(t, t, false, false);
         t = lane_pin(r32[0]) + lane_pin(r32[1]);
         const auto r16s = __builtin_amdgcn_permlane16_swap(t, t, false, false);
         t = lane_pin(r16s[0]) + lane_pin(r16s[1]);
-        if (g == 0) asum[16 * wave + r16] = (int)t;
+        if (g == 0) asum[wk][16 * wr + r16] = (int)t;
+    }
+    // the K halves' accumulators: waves 4-7 through LDS to waves 0-3
+    int* red = (int*)&bt[0][0];
+    if (wk == 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(i32x4*)(red + ((wr * 8 + i * 4 + j) * 64 + lane) * 4) = acc[i][j];
     }
     __syncthreads();
-    // D: lane l holds rows 32 wave + 16 i + 4 (l/16) + r, token 16 j + l%16
+    if (wk == 1) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const i32x4 o = *(const i32x4*)(red + ((wr * 8 + i * 4 + j) * 64 + lane) * 4);
+            acc[i][j] += o;
+        }
+    // D: lane l holds rows 32 wr + 16 i + 4 (l/16) + r, token 16 j + l%16
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int n = n0 + 16 * j + r16;
         if (n >= N) continue;
-        const int as = asum[16 * j + r16];
+        const int as = asum[0][16 * j + r16] + asum[1][16 * j + r16];
         if constexpr (ROWS) {
             const float ts = inv[n];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int m = m0 + 32 * wave + 16 * i + 4 * g;
+                const int m = m0 + 32 * wr + 16 * i + 4 * g;
                 float v[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = fmul_rn(fmul_rn((float)(acc[i][j][r] - as), w_scale), ts);
@@ -1348,7 +1369,7 @@ __global__ __launch_bounds__(kWG) void i2s_gemm_mfma(const uint8_t* w, const int
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int m = m0 + 32 * wave + 16 * i + 4 * g + r;
+                    const int m = m0 + 32 * wr + 16 * i + 4 * g + r;
                     if (m < M) out[(int64_t)m * N + n] = (float)(acc[i][j][r] - as);
                 }
         }
@@ -1560,7 +1581,7 @@ hipError_t launch_i2s_gemm_vnni(const uint8_t* w, const int8_t* a, float* o, int
                                 hipStream_t s) {
     if (i2s_gemm_mfma_ok(M, N, K) && (((uintptr_t)w | (uintptr_t)a) & 15u) == 0) {
         const unsigned grid = (unsigned)(((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN));
-        i2s_gemm_mfma<<<grid, kWG, 0, s>>>(w, a, o, (int)M, (int)N, (int)K);
+        i2s_gemm_mfma<<<grid, TGT, 0, s>>>(w, a, o, (int)M, (int)N, (int)K);
         return hipGetLastError();
     }
     i2s_gemm_vnni_k<<<ceil_div(M * N, kWaves), kWG, 0, s>>>(w, a, o, M, N, K);
@@ -1571,7 +1592,7 @@ hipError_t launch_i2s_gemm_rows(const uint8_t* w, float w_scale, const int8_t* a
                                 int64_t N, int64_t K, hipStream_t s) {
     if (!i2s_gemm_mfma_ok(M, N, K) || (((uintptr_t)w | (uintptr_t)a) & 15u) != 0) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(((M + TGM - 1) / TGM) * ((N + TGN - 1) / TGN));
-    i2s_gemm_mfma<true><<<grid, kWG, 0, s>>>(w, a, y, (int)M, (int)N, (int)K, w_scale, inv);
+    i2s_gemm_mfma<true><<<grid, TGT, 0, s>>>(w, a, y, (int)M, (int)N, (int)K, w_scale, inv);
     return hipGetLastError();
 }
 
