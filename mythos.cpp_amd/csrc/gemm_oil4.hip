@@ -555,15 +555,20 @@ __global__ __launch_bounds__(ws_threads(CW)) void oil4_prefill_ws(const uint16_t
                 }
         } else {
             uint16_t* st = (uint16_t*)lds;
+            // the rows' shifts loaded together (each load behind the bf16 rounding's branches waited alone)
+            int shv[NG][4];
+#pragma unroll
+            for (int i = 0; i < NG; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) shv[i][r] = rsh[min(m0 + 16 * NG * wave + 16 * i + 4 * (lane >> 4) + r, M - 1)];
 #pragma unroll
             for (int i = 0; i < NG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int rr = 16 * NG * wave + 16 * i + 4 * (lane >> 4) + r;
-                    const int sh = rsh[min(m0 + rr, M - 1)];
 #pragma unroll
                     for (int j = 0; j < NT; ++j)
-                        st[rr * BN + 16 * j + (lane & 15)] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -sh));
+                        st[rr * BN + 16 * j + (lane & 15)] = f32_to_bf16_rne(ldexpf(acc[i][j][r], -shv[i][r]));
                 }
         }
     }
@@ -572,11 +577,17 @@ __global__ __launch_bounds__(ws_threads(CW)) void oil4_prefill_ws(const uint16_t
         // real row 128 mt + r: (hi sum + lo sum) * 2^-shift
         float* C = (float*)Cv;
         const float* st = (const float*)lds;
-        constexpr int CPR = BN / 4;
-        for (int c = tid; c < 128 * CPR; c += NTH) {
+        constexpr int CPR = BN / 4, IT = (128 * CPR + NTH - 1) / NTH;
+        int shv[IT];  // the rows' shifts loaded together
+#pragma unroll
+        for (int it = 0; it < IT; ++it) shv[it] = rsh[min(128 * mt + min((tid + it * NTH) / CPR, 127), Mr - 1)];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int c = tid + it * NTH;
+            if (c >= 128 * CPR) break;
             const int r = c / CPR, q = c % CPR, row = 128 * mt + r;
             if (row < Mr) {
-                const int sh = rsh[row];
+                const int sh = shv[it];
                 const float4 hi = *(const float4*)(st + r * BN + 4 * q), lo = *(const float4*)(st + (r + 128) * BN + 4 * q);
                 // oil4_hi_lo: an infinite hi sum (an infinite codebook entry) is the result, as the reference's
                 // single product w * x_k gives, not hi + lo, which is NaN where the lo part has the other sign
