@@ -605,12 +605,24 @@ __global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices v
             mx = fmaxf(mx, s);
         }
     }
-    for (int t0 = KPRE * KRR; t0 < nmem; t0 += KRR) {
-        const int t = t0 + kr;
-        const float s = score(*(const uint4*)(kchunk + (int64_t)(t < nmem ? t : 0) * D));
-        if (t < nmem) {
-            if (kl == 0) sc[t] = s;
-            mx = fmaxf(mx, s);
+    // rows past the preloaded rounds (contexts beyond KPRE * KRR rows): KB rounds' loads in flight together
+    // (one round trip per KB rounds, not per round)
+    constexpr int KB = 4;
+    for (int t0 = KPRE * KRR; t0 < nmem; t0 += KB * KRR) {
+        uint4 kb[KB];
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+            const int t = t0 + b * KRR + kr;
+            kb[b] = *(const uint4*)(kchunk + (int64_t)(t < nmem ? t : 0) * D);
+        }
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+            const int t = t0 + b * KRR + kr;
+            const float s = score(kb[b]);
+            if (t < nmem) {
+                if (kl == 0) sc[t] = s;
+                mx = fmaxf(mx, s);
+            }
         }
     }
     if (ROPE && tid == (pos % NT)) {  // the current position, from LDS
@@ -651,15 +663,21 @@ __global__ __launch_bounds__(NT) void attention_k(Slices q, Slices kin, Slices v
         const int t = sl + SL * j;
         if (t < nmem) axpy(acc[j & 3], sc[t] * inv, kv_widen(vpre[j]));
     }
-    int t = sl + SL * VP;
-    for (; t + 3 * SL < nmem; t += 4 * SL) {
-        float4 v4[4];
+    // rows past the preloaded ones: 8 rows' loads in flight together (rows past the context read row 0 and
+    // are not added)
+    for (int t = sl + SL * VP; t < nmem; t += 8 * SL) {
+        float4 v4[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v4[j] = kv_load4(vcol + (int64_t)(t + j * SL) * D);
+        for (int j = 0; j < 8; ++j) {
+            const int tj = t + j * SL;
+            v4[j] = kv_load4(vcol + (int64_t)(tj < nmem ? tj : 0) * D);
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) axpy(acc[j], sc[t + j * SL] * inv, v4[j]);
+        for (int j = 0; j < 8; ++j) {
+            const int tj = t + j * SL;
+            if (tj < nmem) axpy(acc[j & 3], sc[tj] * inv, v4[j]);
+        }
     }
-    for (; t < nmem; t += SL) axpy(acc[0], sc[t] * inv, kv_load4(vcol + (int64_t)t * D));
     if (ROPE && sl == (pos % SL)) axpy(acc[1], sc[pos] * inv, *(const float4*)(vs + 4 * g));
     acc[0].x += acc[1].x; acc[0].y += acc[1].y; acc[0].z += acc[1].z; acc[0].w += acc[1].w;
     acc[2].x += acc[3].x; acc[2].y += acc[3].y; acc[2].z += acc[3].z; acc[2].w += acc[3].w;

@@ -237,8 +237,10 @@ def test_rope_kv_bit_exact(D, oracle, mth, dev):
     assert not host(kc)[:, :, :pos].any() and not host(kc)[:, :, pos + 1:].any()
 
 
+# contexts past the rows a thread preloads (the K rows of 192 positions, the V rows of 64 at D = 128) run the
+# batched tail loops: ragged ends at 700, 1500 and 333 positions
 @pytest.mark.parametrize("D,ctx,S", [(128, 1, 192), (128, 37, 192), (128, 192, 192), (64, 100, 128),
-                                     (256, 17, 32)])
+                                     (256, 17, 32), (128, 700, 1024), (64, 1500, 2048), (256, 333, 512)])
 def test_attention(D, ctx, S, oracle, mth, dev):
     import torch
     print(f"attention D={D} ctx={ctx} S={S}", flush=True)
