@@ -1201,6 +1201,20 @@ static hipError_t run_attention(const Slices& q, const Slices& k, const Slices& 
     // few workgroups (a decode step of a handful of sequences): 8 waves each (16 measured 0.9 % slower for a
     // batch-1 decode step once the V rows were issued after the staging, 4 waves 1.3 % slower)
     const bool wide = ROPE && np == 1 && rows * heads <= 128;
+    // long contexts (more than 1024 positions) of a few rows x heads: 16 waves, twice the cache loads in flight
+    const bool wider = np == 1 && rows * heads <= 128 && max_seq > 1024;
+    if (wider) {
+        if (head_dim == 64)
+            attention_k<64, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+                                                                      ctx0, np, heads, kv_heads, max_seq, scale);
+        else if (head_dim == 128)
+            attention_k<128, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+                                                                       ctx0, np, heads, kv_heads, max_seq, scale);
+        else
+            attention_k<256, ROPE, KV, 1024><<<grid, 1024, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,
+                                                                       ctx0, np, heads, kv_heads, max_seq, scale);
+        return hipGetLastError();
+    }
     if (head_dim == 64) {
         if (wide)
             attention_k<64, ROPE, KV, 512><<<grid, 512, lds, s>>>(q, k, v, ns, cos_t, sin_t, kc, vc, out, step,

@@ -200,6 +200,17 @@ def prefill_vs_oracle(cfg, model, B, P, kv, oracle, seed, extra_steps=2, ltol=TO
     return want
 
 
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_long_context_decode(kv, oracle):
+    """max_seq 1100 (more than 1024 positions: the decode attention on 16
+    waves) after a 1050-token prompt: the two decode steps attend to 1050+
+    cache rows, past the rows a thread preloads (the batched tail loads of
+    K and V), against the oracle."""
+    cfg = synth.decoder_config(**dict(SMALL, max_seq=1100))
+    model = synth.decoder_model(cfg, config=60, random_gamma=True)
+    prefill_vs_oracle(cfg, model, 1, 1050, kv, oracle, seed=97, ltol=TOL if kv == "f32" else 1e-3)
+
+
 @pytest.mark.parametrize("B,kv", [(1, "f32"), (3, "bf16")])
 def test_prefill_matches_oracle(B, kv, small, oracle):
     cfg, model = small

@@ -238,9 +238,10 @@ def test_rope_kv_bit_exact(D, oracle, mth, dev):
 
 
 # contexts past the rows a thread preloads (the K rows of 192 positions, the V rows of 64 at D = 128) run the
-# batched tail loops: ragged ends at 700, 1500 and 333 positions
+# batched tail loops: ragged ends at 700, 1500, 333, 1999 and 1200 positions; max_seq > 1024 takes 16 waves
 @pytest.mark.parametrize("D,ctx,S", [(128, 1, 192), (128, 37, 192), (128, 192, 192), (64, 100, 128),
-                                     (256, 17, 32), (128, 700, 1024), (64, 1500, 2048), (256, 333, 512)])
+                                     (256, 17, 32), (128, 700, 1024), (64, 1500, 2048), (256, 333, 512),
+                                     (128, 1999, 2048), (256, 1200, 1500)])
 def test_attention(D, ctx, S, oracle, mth, dev):
     import torch
     print(f"attention D={D} ctx={ctx} S={S}", flush=True)
