@@ -483,12 +483,16 @@ __global__ __launch_bounds__(NW * 64, PAIR && NW >= 4 ? 5 : 1) void oil4_gemv_v2
         const int c0 = 8 * (XS * lane + h);
         const int p = c0 >> 8, qq = (c0 & 255) >> 6, m = (c0 & 63) >> 3;
         half8 vh, vl;
+        // two columns per conversion (v_cvt_pk_f16_f32, round to nearest even as the scalar conversion)
+        typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+        typedef float f2v __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float xs = ldexpf(xv[8 * h + oil4_elem_col(t)], sh);
-            const _Float16 hh = (_Float16)xs;
-            vh[t] = hh;
-            vl[t] = (_Float16)(xs - (float)hh);
+        for (int t = 0; t < 8; t += 2) {
+            const f2v xs = {ldexpf(xv[8 * h + oil4_elem_col(t)], sh), ldexpf(xv[8 * h + oil4_elem_col(t + 1)], sh)};
+            const h2v hh = __builtin_convertvector(xs, h2v);
+            const h2v ll = __builtin_convertvector(f2v{xs[0] - (float)hh[0], xs[1] - (float)hh[1]}, h2v);
+            vh[t] = hh[0], vh[t + 1] = hh[1];
+            vl[t] = ll[0], vl[t + 1] = ll[1];
         }
         const int slot = ((p * 8 + m) * 4 + qq) * 8;
         *(half8*)&xw[slot] = vh;

@@ -138,6 +138,14 @@ __device__ __forceinline__ uint32_t dpp_row(uint32_t v) {
     return r;
 }
 __device__ __forceinline__ uint32_t dpp_ror8(uint32_t v) { return dpp_row<0x128>(v); }
+// keep, with the lanes of the DPP banks in BANKS (4 lanes each within a 16-lane row) replaced by moved of the
+// lane 8 places along the row (row_ror:8): one v_mov_b32_dpp with a bank mask
+template <int BANKS>
+__device__ __forceinline__ uint32_t dpp_mix(uint32_t keep, uint32_t moved) {
+    uint32_t r = (uint32_t)__builtin_amdgcn_update_dpp((int)keep, (int)moved, 0x128, 0xf, BANKS, false);
+    asm volatile("" : "+v"(r));
+    return r;
+}
 
 // Max over the 16 lanes of each DPP row (every lane gets the row's max).
 __device__ __forceinline__ float row16_max(float v) {
@@ -241,13 +249,12 @@ struct Oil4TileLoads {
 
     // Rows 0-7 / 8-15 -> lane (j, q): a = piece 2q, b = piece 2q+1 of row j.
     __device__ __forceinline__ void exchange(int p, int lane, uint4& a, uint4& b) const {
-        const bool keep = (lane & 15) < 8;
-        const uint32_t ry0 = dpp_ror8(wy[p].x), ry1 = dpp_ror8(wy[p].y), ry2 = dpp_ror8(wy[p].z),
-                       ry3 = dpp_ror8(wy[p].w);
-        const uint32_t rx0 = dpp_ror8(wx[p].x), rx1 = dpp_ror8(wx[p].y), rx2 = dpp_ror8(wx[p].z),
-                       rx3 = dpp_ror8(wx[p].w);
-        a = make_uint4(keep ? wx[p].x : ry0, keep ? wx[p].y : ry1, keep ? wx[p].z : ry2, keep ? wx[p].w : ry3);
-        b = make_uint4(keep ? rx0 : wy[p].x, keep ? rx1 : wy[p].y, keep ? rx2 : wy[p].z, keep ? rx3 : wy[p].w);
+        // a: wx in lanes 0-7 of each 16-lane row, wy of lanes 0-7 (row_ror:8) in lanes 8-15 (DPP writes of banks
+        // 2-3 only); b: wx of lanes 8-15 in lanes 0-7 (banks 0-1), wy in lanes 8-15
+        a = make_uint4(dpp_mix<0xc>(wx[p].x, wy[p].x), dpp_mix<0xc>(wx[p].y, wy[p].y),
+                       dpp_mix<0xc>(wx[p].z, wy[p].z), dpp_mix<0xc>(wx[p].w, wy[p].w));
+        b = make_uint4(dpp_mix<0x3>(wy[p].x, wx[p].x), dpp_mix<0x3>(wy[p].y, wx[p].y),
+                       dpp_mix<0x3>(wy[p].z, wx[p].z), dpp_mix<0x3>(wy[p].w, wx[p].w));
     }
 };
 
