@@ -35,9 +35,11 @@ __device__ __forceinline__ uint32_t lane_pin(uint32_t r) {
     asm volatile("" : "+v"(r));
     return r;
 }
+// (v_mov_b32_dpp without an "old" operand: every pattern used here gives each
+// lane a source lane inside its row, so there is nothing to initialise)
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-    return lane_pin((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false));
+    return lane_pin((uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true));
 }
 template <typename T>
 __device__ __forceinline__ uint32_t lane_bits(T v) { return __builtin_bit_cast(uint32_t, v); }
