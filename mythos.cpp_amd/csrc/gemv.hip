@@ -780,8 +780,8 @@ void run_oil4_mfma(const uint8_t* nib, const uint16_t* cbs, int64_t cb_block, co
 bool oil4_swiglu_supported(const uint8_t* nib, const uint16_t* cbs, const float* x, int64_t F, int64_t K) {
     // the K range where launch_oil4_gemv runs oil4_gemv_v2 with MTH_OIL4_V2_NPH phases
     constexpr int KP = 256 * MTH_OIL4_V2_NPH;
-    return F > 0 && F % 8 == 0 && 2 * F < (1ll << 31) && K % KP == 0 && K >= 512 && K <= 4096 &&
-           aligned16(nib) && aligned16(cbs) && aligned16(x);
+    return F > 0 && F % 8 == 0 && 2 * F < (1ll << 31) && 2 * F * (K / 2) < (1ll << 32) && K % KP == 0 && K >= 512 &&
+           K <= 4096 && aligned16(nib) && aligned16(cbs) && aligned16(x);
 }
 
 hipError_t launch_oil4_swiglu(const uint8_t* nib, const uint16_t* cbs, const float* x, const NormScale& ns,
@@ -855,7 +855,9 @@ hipError_t launch_oil4_gemv(const uint8_t* nib, const uint16_t* cbs, int64_t cb_
                             const float* x, float* y, int64_t M, int64_t K, int64_t batch,
                             hipStream_t s) {
     const bool aligned = aligned16(nib) && aligned16(x) && aligned16(cbs);
-    if (batch == 1 && aligned && M < (1ll << 31) && (cb_block == 0 || cb_block == 128) && K >= 512 && K <= 4096) {
+    // (oil4_gemv_v2's tile loads use 32-bit byte offsets: M * K / 2 < 2^32)
+    if (batch == 1 && aligned && M * (K / 2) < (1ll << 32) && (cb_block == 0 || cb_block == 128) && K >= 512 &&
+        K <= 4096) {
         constexpr int NPH = MTH_OIL4_V2_NPH;
         bool done = cb_block == 0 ? run_oil4_v2<NPH, true>(nib, cbs, x, y, M, K, s)
                                   : run_oil4_v2<NPH, false>(nib, cbs, x, y, M, K, s);

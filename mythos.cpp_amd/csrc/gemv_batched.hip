@@ -851,8 +851,9 @@ hipError_t launch_oil4_gemv_bt_swiglu(const uint8_t* nib, const uint16_t* cbs, i
 
 bool oil4_bt_supported(int64_t M, int64_t K, int64_t cb_block, int64_t batch) {
     // K <= 8192 keeps the slice count <= 16 (the reduction kernel's limit)
+    // (M * K / 2 < 2^32: the tile loads use 32-bit byte offsets into the nibbles)
     return batch >= 2 && (cb_block == 0 || cb_block == 128) && K >= 512 && K <= 8192 && K % 512 == 0 &&
-           M < (1ll << 31) && M * K < (1ll << 40);
+           M < (1ll << 31) && M * (K / 2) < (1ll << 32);
 }
 
 size_t oil4_bt_partial_bytes(int64_t M, int64_t K) {

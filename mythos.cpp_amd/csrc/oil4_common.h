@@ -205,21 +205,25 @@ struct Oil4TileLoads {
     __device__ __forceinline__ void issue_phases(const uint8_t* nib, const uint16_t* cbs, int rowA, int rowB, int M,
                                                  int K, int k0, int lane) {
         const int j = lane & 15, q = lane >> 4, jj8 = j & 7, hi8 = j >> 3;
-        const int nbr = K >> 7;  // codebook blocks per row
-        const uint8_t* nx = nib + (int64_t)min(rowA + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
-        const uint8_t* ny = nib + (int64_t)min(rowB + jj8, M - 1) * (K >> 1) + (k0 >> 1) + 16 * (2 * q + hi8);
+        const uint32_t nbr = (uint32_t)K >> 7;  // codebook blocks per row
+        // 32-bit byte offsets from the uniform bases (the callers keep M * K / 2 below 2^32), so the loads take a
+        // scalar base and a lane offset instead of 64-bit address arithmetic per lane
+        const uint32_t hb = (uint32_t)K >> 1, col = (uint32_t)(k0 >> 1) + 16 * (2 * q + hi8);
+        const uint32_t ox = (uint32_t)min(rowA + jj8, M - 1) * hb + col, oy = (uint32_t)min(rowB + jj8, M - 1) * hb + col;
         // codebook loads: lane l -> row 8u + l/8, 16-byte piece l % 8 of the
         // 4 blocks of a phase pair
-        const uint16_t* cl0 = cbs + ((int64_t)min(rowA + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
-        const uint16_t* cl1 = cbs + ((int64_t)min(rowB + (lane >> 3), M - 1) * nbr + (k0 >> 7)) * 16 + 8 * (lane & 7);
+        const uint32_t cpiece = ((uint32_t)(k0 >> 7) * 16 + 8 * (lane & 7)) * 2;
+        const uint32_t oc0 = (uint32_t)min(rowA + (lane >> 3), M - 1) * nbr * 32 + cpiece;
+        const uint32_t oc1 = (uint32_t)min(rowB + (lane >> 3), M - 1) * nbr * 32 + cpiece;
+        const uint8_t* cb8 = (const uint8_t*)cbs;
 #pragma unroll
         for (int p = P0; p < P1; ++p) {
             if (!SHARED && p % 2 == 0) {
-                c0[p / 2] = ld16(cl0 + (p / 2) * 64);
-                c1[p / 2] = ld16(cl1 + (p / 2) * 64);
+                c0[p / 2] = ld16(cb8 + oc0 + (p / 2) * 128);
+                c1[p / 2] = ld16(cb8 + oc1 + (p / 2) * 128);
             }
-            wx[p] = ld_stream(nx + 128 * p);
-            wy[p] = ld_stream(ny + 128 * p);
+            wx[p] = ld_stream(nib + ox + 128 * p);
+            wy[p] = ld_stream(nib + oy + 128 * p);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
