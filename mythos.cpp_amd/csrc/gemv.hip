@@ -99,8 +99,9 @@ void oil8_gemv_k(Oil8SegArgs sg, const float* x, int K, int batch, ResidOut ro) 
     const float rx0 = rxp[ro.x ? rrow : 0], rg0 = rgp[ro.x ? rrow : 0];
     __builtin_amdgcn_sched_barrier(0);
     uint4 w[R];
+    // (32-bit byte offsets from the segment's base: the launchers keep rows * K below 2^32)
 #pragma unroll
-    for (int r = 0; r < R; ++r) w[r] = ld_stream(idx + (int64_t)min(m0 + r, M - 1) * K + kl);
+    for (int r = 0; r < R; ++r) w[r] = ld_stream(idx + ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)kl));
     __builtin_amdgcn_sched_barrier(0);
     tab[tid] = cbv;
     __syncthreads();
@@ -806,7 +807,7 @@ hipError_t launch_oil4_swiglu(const uint8_t* nib, const uint16_t* cbs, const flo
 
 hipError_t launch_oil8_gemv(const uint8_t* idx, const float* cb, const float* x, float* y,
                             int64_t M, int64_t K, int64_t batch, hipStream_t s) {
-    const bool fast = (K % 16 == 0) && K <= 4096 && M < (1ll << 31) && aligned16(idx) && aligned16(x);
+    const bool fast = (K % 16 == 0) && K <= 4096 && M * K < (1ll << 32) && aligned16(idx) && aligned16(x);
     if (fast) {
         const Oil8Seg seg{idx, cb, y, M};
         return launch_oil8_gemv_segs(&seg, 1, x, K, batch, s);
@@ -820,7 +821,7 @@ bool oil8_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K) {
     if (nseg < 1 || nseg > kOil8MaxSegs || K % 16 != 0 || K > 4096) return false;
     int64_t total = 0;
     for (int i = 0; i < nseg; ++i) {
-        if (seg[i].rows < 1 || !aligned16(seg[i].idx)) return false;
+        if (seg[i].rows < 1 || seg[i].rows * K >= (1ll << 32) || !aligned16(seg[i].idx)) return false;
         total += seg[i].rows;
     }
     return total < (1ll << 31);
@@ -828,6 +829,8 @@ bool oil8_segs_fusable(const Oil8Seg* seg, int nseg, int64_t K) {
 
 hipError_t launch_oil8_gemv_segs(const Oil8Seg* seg, int nseg, const float* x, int64_t K, int64_t batch,
                                  hipStream_t s) {
+    for (int i = 0; i < nseg; ++i)  // the kernel's byte offsets into a segment's indices are 32-bit
+        if (seg[i].rows * K >= (1ll << 32)) return hipErrorInvalidValue;
     constexpr int R = 4;
     const Oil8SegArgs a = make_seg_args(seg, nseg, R);
     oil8_gemv_k<R><<<seg_groups(seg, nseg, R), kWG, 0, s>>>(a, x, (int)K, (int)batch, ResidOut{});
@@ -836,6 +839,7 @@ hipError_t launch_oil8_gemv_segs(const Oil8Seg* seg, int nseg, const float* x, i
 
 hipError_t launch_oil8_gemv_resid(const Oil8Seg& seg, const float* x, int64_t K, const ResidOut& ro, int* nparts,
                                   hipStream_t s) {
+    if (seg.rows * K >= (1ll << 32)) return hipErrorInvalidValue;  // 32-bit byte offsets into the indices
     constexpr int R = 4;
     const Oil8SegArgs a = make_seg_args(&seg, 1, R);
     *nparts = seg_groups(&seg, 1, R);
